@@ -1,0 +1,115 @@
+/*
+ * gdn_mi355x.h -- C ABI of the MI355X (gfx950) fused chunked Gated DeltaNet
+ * forward.
+ *
+ * Replaces the reference's GPU boundary for this path:
+ *   - the Python launcher  gdn_chunk_fwd(q, k, v, beta, g) -> (o, h_final)
+ *     (gdn_triton.py:113-140), and
+ *   - the raw kernel launch _gdn_fwd_kernel.fn[grid](Q, K, V, Beta, G, O, Hf,
+ *     <b,t,h strides of every tensor>, T, H, DK, DV, C, BV)
+ *     (gdn_triton.py:29-41; bench_gdn.py:43-59).
+ * The struct below carries exactly what that launch takes (device pointers,
+ * per-tensor (b, t, h) strides, T/H/K/V, chunk size C and V-slice BV) plus
+ * what the north-star surface adds (h0, scale, dtypes).
+ *
+ * Semantics (per batch b and head h; the state S is K x V, S = h^T of the
+ * reference's V x K state, gdn_ref.py:3-9):
+ *     S_t = e^{g_t} S_{t-1} + k_t u_t^T,
+ *     u_t = beta_t (v_t - e^{g_t} S_{t-1}^T k_t),
+ *     o_t = scale * S_t^T q_t.
+ *
+ * Contract:
+ *   - All pointers are device pointers on the current HIP device.  The call
+ *     only enqueues work on `stream`; it never allocates, never synchronises
+ *     and keeps no state between calls (re-entrant).
+ *   - Inputs are read-only.  `o` and `final_state` are written in full.
+ *   - q, k, v: innermost (K / V) dimension contiguous; base pointer and the
+ *     b/t/h strides (in elements) must give 16-byte aligned rows.
+ *   - g, beta: any strides.  h0 / final_state: any strides (b, h, k, v).
+ *   - h0 may be NULL (zero initial state).
+ *   - T may be any value >= 0; a trailing partial chunk is masked in-kernel
+ *     (equivalent to the reference's zero padding, gdn_ref.py:102-114).
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_MI355X_ABI_VERSION 1
+
+/* Element types of the tensors crossing the boundary. */
+enum GdnDtype {
+  GDN_DTYPE_F32 = 0,
+  GDN_DTYPE_F16 = 1,
+  GDN_DTYPE_BF16 = 2
+};
+
+/* Status codes.  0 is success; values below 1000 are hipError_t values
+ * passed through from the HIP runtime; values from 1000 are argument
+ * errors detected before launch (nothing is enqueued). */
+enum GdnStatus {
+  GDN_OK = 0,
+  GDN_ERR_NULL_POINTER = 1001,
+  GDN_ERR_BAD_SHAPE = 1002,
+  GDN_ERR_UNSUPPORTED = 1003,
+  GDN_ERR_MISALIGNED = 1004,
+  GDN_ERR_BAD_DTYPE = 1005
+};
+
+typedef struct GdnFwdParams {
+  /* inputs: q, k [B,T,H,K]; v [B,T,H,V]; g, beta [B,T,H]; h0 [B,H,K,V] */
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;          /* nullable */
+  /* outputs: o [B,T,H,V]; final_state [B,H,K,V] fp32 */
+  void* o;
+  float* final_state;
+  /* strides in elements: (b, t, h) for the [B,T,H,*] tensors */
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t g_stride[3];
+  int64_t beta_stride[3];
+  int64_t o_stride[3];
+  /* strides in elements: (b, h, k, v) for the state tensors */
+  int64_t h0_stride[4];
+  int64_t fs_stride[4];
+  int32_t B, T, H, K, V;
+  float scale;              /* o = scale * S^T q (FLA convention) */
+  int32_t chunk_size;       /* C: 32 or 64 */
+  int32_t block_v;          /* BV: 16, 32 or 64 dividing V; 0 = auto */
+  int32_t qkv_dtype;        /* GdnDtype of q, k, v */
+  int32_t g_dtype;          /* GdnDtype of g */
+  int32_t beta_dtype;       /* GdnDtype of beta */
+  int32_t o_dtype;          /* GdnDtype of o */
+} GdnFwdParams;
+
+/* Enqueue one fused chunked GDN forward on `stream` (a hipStream_t; NULL =
+ * the legacy default stream).  Returns a GdnStatus / hipError_t value.
+ * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140). */
+int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
+
+/* The block_v the launcher picks when params->block_v == 0 (for logging and
+ * tests); -1 if the shape is unsupported.  No counterpart in the reference,
+ * whose autotuner picks BV at run time (gdn_triton.py:18-28). */
+int gdn_fwd_auto_block_v(int B, int H, int K, int V, int chunk_size,
+                         int qkv_dtype);
+
+/* Human-readable text for a status code. */
+const char* gdn_fwd_status_string(int status);
+
+/* GDN_MI355X_ABI_VERSION of the built library. */
+int gdn_fwd_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_MI355X_H */

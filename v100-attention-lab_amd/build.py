@@ -1,0 +1,92 @@
+"""Build the gfx950 C-ABI library ``lib/libgdn_mi355x.so`` with hipcc.
+
+Usage: ``python v100-attention-lab_amd/build.py`` (or ``build()`` from
+Python).  The library is built in-tree so that it travels with the source
+tree; nothing is installed.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import time
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+# One translation unit per q/k/v dtype plus the host API, compiled in parallel.
+SOURCES = ["gdn_fwd_api.hip", "gdn_fwd_f16.hip", "gdn_fwd_bf16.hip", "gdn_fwd_f32.hip"]
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
+INCLUDE = os.path.join(REPO_DIR, "include")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_NAME = "libgdn_mi355x.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # No packed-fp32 VALU (v_pk_*_f32) anywhere in device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(exe):
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build")
+    return exe
+
+
+def _filtered(stderr: str) -> str:
+    # hipcc's host pass does not know the packed-fp32 feature and says so;
+    # that note is expected and filtered.
+    noise = "is not a recognized feature for this target"
+    return "\n".join(l for l in stderr.splitlines() if noise not in l)
+
+
+def build(verbose: bool = True, extra_flags=None) -> str:
+    """Compile the HIP sources into ``lib/libgdn_mi355x.so``; returns its path."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    t0 = time.time()
+    procs = []
+    objs = []
+    for src in SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", "-c",
+               os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print("[build]", " ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                            text=True)))
+        objs.append(obj)
+    failed = []
+    for src, pr in procs:
+        out, err = pr.communicate()
+        err = _filtered(err)
+        if pr.returncode != 0:
+            failed.append(f"{src} ({pr.returncode}):\n{err}")
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
+    tmp = LIB_PATH + ".tmp"
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    res = subprocess.run(link, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed ({res.returncode}):\n{_filtered(res.stderr)}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"[build] {LIB_PATH} ({time.time() - t0:.1f} s)", flush=True)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,103 @@
+// Host side of the C ABI declared in include/gdn_mi355x.h: argument checks,
+// BV choice and dispatch to the per-dtype launchers.
+
+#include "gdn_fwd_kernel.h"
+
+namespace gdn {
+
+// BV choice: the largest slice that still gives at least one workgroup per
+// CU (256 CUs); below that, the smallest supported slice.
+int auto_block_v(int B, int H, int K, int V, int C, int dtype) {
+  const long long bh = (long long)B * H;
+  int best = -1;
+  for (int bv : {64, 32, 16}) {
+    if (V % bv != 0 || !supported(dtype, K, C, bv)) continue;
+    if (best < 0) best = bv;
+    if (bh * (V / bv) >= 256) return bv;
+    best = bv;
+  }
+  return best;
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" {
+
+int gdn_fwd_abi_version(void) { return GDN_MI355X_ABI_VERSION; }
+
+int gdn_fwd_auto_block_v(int B, int H, int K, int V, int chunk_size, int qkv_dtype) {
+  if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || V % 16 != 0) return -1;
+  return auto_block_v(B, H, K, V, chunk_size, qkv_dtype);
+}
+
+const char* gdn_fwd_status_string(int status) {
+  switch (status) {
+    case GDN_OK: return "success";
+    case GDN_ERR_NULL_POINTER: return "gdn_fwd: a required pointer is NULL";
+    case GDN_ERR_BAD_SHAPE: return "gdn_fwd: invalid shape (B, H, K, V must be > 0, T >= 0, V % 16 == 0)";
+    case GDN_ERR_UNSUPPORTED:
+      return "gdn_fwd: unsupported configuration (K in {32,64,128,256}, chunk_size in {32,64}, "
+             "block_v in {16,32,64} dividing V, within the 160 KB LDS budget)";
+    case GDN_ERR_MISALIGNED:
+      return "gdn_fwd: q/k/v rows must be 16-byte aligned with a contiguous last dimension";
+    case GDN_ERR_BAD_DTYPE: return "gdn_fwd: unknown dtype code";
+    default: return hipGetErrorString((hipError_t)status);
+  }
+}
+
+int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
+  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
+  const GdnFwdParams& P = *prm;
+  if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0)
+    return GDN_ERR_BAD_SHAPE;
+  if (!valid_dtype(P.qkv_dtype) || !valid_dtype(P.g_dtype) || !valid_dtype(P.beta_dtype) ||
+      !valid_dtype(P.o_dtype))
+    return GDN_ERR_BAD_DTYPE;
+  if (P.final_state == nullptr) return GDN_ERR_NULL_POINTER;
+  if (P.T > 0 && (P.q == nullptr || P.k == nullptr || P.v == nullptr || P.g == nullptr ||
+                  P.beta == nullptr || P.o == nullptr))
+    return GDN_ERR_NULL_POINTER;
+  int bv = P.block_v;
+  if (bv == 0) bv = auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
+  if (bv <= 0 || P.V % bv != 0 || !supported(P.qkv_dtype, P.K, P.chunk_size, bv))
+    return GDN_ERR_UNSUPPORTED;
+  // 16-byte rows for the vector loads of q, k, v.
+  const int eb = elem_bytes(P.qkv_dtype);
+  const void* ptrs[3] = {P.q, P.k, P.v};
+  const int64_t* strides[3] = {P.q_stride, P.k_stride, P.v_stride};
+  if (P.T > 0) {
+    for (int i = 0; i < 3; ++i) {
+      if (reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) return GDN_ERR_MISALIGNED;
+      for (int d = 0; d < 3; ++d)
+        if ((strides[i][d] * eb) % 16 != 0) return GDN_ERR_MISALIGNED;
+    }
+  }
+  const long long units = (long long)P.B * P.H * (P.V / bv);
+  if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
+
+  KArgs a;
+  a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
+  a.o = P.o; a.fs = P.final_state;
+  for (int d = 0; d < 3; ++d) {
+    a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
+    a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.so[d] = P.o_stride[d];
+  }
+  for (int d = 0; d < 4; ++d) { a.sh0[d] = P.h0_stride[d]; a.sfs[d] = P.fs_stride[d]; }
+  a.B = P.B; a.T = P.T; a.H = P.H; a.V = P.V; a.nv = P.V / bv;
+  a.scale = P.scale;
+  a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.o_dtype = P.o_dtype;
+  a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+
+  const int grid = (int)units;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (P.qkv_dtype) {
+    case GDN_DTYPE_F16: return launch_f16(a, P.K, P.chunk_size, bv, grid, s);
+    case GDN_DTYPE_BF16: return launch_bf16(a, P.K, P.chunk_size, bv, grid, s);
+    case GDN_DTYPE_F32: return launch_f32(a, P.K, P.chunk_size, bv, grid, s);
+    default: return GDN_ERR_BAD_DTYPE;
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,11 @@
+// Kernel instantiations for bf16 q/k/v inputs.
+
+#include "gdn_fwd_kernel.h"
+
+namespace gdn {
+
+int launch_bf16(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s) {
+  return launch_k<bf16_t>(a, K, C, bv, grid, s);
+}
+
+}  // namespace gdn

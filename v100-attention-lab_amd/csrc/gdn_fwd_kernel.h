@@ -1,0 +1,641 @@
+// Fused chunked Gated DeltaNet forward for MI355X (gfx950 / CDNA4).
+//
+// One workgroup (4 waves of 64) owns one (batch b, head h, V-slice of BV
+// columns) and scans the chunks of the sequence in order, keeping its
+// K x BV slice of the fp32 state S = h^T resident in the MFMA accumulator
+// registers of its "scan" waves for the whole sequence.  Nothing but the
+// final state leaves the chip, so memory stays O(B*H*K*V).
+//
+// Per chunk of C steps (b = cumsum(g) inside the chunk; the math is the
+// chunked UT form of the reference, gdn_ref.py:51-58, gdn_triton.py:54-106):
+//   P0  q, k [C,K], v [C,BV], g, beta [C] -> LDS (16-byte global loads;
+//       k is also stored transposed; bf16 inputs become fp16 operands).
+//   P1  b, e^{b}, e^{bC-b} (wave 0, in registers -> LDS).
+//   P2  MFMA: G = K K^T -> A[t,j] = beta_t e^{b_t-b_j} G[t,j]   (t > j)
+//             Q K^T     -> P[t,j] = e^{b_t-b_j} (q_t.k_j)       (t >= j)
+//       masks are applied before the exponential.
+//   P3  VALU forward substitution T = (I+A)^{-1}, one lane per column,
+//       rows of A broadcast from LDS; then Tw = -T diag(beta e^b) and
+//       Tu = T diag(beta) as MFMA operands.
+//   P4  MFMA: W'^T = K^T Tw^T  (W' = -W, W = (I+A)^{-1} diag(beta e^b) K).
+//   P5  scan waves (16 state columns each), MFMA:
+//         u   = Tu V + W' S                    (U - W h^T)
+//         o   = scale (P u + diag(e^b) Q S)
+//         S  <- e^{bC} S + K^T diag(e^{bC-b}) u
+//       The last line is the reference's update h(e^{bC}I - Wbar^T K) +
+//       Ubar^T K (gdn_ref.py:93-98) reassociated: Ubar - Wbar h^T =
+//       diag(e^{bC-b}) (U - W h^T), which avoids the K x K temporary.
+//
+// MFMA operand layout.  v_mfma_f32_16x16x32_{f16} takes, per lane l, row
+// (A) / column (B) l%16 and eight reduction slots owned by lane group
+// g = l/16.  The accumulator D holds column l%16 and rows 4g..4g+3.  Since
+// the reduction is a plain sum, any bijection between (g, slot) and the
+// reduction index works as long as A and B agree.  This file uses
+//     pi(g, s) = s < 4 ? 4g + s : 16 + 4g + (s - 4)     (within a 32-block)
+// because then the two accumulator tiles covering rows [32c, 32c+32) of a
+// product P are, lane for lane, exactly the B operand of P (reduction over
+// P's rows) and the A operand of P^T.  The state S (K x BV) therefore feeds
+// the next chunk's "x S" products straight from its accumulators, and u
+// feeds "P u" and "K^T u" straight from its accumulators: no LDS round trip
+// and no cross-lane shuffle on the serial path.  fp32 inputs use
+// v_mfma_f32_16x16x4_f32 eight times per 32-block (slot s = one MFMA).
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "gdn_mi355x.h"
+
+namespace gdn {
+
+typedef _Float16 f16;
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kLdsLimit = 160 * 1024;
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits) {
+  return __uint_as_float(bits << 16);
+}
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return (uint16_t)((u >> 16) | 0x0040u);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float load_scalar(const void* base, int64_t off,
+                                             int dtype) {
+  if (dtype == GDN_DTYPE_F32) return static_cast<const float*>(base)[off];
+  if (dtype == GDN_DTYPE_F16) return (float)static_cast<const f16*>(base)[off];
+  return bf16_bits_to_float(static_cast<const uint16_t*>(base)[off]);
+}
+
+__device__ __forceinline__ void store_scalar(void* base, int64_t off, int dtype,
+                                             float x) {
+  if (dtype == GDN_DTYPE_F32) {
+    static_cast<float*>(base)[off] = x;
+  } else if (dtype == GDN_DTYPE_F16) {
+    static_cast<f16*>(base)[off] = (f16)x;
+  } else {
+    static_cast<uint16_t*>(base)[off] = float_to_bf16_bits(x);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// input element type -> MFMA operand type, 16 bytes at a time
+// ---------------------------------------------------------------------------
+
+template <typename TIn>
+struct InTraits;
+
+template <>
+struct InTraits<f16> {
+  static constexpr int kVec = 8;  // elements per 16-byte load
+  __device__ static __forceinline__ void to_op(const uint4& r, f16* out) {
+    const f16* p = reinterpret_cast<const f16*>(&r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = p[e];
+  }
+};
+
+template <>
+struct InTraits<bf16_t> {
+  static constexpr int kVec = 8;
+  // bf16 -> fp16 is exact for |x| in fp16's normal range; smaller values
+  // keep fp16's subnormal precision (absolute 2^-24).
+  __device__ static __forceinline__ void to_op(const uint4& r, f16* out) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[2 * e] = (f16)bf16_bits_to_float(w[e] & 0xffffu);
+      out[2 * e + 1] = (f16)bf16_bits_to_float(w[e] >> 16);
+    }
+  }
+};
+
+template <>
+struct InTraits<float> {
+  static constexpr int kVec = 4;
+  __device__ static __forceinline__ void to_op(const uint4& r, float* out) {
+    out[0] = __uint_as_float(r.x);
+    out[1] = __uint_as_float(r.y);
+    out[2] = __uint_as_float(r.z);
+    out[3] = __uint_as_float(r.w);
+  }
+};
+
+template <typename TIn>
+struct OpOf {
+  using type = f16;
+};
+template <>
+struct OpOf<float> {
+  using type = float;
+};
+
+// ---------------------------------------------------------------------------
+// MFMA operand traits
+// ---------------------------------------------------------------------------
+
+template <typename TOp>
+struct Mma;
+
+template <>
+struct Mma<f16> {
+  using frag = f16x8;
+  __device__ static __forceinline__ f32x4 mma(const frag& a, const frag& b,
+                                              f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // Slots 0..7 <- blk[8g .. 8g+8)   (plain layout, used when both operands
+  // come from LDS rows).
+  __device__ static __forceinline__ frag load_contig(const f16* blk, int g) {
+    return *reinterpret_cast<const f16x8*>(blk + 8 * g);
+  }
+  // Slots 0..7 <- blk[pi(g, 0..7)].
+  __device__ static __forceinline__ frag load_pi(const f16* blk, int g) {
+    const f16x4 lo = *reinterpret_cast<const f16x4*>(blk + 4 * g);
+    const f16x4 hi = *reinterpret_cast<const f16x4*>(blk + 16 + 4 * g);
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  // Accumulator tiles (rows [0,16) and [16,32) of a 32-block) -> operand.
+  __device__ static __forceinline__ frag from_acc(const f32x4& lo,
+                                                  const f32x4& hi) {
+    return frag{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3],
+                (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
+  }
+  __device__ static __forceinline__ void store4(f16* dst, const f32x4& x) {
+    *reinterpret_cast<f16x4*>(dst) =
+        f16x4{(f16)x[0], (f16)x[1], (f16)x[2], (f16)x[3]};
+  }
+};
+
+template <>
+struct Mma<float> {
+  using frag = f32x8;
+  __device__ static __forceinline__ f32x4 mma(const frag& a, const frag& b,
+                                              f32x4 c) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+    }
+    return c;
+  }
+  __device__ static __forceinline__ frag load_contig(const float* blk, int g) {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(blk + 8 * g);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(blk + 8 * g + 4);
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  __device__ static __forceinline__ frag load_pi(const float* blk, int g) {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(blk + 4 * g);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(blk + 16 + 4 * g);
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  __device__ static __forceinline__ frag from_acc(const f32x4& lo,
+                                                  const f32x4& hi) {
+    return frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  __device__ static __forceinline__ void store4(float* dst, const f32x4& x) {
+    *reinterpret_cast<f32x4*>(dst) = x;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// LDS layout of one workgroup
+// ---------------------------------------------------------------------------
+
+template <typename TOp, int K, int C, int BV>
+struct alignas(16) Smem {
+  static constexpr int kPad = 16 / (int)sizeof(TOp);
+  static constexpr int SK = K + kPad;  // row stride of [C][K] tiles
+  static constexpr int SC = C + kPad;  // row stride of [*][C] tiles
+  TOp q[C * SK];      // q rows
+  TOp k[C * SK];      // k rows
+  TOp w[C * SK];      // W' = -W rows
+  TOp kt[K * SC];     // k transposed: kt[kk][t]
+  TOp vt[BV * SC];    // v slice transposed: vt[vc][t]
+  TOp p[C * SC];      // P[t][j] = e^{b_t-b_j} q_t.k_j, j <= t (else 0)
+  TOp tw[C * SC];     // Tw = -T diag(beta e^b)
+  TOp tu[C * SC];     // Tu = T diag(beta)
+  float a[C * C];     // A (strictly lower) for the substitution
+  float gate[C];
+  float beta[C];
+  float b[C];         // cumsum(g) inside the chunk
+  float eb[C];        // e^{b_t}
+  float ec[C];        // e^{b_C - b_t}
+};
+
+template <typename TOp, int K, int C, int BV>
+constexpr int smem_bytes() {
+  return (int)sizeof(Smem<TOp, K, C, BV>);
+}
+
+struct KArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;
+  void* o;
+  float* fs;
+  int64_t sq[3], sk[3], sv[3], sg[3], sb[3], so[3];
+  int64_t sh0[4], sfs[4];
+  int B, T, H, V, nv;
+  float scale;
+  int g_dtype, beta_dtype, o_dtype;
+  int xcd_remap;
+};
+
+// ---------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------
+
+template <typename TIn, int K, int C, int BV>
+__global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
+  using TOp = typename OpOf<TIn>::type;
+  using M = Mma<TOp>;
+  using frag = typename M::frag;
+  using S = Smem<TOp, K, C, BV>;
+  constexpr int SK = S::SK, SC = S::SC;
+  constexpr int NSW = BV / 16;   // scan waves, 16 state columns each
+  constexpr int KB = K / 32, CB = C / 32, KT = K / 16, CT = C / 16;
+  constexpr int VEC = InTraits<TIn>::kVec;
+  static_assert(NSW >= 1 && NSW <= kWaves, "BV must be 16..64");
+  static_assert(K % 32 == 0 && C % 32 == 0 && BV % VEC == 0, "tile shape");
+
+  __shared__ S s;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int n = lane & 15;   // A row / B column / D column of this lane
+  const int gq = lane >> 4;  // lane group: reduction slots / D rows
+
+  // Work unit.  With xcd_remap, units u = x*(N/8) .. are dispatched to XCD x
+  // (workgroups go round-robin over the 8 XCDs), so the V-slices of one
+  // (b, h) share an L2 and fetch q/k from HBM once.
+  int unit = blockIdx.x;
+  if (p.xcd_remap) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const int v0 = vs * BV;
+  const int T = p.T;
+
+  const TIn* qg = static_cast<const TIn*>(p.q) + bi * p.sq[0] + hi * p.sq[2];
+  const TIn* kg = static_cast<const TIn*>(p.k) + bi * p.sk[0] + hi * p.sk[2];
+  const TIn* vg = static_cast<const TIn*>(p.v) + bi * p.sv[0] + hi * p.sv[2] + v0;
+  const int64_t g_base = bi * p.sg[0] + hi * p.sg[2];
+  const int64_t b_base = bi * p.sb[0] + hi * p.sb[2];
+
+  // State slice S[:, v0 + 16*wave + n] in D layout: tile r holds rows
+  // 16r + 4gq + i.
+  f32x4 st[KT];
+  const int vcol = 16 * wave + n;  // column inside this workgroup's slice
+#pragma unroll
+  for (int r = 0; r < KT; ++r) st[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (wave < NSW && p.h0 != nullptr) {
+    const float* h0 = p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + (v0 + vcol) * p.sh0[3];
+#pragma unroll
+    for (int r = 0; r < KT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st[r][i] = h0[(16 * r + 4 * gq + i) * p.sh0[2]];
+  }
+
+  for (int t0 = 0; t0 < T; t0 += C) {
+    // ---------------- P0: chunk tiles -> LDS ----------------
+    {
+      constexpr int RV = K / VEC;  // 16-byte vectors per q/k row
+#pragma unroll 2
+      for (int idx = tid; idx < C * RV; idx += kThreads) {
+        const int t = idx / RV;
+        const int c = (idx % RV) * VEC;
+        uint4 rq = {0u, 0u, 0u, 0u}, rk = {0u, 0u, 0u, 0u};
+        if (t0 + t < T) {
+          rq = *reinterpret_cast<const uint4*>(qg + (int64_t)(t0 + t) * p.sq[1] + c);
+          rk = *reinterpret_cast<const uint4*>(kg + (int64_t)(t0 + t) * p.sk[1] + c);
+        }
+        TOp xq[VEC], xk[VEC];
+        InTraits<TIn>::to_op(rq, xq);
+        InTraits<TIn>::to_op(rk, xk);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          s.q[t * SK + c + e] = xq[e];
+          s.k[t * SK + c + e] = xk[e];
+          s.kt[(c + e) * SC + t] = xk[e];
+        }
+      }
+      constexpr int RVV = BV / VEC;
+      for (int idx = tid; idx < C * RVV; idx += kThreads) {
+        const int t = idx / RVV;
+        const int c = (idx % RVV) * VEC;
+        uint4 rv = {0u, 0u, 0u, 0u};
+        if (t0 + t < T) rv = *reinterpret_cast<const uint4*>(vg + (int64_t)(t0 + t) * p.sv[1] + c);
+        TOp xv[VEC];
+        InTraits<TIn>::to_op(rv, xv);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s.vt[(c + e) * SC + t] = xv[e];
+      }
+      if (tid < C) {
+        const bool ok = t0 + tid < T;
+        s.gate[tid] = ok ? load_scalar(p.g, g_base + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype) : 0.f;
+        s.beta[tid] = ok ? load_scalar(p.beta, b_base + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0.f;
+      }
+    }
+    __syncthreads();
+
+    // ---------------- P1: gate cumsum and decays ----------------
+    if (wave == 0) {
+      // Sequential prefix sum in each lane (same association order as a
+      // sequential cumsum).
+      float bt = 0.f;
+      for (int j = 0; j < C; ++j) {
+        const float gj = s.gate[j];
+        if (j <= lane) bt += gj;
+      }
+      const float bC = __shfl(bt, C - 1, 64);
+      if (lane < C) {
+        s.b[lane] = bt;
+        s.eb[lane] = expf(bt);
+        s.ec[lane] = expf(bC - bt);
+      }
+    }
+    __syncthreads();
+
+    // ---------------- P2: K K^T -> A,  Q K^T -> P ----------------
+    {
+      constexpr int NJ = 2 * CT * CT;
+      for (int job = wave; job < NJ; job += kWaves) {
+        const int mat = job / (CT * CT);
+        const int mt = (job / CT) % CT;
+        const int nt = job % CT;
+        const int j = 16 * nt + n;
+        if (nt > mt) {  // tile above the diagonal
+          if (mat == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s.p[(16 * mt + 4 * gq + i) * SC + j] = (TOp)0.f;
+          }
+          continue;
+        }
+        const TOp* arow = (mat == 0 ? s.k : s.q) + (16 * mt + n) * SK;
+        const TOp* brow = s.k + (16 * nt + n) * SK;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          acc = M::mma(M::load_contig(arow + 32 * kb, gq), M::load_contig(brow + 32 * kb, gq), acc);
+        }
+        const float bj = s.b[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * mt + 4 * gq + i;
+          if (mat == 0) {
+            s.a[t * C + j] = (t > j) ? acc[i] * expf(s.b[t] - bj) * s.beta[t] : 0.f;
+          } else {
+            s.p[t * SC + j] = (TOp)((t >= j) ? acc[i] * expf(s.b[t] - bj) : 0.f);
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---------------- P3: T = (I + A)^{-1} by forward substitution ----------
+    if (wave == 0) {
+      // Lane c owns column c of T: T[i][c] = [i == c] - sum_{j<i} A[i][j] T[j][c].
+      float tc[C];
+#pragma unroll
+      for (int i = 0; i < C; ++i) {
+        float acc = (lane == i) ? 1.f : 0.f;
+#pragma unroll
+        for (int j4 = 0; j4 < i; j4 += 4) {
+          const f32x4 a4 = *reinterpret_cast<const f32x4*>(&s.a[i * C + j4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j4 + e < i) acc = fmaf(-a4[e], tc[j4 + e], acc);
+        }
+        tc[i] = acc;
+      }
+      if (lane < C) {
+        const float ru = s.beta[lane];
+        const float rw = -ru * s.eb[lane];
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+          s.tw[i * SC + lane] = (TOp)(tc[i] * rw);
+          s.tu[i * SC + lane] = (TOp)(tc[i] * ru);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---------------- P4: W'^T = K^T Tw^T -> s.w (rows of W') ----------------
+    {
+      constexpr int NJ = KT * CT;
+      for (int job = wave; job < NJ; job += kWaves) {
+        const int mt = job / CT;  // K tile
+        const int nt = job % CT;  // t tile
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          acc = M::mma(M::load_pi(s.kt + (16 * mt + n) * SC + 32 * cb, gq),
+                       M::load_pi(s.tw + (16 * nt + n) * SC + 32 * cb, gq), acc);
+        }
+        M::store4(s.w + (16 * nt + n) * SK + 16 * mt + 4 * gq, acc);
+      }
+    }
+    __syncthreads();
+
+    // ---------------- P5: state-dependent part (scan waves) ----------------
+    if (wave < NSW) {
+      frag sB[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
+
+      f32x4 u[CT], oq[CT];
+#pragma unroll
+      for (int mt = 0; mt < CT; ++mt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          acc = M::mma(M::load_pi(s.tu + (16 * mt + n) * SC + 32 * cb, gq),
+                       M::load_pi(s.vt + vcol * SC + 32 * cb, gq), acc);
+        f32x4 accq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          acc = M::mma(M::load_pi(s.w + (16 * mt + n) * SK + 32 * kb, gq), sB[kb], acc);
+          accq = M::mma(M::load_pi(s.q + (16 * mt + n) * SK + 32 * kb, gq), sB[kb], accq);
+        }
+        u[mt] = acc;
+        oq[mt] = accq;
+      }
+
+      frag uB[CB], utB[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const f32x4 lo = u[2 * cb], hi = u[2 * cb + 1];
+        uB[cb] = M::from_acc(lo, hi);
+        f32x4 lo2, hi2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo2[i] = lo[i] * s.ec[32 * cb + 4 * gq + i];
+          hi2[i] = hi[i] * s.ec[32 * cb + 16 + 4 * gq + i];
+        }
+        utB[cb] = M::from_acc(lo2, hi2);
+      }
+
+      const int64_t o_col = bi * p.so[0] + hi * p.so[2] + v0 + vcol;
+#pragma unroll
+      for (int mt = 0; mt < CT; ++mt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          acc = M::mma(M::load_pi(s.p + (16 * mt + n) * SC + 32 * cb, gq), uB[cb], acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * mt + 4 * gq + i;
+          if (t0 + t < T) {
+            const float val = p.scale * (acc[i] + s.eb[t] * oq[mt][i]);
+            store_scalar(p.o, o_col + (int64_t)(t0 + t) * p.so[1], p.o_dtype, val);
+          }
+        }
+      }
+
+      const float ebC = s.eb[C - 1];
+#pragma unroll
+      for (int r = 0; r < KT; ++r) {
+        f32x4 acc = st[r] * ebC;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          acc = M::mma(M::load_pi(s.kt + (16 * r + n) * SC + 32 * cb, gq), utB[cb], acc);
+        st[r] = acc;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (wave < NSW) {
+    float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
+#pragma unroll
+    for (int r = 0; r < KT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fs[(16 * r + 4 * gq + i) * p.sfs[2]] = st[r][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch over compile-time shapes
+// ---------------------------------------------------------------------------
+
+inline int elem_bytes(int dtype) { return dtype == GDN_DTYPE_F32 ? 4 : 2; }
+
+inline bool valid_dtype(int d) {
+  return d == GDN_DTYPE_F32 || d == GDN_DTYPE_F16 || d == GDN_DTYPE_BF16;
+}
+
+template <typename TIn, int K, int C, int BV>
+constexpr bool fits() {
+  return smem_bytes<typename OpOf<TIn>::type, K, C, BV>() <= kLdsLimit;
+}
+
+template <typename TIn, int K, int C, int BV>
+int launch_one(const KArgs& a, int grid, hipStream_t stream) {
+  if constexpr (fits<TIn, K, C, BV>()) {
+    hipLaunchKernelGGL((gdn_fwd_kernel<TIn, K, C, BV>), dim3(grid), dim3(kThreads), 0,
+                       stream, a);
+    return (int)hipGetLastError();
+  } else {
+    return GDN_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename TIn, int K, int C>
+int launch_bv(const KArgs& a, int bv, int grid, hipStream_t s) {
+  switch (bv) {
+    case 16: return launch_one<TIn, K, C, 16>(a, grid, s);
+    case 32: return launch_one<TIn, K, C, 32>(a, grid, s);
+    case 64: return launch_one<TIn, K, C, 64>(a, grid, s);
+    default: return GDN_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename TIn, int K>
+int launch_c(const KArgs& a, int c, int bv, int grid, hipStream_t s) {
+  switch (c) {
+    case 32: return launch_bv<TIn, K, 32>(a, bv, grid, s);
+    case 64: return launch_bv<TIn, K, 64>(a, bv, grid, s);
+    default: return GDN_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename TIn>
+int launch_k(const KArgs& a, int kdim, int c, int bv, int grid, hipStream_t s) {
+  switch (kdim) {
+    case 32: return launch_c<TIn, 32>(a, c, bv, grid, s);
+    case 64: return launch_c<TIn, 64>(a, c, bv, grid, s);
+    case 128: return launch_c<TIn, 128>(a, c, bv, grid, s);
+    case 256: return launch_c<TIn, 256>(a, c, bv, grid, s);
+    default: return GDN_ERR_UNSUPPORTED;
+  }
+}
+
+// Whether (dtype, K, C, BV) has an instantiated kernel.
+inline bool supported(int dtype, int K, int C, int BV) {
+  auto f = [&](auto tag) -> bool {
+    using TIn = decltype(tag);
+    auto byk = [&](auto kc) -> bool {
+      constexpr int KK = decltype(kc)::value;
+      auto byc = [&](auto cc) -> bool {
+        constexpr int CC = decltype(cc)::value;
+        switch (BV) {
+          case 16: return fits<TIn, KK, CC, 16>();
+          case 32: return fits<TIn, KK, CC, 32>();
+          case 64: return fits<TIn, KK, CC, 64>();
+          default: return false;
+        }
+      };
+      if (C == 32) return byc(std::integral_constant<int, 32>{});
+      if (C == 64) return byc(std::integral_constant<int, 64>{});
+      return false;
+    };
+    switch (K) {
+      case 32: return byk(std::integral_constant<int, 32>{});
+      case 64: return byk(std::integral_constant<int, 64>{});
+      case 128: return byk(std::integral_constant<int, 128>{});
+      case 256: return byk(std::integral_constant<int, 256>{});
+      default: return false;
+    }
+  };
+  if (dtype == GDN_DTYPE_F32) return f(float{});
+  if (dtype == GDN_DTYPE_F16) return f(f16{});
+  if (dtype == GDN_DTYPE_BF16) return f(bf16_t{});
+  return false;
+}
+
+// Per-dtype launchers, each defined in its own translation unit
+// (gdn_fwd_f16.hip, gdn_fwd_bf16.hip, gdn_fwd_f32.hip) so they compile in
+// parallel.
+int launch_f16(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
+int launch_bf16(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
+int launch_f32(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
+
+}  // namespace gdn
