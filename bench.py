@@ -1,0 +1,263 @@
+"""Benchmark of the MI355X fused chunked GDN forward (BASELINE.json metric).
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` times K back-to-back
+forwards of the headline workload (configs[2]: fp16, B=2, H=16, T=4096,
+K=V=128, C=32) with inputs already resident in HBM, and prints ONE JSON line
+with tokens/s, ms per step, the roofline position of the kernel and a CPU
+baseline (the oracle's chunked-UT restatement of gdn_ref.py:48-99 on this
+host's cores).
+
+A "step" is one ``gdn_fwd`` call over the whole batch (one kernel launch).
+Extra fields report the C=64 variant and a cold-cache timing (caches flushed
+with a 512 MiB write between launches, each launch timed with its own
+events).  ``--config`` selects another BASELINE config for exploration;
+the driver's line is the default.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+
+CONFIGS = {
+    # name: (B, T, H, K, V, dtype, chunk, with_h0)
+    "cfg1": (2, 1024, 16, 128, 128, torch.float16, 32, False),
+    "cfg2": (2, 4096, 16, 128, 128, torch.float16, 32, False),
+    "cfg2_c64": (2, 4096, 16, 128, 128, torch.float16, 64, False),
+    "cfg3": (2, 16384, 16, 128, 128, torch.float16, 32, False),
+    "cfg4": (4, 4096, 16, 128, 128, torch.bfloat16, 32, True),
+}
+
+DTYPE_NAME = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
+
+
+def make_inputs(B, T, H, K, V, dtype, with_h0, device, seed=0):
+    """BASELINE.json recipe: q, k L2-normalised N(0,1); v N(0,1); beta =
+    sigmoid(N(0,1)); g = logsigmoid(N(0,1)); h0 = 0.1 N(0,1) (K x V)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def l2n(x):
+        return x / torch.sqrt(x.float().pow(2).sum(-1, keepdim=True) + 1e-6).to(x.dtype)
+
+    q = l2n(torch.randn(B, T, H, K, generator=gen, device=device)).to(dtype)
+    k = l2n(torch.randn(B, T, H, K, generator=gen, device=device)).to(dtype)
+    v = torch.randn(B, T, H, V, generator=gen, device=device).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen, device=device)).float()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen, device=device)).float()
+    h0 = (0.1 * torch.randn(B, H, K, V, generator=gen, device=device)).float() if with_h0 else None
+    return q, k, v, g, beta, h0
+
+
+def algorithmic_bytes(B, T, H, K, V, in_bytes, with_h0):
+    """Compulsory HBM bytes: per head-token q, k, v in and o out at the input
+    width plus fp32 g and beta; per (b, h) the fp32 K x V final state (and
+    h0 when given)."""
+    return B * T * H * (in_bytes * (2 * K + 2 * V) + 8) + B * H * 4 * K * V * (2 if with_h0 else 1)
+
+
+def algorithmic_flops(B, T, H, K, V, C):
+    """MFMA flops: per head-token 4CK (K K^T, Q K^T) + 2CV (P u) + 6KV
+    (W S, Q S, K^T u)."""
+    return B * T * H * (4 * C * K + 2 * C * V + 6 * K * V)
+
+
+def time_steps(fn, steps, warmup):
+    """Warm up, then time exactly ``steps`` back-to-back calls between two
+    events on the current stream (the stream the kernel is launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_cold(fn, reps, flush_bytes=512 << 20):
+    """Per-launch time with L2/MALL flushed by a 512 MiB write before each
+    launch; the flush is outside the events."""
+    buf = torch.empty(flush_bytes // 4, dtype=torch.float32, device="cuda")
+    ts = []
+    for _ in range(reps):
+        buf.fill_(1.0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    del buf
+    return statistics.median(ts)
+
+
+def cpu_baseline(B, T, H, K, V, dtype, C, budget_s=12.0):
+    """The oracle's chunked UT (fp32 PyTorch, same op order as
+    gdn_ref.py:48-99) on this host's cores over the full workload; median of
+    the runs that fit in ``budget_s`` after one warmup."""
+    from oracle import gdn_oracle as ref
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=0, dtype=dtype)
+    ref.chunked_ut(q, k, v, beta, g, C=C)  # warmup
+    ts = []
+    t_start = time.time()
+    while len(ts) < 3 or (time.time() - t_start < budget_s and len(ts) < 30):
+        t0 = time.perf_counter()
+        ref.chunked_ut(q, k, v, beta, g, C=C)
+        ts.append(time.perf_counter() - t0)
+    ms = 1e3 * statistics.median(ts)
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(B * T / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle chunked_ut (fp32 torch CPU, gdn_ref.py:48-99 op order) on the full "
+                   f"workload B{B} H{H} T{T} K{K} V{V} C{C}; median of {len(ts)} runs after 1 "
+                   f"warmup; {n} threads on '{cpu_model}'"),
+        "ms_per_step": round(ms, 3),
+    }
+
+
+def load_traffic(config):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE
+    (profiles/gdn_fwd_<config>_traffic.json), or None."""
+    path = os.path.join(REPO, "profiles", f"gdn_fwd_{config}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--block-v", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device copy (scale for rocprof byte counters)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The GDN "
+              "forward shards over (batch, head) with no communication; multi-GPU runs are not "
+              "part of this build.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    if args.calibrate_copy:
+        # A plain copy of known size: rocprofv3 FETCH_SIZE / WRITE_SIZE of this
+        # kernel divided by 256 MiB gives the counters' scale on this device.
+        n = 256 << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "launches": 3}))
+        return
+
+    pkg = importlib.import_module("v100-attention-lab_amd")
+    dev = torch.device("cuda:0")
+    B, T, H, K, V, dtype, C, with_h0 = CONFIGS[args.config]
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
+
+    def step(chunk=C):
+        return pkg.gdn_fwd(q, k, v, g, beta, h0, scale=1.0, chunk_size=chunk, block_v=args.block_v)
+
+    ms = time_steps(step, args.steps, args.warmup)
+    tokens_per_s = B * T / (ms / 1e3)
+    in_bytes = torch.finfo(dtype).bits // 8
+    alg_bytes = algorithmic_bytes(B, T, H, K, V, in_bytes, with_h0)
+    alg_flops = algorithmic_flops(B, T, H, K, V, C)
+    achieved_gbs = alg_bytes / (ms / 1e3) / 1e9
+    achieved_tflops = alg_flops / (ms / 1e3) / 1e12
+    bv = args.block_v or pkg.auto_block_v(B, H, K, V, C, dtype)
+
+    line = {
+        "metric": "GDN fwd tokens/sec at B2 H16 K=V=128 T=4096; % MFMA/HBM roofline",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAME[dtype],
+        "data": "synthetic (BASELINE.json recipe, seed 0)",
+        "config": {"workload": f"gdn_fwd {args.config}", "B": B, "T": T, "H": H, "K": K, "V": V,
+                   "chunk_size": C, "block_v": bv, "h0": with_h0,
+                   "inputs": f"q,k,v {DTYPE_NAME[dtype]}; g,beta f32; o {DTYPE_NAME[dtype]}; "
+                             "final_state f32 [B,H,K,V]"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 5),
+            "traffic": load_traffic(args.config),
+        },
+        "head_tokens_per_s": round(B * T * H / (ms / 1e3), 1),
+        "mfma": {"algorithmic_tflops": round(achieved_tflops, 3), "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                 "frac": round(achieved_tflops / MFMA_F16_PEAK_TFLOPS, 6),
+                 "flops_per_launch": alg_flops},
+        "algorithmic_bytes_per_launch": alg_bytes,
+    }
+
+    if not args.no_extras:
+        line["cold_cache_ms"] = round(time_cold(step, 5), 5)
+        if args.config == "cfg2":
+            ms64 = time_steps(lambda: step(64), max(5, args.steps // 2), 3)
+            line["c64"] = {"ms_per_step": round(ms64, 5),
+                           "tokens_per_s": round(B * T / (ms64 / 1e3), 1)}
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        step()
+        torch.cuda.synchronize()
+        line["peak_hbm_delta_bytes"] = torch.cuda.max_memory_allocated() - base
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(B, T, H, K, V, dtype, C)
+
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

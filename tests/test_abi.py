@@ -1,0 +1,189 @@
+"""CPU tests of the C-ABI library and the host-side checks (no GPU needed).
+
+* the library built from v100-attention-lab_amd/csrc loads and exports every
+  function declared in include/gdn_mi355x.h;
+* the ctypes mirror of GdnFwdParams has the C struct's exact layout (checked
+  against offsetof/sizeof from gcc on the header);
+* argument errors come back as status codes before anything is enqueued;
+* the Python surface rejects bad inputs with ValueError and never falls
+  back to a CPU path.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "gdn_mi355x.h")
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    if not os.path.exists(pkg.LIB_PATH):
+        from importlib import import_module
+        import_module("v100-attention-lab_amd.build").build(verbose=False)
+    return pkg.load_library()
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(gdn_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_api(pkg):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    assert _declared_functions() == sorted(L.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib, pkg):
+    out = subprocess.run(["nm", "-D", "--defined-only", pkg.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\s[TW]\s+(\S+)$", out, flags=re.M))
+    for name in _declared_functions():
+        assert name in exported, f"{name} not exported"
+        assert hasattr(lib, name)
+
+
+def test_abi_version(lib):
+    assert lib.gdn_fwd_abi_version() == 1
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """Compile a probe against the header with gcc and compare offsets."""
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    fields = [f for f, _ in L.GdnFwdParams._fields_]
+    src = tmp_path / "layout.c"
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(GdnFwdParams, {f}));' for f in fields)
+    src.write_text(f"#include <stddef.h>\n#include <stdio.h>\n#include \"gdn_mi355x.h\"\n"
+                   f"int main(void) {{\n{body}\n  printf(\"sizeof %zu\\n\", sizeof(GdnFwdParams));\n"
+                   f"  return 0;\n}}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{os.path.dirname(HEADER)}", str(src),
+                    "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    c_layout = dict(zip(out[0::2], map(int, out[1::2])))
+    for f in fields:
+        assert getattr(L.GdnFwdParams, f).offset == c_layout[f], f
+    assert ctypes.sizeof(L.GdnFwdParams) == c_layout["sizeof"]
+
+
+def _params(L, **kw):
+    P = L.GdnFwdParams()
+    fake = 0x1000  # never dereferenced: every case below fails validation first
+    P.q = P.k = P.v = P.g = P.beta = P.o = P.final_state = fake
+    P.q_stride[:] = (4096 * 16 * 128, 16 * 128, 128)
+    P.k_stride[:] = P.q_stride[:]
+    P.v_stride[:] = P.q_stride[:]
+    P.g_stride[:] = (4096 * 16, 16, 1)
+    P.beta_stride[:] = P.g_stride[:]
+    P.o_stride[:] = P.q_stride[:]
+    P.fs_stride[:] = (16 * 128 * 128, 128 * 128, 128, 1)
+    P.B, P.T, P.H, P.K, P.V = 2, 4096, 16, 128, 128
+    P.scale, P.chunk_size, P.block_v = 1.0, 32, 0
+    P.qkv_dtype, P.g_dtype, P.beta_dtype, P.o_dtype = 1, 0, 0, 1
+    for k_, v_ in kw.items():
+        setattr(P, k_, v_)
+    return P
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=0), 1002), (dict(T=-1), 1002), (dict(V=24), 1002),
+    (dict(chunk_size=48), 1003), (dict(K=96), 1003), (dict(block_v=128), 1003),
+    (dict(block_v=48), 1003), (dict(qkv_dtype=7), 1005), (dict(o_dtype=-1), 1005),
+    (dict(q=0x1008), 1004), (dict(final_state=None), 1001), (dict(v=None), 1001),
+])
+def test_launch_rejects_bad_arguments(lib, kw, code):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    P = _params(L, **kw)
+    assert lib.gdn_fwd_launch(ctypes.byref(P), None) == code
+    assert lib.gdn_fwd_status_string(code).decode().startswith("gdn_fwd:")
+
+
+def test_misaligned_stride_rejected(lib):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    P = _params(L)
+    P.k_stride[1] = 16 * 128 + 1
+    assert lib.gdn_fwd_launch(ctypes.byref(P), None) == 1004
+    assert lib.gdn_fwd_launch(None, None) == 1001
+
+
+def test_auto_block_v(pkg):
+    # one workgroup per CU (256) when possible, else the narrowest slice
+    assert pkg.auto_block_v(2, 16, 128, 128) == 16
+    assert pkg.auto_block_v(4, 16, 128, 128) == 32
+    assert pkg.auto_block_v(16, 16, 128, 128) == 64
+    assert pkg.auto_block_v(1, 2, 64, 48) == 16
+    assert pkg.auto_block_v(1, 1, 96, 64) == -1
+
+
+def test_status_strings(lib):
+    assert lib.gdn_fwd_status_string(0).decode() == "success"
+    for code in (1001, 1002, 1003, 1004, 1005):
+        assert "gdn_fwd" in lib.gdn_fwd_status_string(code).decode()
+
+
+# --------------------------------------------------------------------------
+# Python surface: validation happens before any device work
+# --------------------------------------------------------------------------
+
+def _cpu_inputs(B=1, T=64, H=2, K=64, V=32, dtype=torch.float16):
+    q = torch.zeros(B, T, H, K, dtype=dtype)
+    return q, q.clone(), torch.zeros(B, T, H, V, dtype=dtype), torch.zeros(B, T, H), torch.zeros(B, T, H)
+
+
+def test_cpu_tensors_are_rejected_no_fallback(pkg):
+    q, k, v, g, b = _cpu_inputs()
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.gdn_fwd(q, k, v, g, b)
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.gdn_chunk_fwd(q, k, v, b, g)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: a.__setitem__(1, a[1][:, :, :, :32]), "k shape"),
+    (lambda a: a.__setitem__(2, a[2][:, :10]), "v shape"),
+    (lambda a: a.__setitem__(3, a[3][:, :, :1]), "g must be"),
+    (lambda a: a.__setitem__(2, a[2].float()), "share a dtype"),
+    (lambda a: [a.__setitem__(i, a[i].to(torch.int32)) for i in range(3)], "not supported"),
+])
+def test_shape_and_dtype_validation(pkg, mutate, msg):
+    args = list(_cpu_inputs())
+    mutate(args)
+    with pytest.raises(ValueError, match=msg):
+        pkg.gdn_fwd(*args)
+
+
+def test_h0_and_option_validation(pkg):
+    q, k, v, g, b = _cpu_inputs()
+    with pytest.raises(ValueError, match="h0 must be"):
+        pkg.gdn_fwd(q, k, v, g, b, torch.zeros(1, 2, 32, 64))
+    with pytest.raises(ValueError, match="float32"):
+        pkg.gdn_fwd(q, k, v, g, b, torch.zeros(1, 2, 64, 32, dtype=torch.float16))
+    with pytest.raises(ValueError, match="chunk_size"):
+        pkg.gdn_fwd(q, k, v, g, b, chunk_size=16)
+    with pytest.raises(ValueError, match="block_v"):
+        pkg.gdn_fwd(q, k, v, g, b, block_v=64)
+    q2, k2, _, g2, b2 = _cpu_inputs(K=96)
+    with pytest.raises(ValueError, match="K=96"):
+        pkg.gdn_fwd(q2, k2, v, g2, b2)
+
+
+def test_missing_library_raises_importerror(tmp_path):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    saved = L._lib
+    L._lib = None
+    try:
+        with pytest.raises(ImportError, match="not found"):
+            L.load_library(str(tmp_path / "nope.so"))
+    finally:
+        L._lib = saved

@@ -76,13 +76,6 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
     _code(q, "q")
     _code(g, "g")
     _code(beta, "beta")
-    dev = q.device
-    if dev.type != "cuda":
-        raise ValueError("gdn_fwd runs on a ROCm GPU: inputs must be on a cuda device "
-                         f"(got {dev}); there is no CPU path")
-    others = (k, v, g, beta) + ((h0,) if h0 is not None else ())
-    if any(t.device != dev for t in others):
-        raise ValueError("all inputs must be on the same device")
     if B <= 0 or H <= 0:
         raise ValueError(f"B and H must be positive (got B={B}, H={H})")
     if K not in SUPPORTED_K:
@@ -93,6 +86,13 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
         raise ValueError(f"chunk_size={chunk_size} not supported {SUPPORTED_CHUNKS}")
     if block_v is not None and (block_v not in SUPPORTED_BLOCK_V or V % block_v):
         raise ValueError(f"block_v={block_v} must be one of {SUPPORTED_BLOCK_V} and divide V={V}")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("gdn_fwd runs on a ROCm GPU: inputs must be on a cuda device "
+                         f"(got {dev}); there is no CPU path")
+    others = (k, v, g, beta) + ((h0,) if h0 is not None else ())
+    if any(t.device != dev for t in others):
+        raise ValueError("all inputs must be on the same device")
     if T > 0:
         for name, t in (("q", q), ("k", k), ("v", v)):
             _check_rows(t, name)
