@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GDN_MI355X_ABI_VERSION 1
+#define GDN_MI355X_ABI_VERSION 2
 
 /* Element types of the tensors crossing the boundary. */
 enum GdnDtype {
@@ -58,6 +58,13 @@ enum GdnStatus {
   GDN_ERR_UNSUPPORTED = 1003,
   GDN_ERR_MISALIGNED = 1004,
   GDN_ERR_BAD_DTYPE = 1005
+};
+
+/* Launch options (bit flags). */
+enum GdnFlags {
+  /* Use the phase-by-phase kernel even where the pipelined one applies
+   * (testing and comparison). */
+  GDN_FLAG_PHASED_KERNEL = 1
 };
 
 typedef struct GdnFwdParams {
@@ -89,6 +96,7 @@ typedef struct GdnFwdParams {
   int32_t g_dtype;          /* GdnDtype of g */
   int32_t beta_dtype;       /* GdnDtype of beta */
   int32_t o_dtype;          /* GdnDtype of o */
+  int32_t flags;            /* GdnFlags; 0 = default */
 } GdnFwdParams;
 
 /* Enqueue one fused chunked GDN forward on `stream` (a hipStream_t; NULL =

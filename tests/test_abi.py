@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_fwd_abi_version() == 1
+    assert lib.gdn_fwd_abi_version() == 2
 
 
 def test_struct_layout_matches_header(tmp_path):
@@ -120,7 +120,9 @@ def test_auto_block_v(pkg):
     # one workgroup per CU (256) when possible, else the narrowest slice
     assert pkg.auto_block_v(2, 16, 128, 128) == 16
     assert pkg.auto_block_v(4, 16, 128, 128) == 32
-    assert pkg.auto_block_v(16, 16, 128, 128) == 64
+    assert pkg.auto_block_v(16, 16, 128, 128) == 32
+    assert pkg.auto_block_v(16, 16, 96, 128) == -1
+    assert pkg.auto_block_v(1, 2, 128, 128, dtype=torch.float32) == 16
     assert pkg.auto_block_v(1, 2, 64, 48) == 16
     assert pkg.auto_block_v(1, 1, 96, 64) == -1
 

@@ -18,6 +18,8 @@ pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-5
 TOL_LOWP = 1e-3
 
+KERNELS = ["auto", "phased"]
+
 
 def _run(pkg, dev, q, k, v, g, beta, h0=None, **kw):
     o, fs = pkg.gdn_fwd(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
@@ -75,40 +77,43 @@ def test_fp32_mild_gates_vs_chunked(pkg, cuda, K, V, T, with_h0):
 
 @pytest.mark.parametrize("gate,T,K,V", [(0.05, 256, 128, 128), (0.3, 256, 128, 128),
                                         (0.1, 512, 64, 64)])
-def test_fp16_reference_cases(pkg, cuda, gate, T, K, V):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_fp16_reference_cases(pkg, cuda, kernel, gate, T, K, V):
     """The reference's own correctness cases (bench_gdn.py:204-209), B=2 H=4."""
     q, k, v, beta, g = ref.make_inputs_reference(2, T, 4, K, V, seed=0, gate_scale=gate)
-    o, fs = _run(pkg, cuda, q, k, v, g, beta, output_dtype=torch.float32)
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, output_dtype=torch.float32, kernel=kernel)
     o_ref, h_ref = _recurrent(q, k, v, g, beta, None, dtype=torch.float32)
     eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
-    _report(f"fp16 ref-case gate={gate} T={T} K={K}", eo, eh)
+    _report(f"{kernel} fp16 ref-case gate={gate} T={T} K={K}", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
 
 
 @pytest.mark.parametrize("C", [32, 64])
-def test_cfg1_fp16(pkg, cuda, C):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_cfg1_fp16(pkg, cuda, kernel, C):
     """fp16 B2 H16 T1024 K=V=128 vs the fp32 recurrence."""
     q, k, v, g, beta, _ = ref.make_inputs_baseline(2, 1024, 16, 128, 128, seed=0)
-    o, fs = _run(pkg, cuda, q, k, v, g, beta, chunk_size=C)
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, chunk_size=C, kernel=kernel)
     o_ref, h_ref = _recurrent(q, k, v, g, beta, None, dtype=torch.float32)
     eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
-    _report(f"cfg1 fp16 C={C}", eo, eh)
+    _report(f"{kernel} cfg1 fp16 C={C}", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("degenerate", [False, True])
-def test_h0_and_degenerate(pkg, cuda, dtype, degenerate):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_h0_and_degenerate(pkg, cuda, kernel, dtype, degenerate):
     """configs[4] recipe at reduced T: h0 ~ N(0, 0.1^2); degenerate g=0, beta=1."""
     q, k, v, g, beta, h0 = ref.make_inputs_baseline(2, 512, 4, 128, 128, seed=3, dtype=dtype,
                                                     with_h0=True, degenerate=degenerate)
-    o32, fs = _run(pkg, cuda, q, k, v, g, beta, h0, output_dtype=torch.float32)
+    o32, fs = _run(pkg, cuda, q, k, v, g, beta, h0, output_dtype=torch.float32, kernel=kernel)
     o_ref, h_ref = _recurrent(q, k, v, g, beta, h0, dtype=torch.float64)
     eo, eh = ref.rel_err(o_ref, o32), ref.rel_err(h_ref, fs)
-    _report(f"{dtype} h0 degenerate={degenerate} (fp32 out)", eo, eh)
+    _report(f"{kernel} {dtype} h0 degenerate={degenerate} (fp32 out)", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
     # Default output dtype: the kernel's fp32 result rounded once to storage.
-    o_st, _ = _run(pkg, cuda, q, k, v, g, beta, h0)
+    o_st, _ = _run(pkg, cuda, q, k, v, g, beta, h0, kernel=kernel)
     assert o_st.dtype == dtype
     storage = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
     e_st = ref.rel_err(o_ref, o_st)
@@ -117,25 +122,30 @@ def test_h0_and_degenerate(pkg, cuda, dtype, degenerate):
 
 
 @pytest.mark.parametrize("K,V,T,C", [(64, 48, 77, 32), (32, 96, 33, 32), (128, 64, 130, 64),
-                                     (256, 32, 64, 32), (64, 128, 1, 32)])
-def test_shapes_k_ne_v_and_tails(pkg, cuda, K, V, T, C):
+                                     (256, 32, 64, 32), (64, 128, 1, 32), (128, 32, 300, 32),
+                                     (128, 48, 31, 32), (64, 64, 545, 32)])
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_shapes_k_ne_v_and_tails(pkg, cuda, kernel, K, V, T, C):
     """K != V pins the [B,H,K,V] state layout; T % C != 0 pins the tail mask."""
     q, k, v, beta, g = ref.make_inputs_reference(2, T, 3, K, V, seed=11, gate_scale=0.1)
     h0 = 0.1 * torch.randn(2, 3, K, V, generator=torch.Generator().manual_seed(2))
-    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, chunk_size=C, output_dtype=torch.float32)
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, chunk_size=C, output_dtype=torch.float32,
+                 kernel=kernel)
     o_ref, h_ref = _recurrent(q, k, v, g, beta, h0)
     eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
-    _report(f"K={K} V={V} T={T} C={C}", eo, eh)
+    _report(f"{kernel} K={K} V={V} T={T} C={C}", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
 
 
 @pytest.mark.parametrize("block_v", [16, 32, 64])
-def test_block_v_variants_agree(pkg, cuda, block_v):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_block_v_variants_agree(pkg, cuda, kernel, block_v):
     q, k, v, g, beta, h0 = ref.make_inputs_baseline(1, 256, 4, 128, 128, seed=4, with_h0=True)
-    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, block_v=block_v, output_dtype=torch.float32)
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, block_v=block_v, output_dtype=torch.float32,
+                 kernel=kernel)
     o_ref, h_ref = _recurrent(q, k, v, g, beta, h0)
     eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
-    _report(f"block_v={block_v}", eo, eh)
+    _report(f"{kernel} block_v={block_v}", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
 
 
@@ -162,7 +172,8 @@ def test_scale_linearity(pkg, cuda):
     assert ref.rel_err(o1 * 0.125, o2) <= 1e-6
 
 
-def test_strided_inputs_and_gate_dtypes(pkg, cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_strided_inputs_and_gate_dtypes(pkg, cuda, kernel):
     """Non-contiguous b/t/h strides (head-major storage) and bf16 beta/g."""
     B, T, H, K, V = 2, 96, 3, 64, 32
     q, k, v, beta, g = ref.make_inputs_reference(B, T, H, K, V, seed=9, gate_scale=0.1)
@@ -172,7 +183,8 @@ def test_strided_inputs_and_gate_dtypes(pkg, cuda):
     vs = v.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
     gs = g.to(torch.bfloat16)
     bs = beta.to(torch.bfloat16)
-    o, fs = pkg.gdn_fwd(qs, ks, vs, gs.to(cuda), bs.to(cuda), output_dtype=torch.float32)
+    o, fs = pkg.gdn_fwd(qs, ks, vs, gs.to(cuda), bs.to(cuda), output_dtype=torch.float32,
+                        kernel=kernel)
     torch.cuda.synchronize()
     o_ref, h_ref = _recurrent(q, k, v, gs.float(), bs.float(), None)
     eo, eh = ref.rel_err(o_ref, o.cpu()), ref.rel_err(h_ref, fs.cpu())

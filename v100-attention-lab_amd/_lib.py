@@ -9,7 +9,7 @@ import threading
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libgdn_mi355x.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum GdnDtype
 DTYPE_F32 = 0
@@ -23,6 +23,9 @@ GDN_ERR_BAD_SHAPE = 1002
 GDN_ERR_UNSUPPORTED = 1003
 GDN_ERR_MISALIGNED = 1004
 GDN_ERR_BAD_DTYPE = 1005
+
+# enum GdnFlags
+FLAG_PHASED_KERNEL = 1
 
 # Every symbol the header declares; tests check the library exports them.
 EXPORTED_SYMBOLS = (
@@ -68,6 +71,7 @@ class GdnFwdParams(ctypes.Structure):
         ("g_dtype", ctypes.c_int32),
         ("beta_dtype", ctypes.c_int32),
         ("o_dtype", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
 
 

@@ -5,10 +5,15 @@
 
 namespace gdn {
 
-// BV choice: the largest slice that still gives at least one workgroup per
-// CU (256 CUs); below that, the smallest supported slice.
+// BV choice.  Pipelined shapes: 32 columns per workgroup when that still
+// gives one workgroup per CU (256 CUs), else 16.  Phased kernel: the largest
+// slice that still gives one workgroup per CU, else the smallest supported.
 int auto_block_v(int B, int H, int K, int V, int C, int dtype) {
   const long long bh = (long long)B * H;
+  if (pipe_supported(dtype, K, C, 16) && V % 16 == 0) {
+    if (V % 32 == 0 && bh * (V / 32) >= 256) return 32;
+    return 16;
+  }
   int best = -1;
   for (int bv : {64, 32, 16}) {
     if (V % bv != 0 || !supported(dtype, K, C, bv)) continue;
@@ -92,6 +97,10 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
 
   const int grid = (int)units;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!(P.flags & GDN_FLAG_PHASED_KERNEL) && pipe_supported(P.qkv_dtype, P.K, P.chunk_size, bv)) {
+    if (P.qkv_dtype == GDN_DTYPE_F16) return launch_pipe_f16(a, P.K, bv, grid, s);
+    return launch_pipe_bf16(a, P.K, bv, grid, s);
+  }
   switch (P.qkv_dtype) {
     case GDN_DTYPE_F16: return launch_f16(a, P.K, P.chunk_size, bv, grid, s);
     case GDN_DTYPE_BF16: return launch_bf16(a, P.K, P.chunk_size, bv, grid, s);

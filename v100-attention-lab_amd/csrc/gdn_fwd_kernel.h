@@ -637,5 +637,13 @@ inline bool supported(int dtype, int K, int C, int BV) {
 int launch_f16(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
 int launch_bf16(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
 int launch_f32(const KArgs& a, int K, int C, int bv, int grid, hipStream_t s);
+// The pipelined kernel (gdn_fwd_pipe.h) covers fp16/bf16 inputs, C = 32,
+// K in {64, 128}, BV in {16, 32}; everything else runs the phased kernel.
+inline bool pipe_supported(int dtype, int K, int C, int BV) {
+  return (dtype == GDN_DTYPE_F16 || dtype == GDN_DTYPE_BF16) && C == 32 && (K == 64 || K == 128) &&
+         (BV == 16 || BV == 32);
+}
+int launch_pipe_f16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
+int launch_pipe_bf16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
 
 }  // namespace gdn

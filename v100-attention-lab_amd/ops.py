@@ -99,7 +99,10 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
     return B, T, H, K, V
 
 
-def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v):
+_KERNELS = {"auto": 0, "phased": _lib.FLAG_PHASED_KERNEL}
+
+
+def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v, kernel="auto"):
     lib = _lib.load_library()
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -124,6 +127,7 @@ def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v):
     P.g_dtype = _DTYPE_CODE[g.dtype]
     P.beta_dtype = _DTYPE_CODE[beta.dtype]
     P.o_dtype = _DTYPE_CODE[o.dtype]
+    P.flags = _KERNELS[kernel]
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         status = lib.gdn_fwd_launch(ctypes.byref(P), ctypes.c_void_p(stream))
@@ -134,7 +138,8 @@ def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v):
 def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
             beta: torch.Tensor, h0: Optional[torch.Tensor] = None, scale: float = 1.0,
             chunk_size: int = 32, *, block_v: Optional[int] = None,
-            output_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+            output_dtype: Optional[torch.dtype] = None,
+            kernel: str = "auto") -> Tuple[torch.Tensor, torch.Tensor]:
     """Fused chunked Gated DeltaNet forward on an MI355X.
 
     Args:
@@ -149,6 +154,9 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
       block_v: V columns per workgroup (16, 32, 64); None picks one.
       output_dtype: dtype of ``o``; defaults to ``q.dtype`` (as the
         reference, gdn_triton.py:126).
+      kernel: ``"auto"`` runs the software-pipelined kernel where it applies
+        (fp16/bf16, chunk 32, K in {64, 128}, block_v 16/32) and the
+        phase-by-phase kernel elsewhere; ``"phased"`` forces the latter.
 
     Returns:
       ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.
@@ -157,12 +165,14 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     ``S = e^{g} S; u = beta (v - S^T k); S += k u^T; o = scale S^T q``.
     """
     B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v)
+    if kernel not in _KERNELS:
+        raise ValueError(f"kernel={kernel!r} must be one of {sorted(_KERNELS)}")
     out_dtype = q.dtype if output_dtype is None else output_dtype
     if out_dtype not in _DTYPE_CODE:
         raise ValueError(f"output_dtype {out_dtype} not supported")
     o = torch.empty(B, T, H, V, dtype=out_dtype, device=q.device)
     fs = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    _launch(q, k, v, g, beta, h0, o, fs, fs.stride(), scale, chunk_size, block_v)
+    _launch(q, k, v, g, beta, h0, o, fs, fs.stride(), scale, chunk_size, block_v, kernel)
     return o, fs
 
 
