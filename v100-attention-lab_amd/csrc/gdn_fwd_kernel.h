@@ -220,6 +220,15 @@ struct Mma<float> {
   }
 };
 
+// The fp16 rounding residual of two accumulator tiles, as an operand:
+// x - (float)hi, so that hi + lo carries x to about 2^-22 relative.
+__device__ __forceinline__ f16x8 split_lo(const f32x4& lo, const f32x4& hi, const f16x8& h) {
+  return f16x8{(f16)(lo[0] - (float)h[0]), (f16)(lo[1] - (float)h[1]),
+               (f16)(lo[2] - (float)h[2]), (f16)(lo[3] - (float)h[3]),
+               (f16)(hi[0] - (float)h[4]), (f16)(hi[1] - (float)h[5]),
+               (f16)(hi[2] - (float)h[6]), (f16)(hi[3] - (float)h[7])};
+}
+
 // ---------------------------------------------------------------------------
 // LDS layout of one workgroup
 // ---------------------------------------------------------------------------
@@ -235,6 +244,7 @@ struct alignas(16) Smem {
   TOp kt[K * SC];     // k transposed: kt[kk][t]
   TOp vt[BV * SC];    // v slice transposed: vt[vc][t]
   TOp p[C * SC];      // P[t][j] = e^{b_t-b_j} q_t.k_j, j <= t (else 0)
+  TOp plo[C * SC];    // fp16 residual P - (float)P (fp16 operands only)
   TOp tw[C * SC];     // Tw = -T diag(beta e^b)
   TOp tu[C * SC];     // Tu = T diag(beta)
   float a[C * C];     // A (strictly lower) for the substitution
@@ -395,7 +405,10 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         if (nt > mt) {  // tile above the diagonal
           if (mat == 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s.p[(16 * mt + 4 * gq + i) * SC + j] = (TOp)0.f;
+            for (int i = 0; i < 4; ++i) {
+              s.p[(16 * mt + 4 * gq + i) * SC + j] = (TOp)0.f;
+              s.plo[(16 * mt + 4 * gq + i) * SC + j] = (TOp)0.f;
+            }
           }
           continue;
         }
@@ -413,7 +426,9 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
           if (mat == 0) {
             s.a[t * C + j] = (t > j) ? acc[i] * expf(s.b[t] - bj) * s.beta[t] : 0.f;
           } else {
-            s.p[t * SC + j] = (TOp)((t >= j) ? acc[i] * expf(s.b[t] - bj) : 0.f);
+            const float pv = (t >= j) ? acc[i] * expf(s.b[t] - bj) : 0.f;
+            s.p[t * SC + j] = (TOp)pv;
+            s.plo[t * SC + j] = (TOp)(pv - (float)(TOp)pv);
           }
         }
       }
@@ -489,11 +504,12 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         oq[mt] = accq;
       }
 
-      frag uB[CB], utB[CB];
+      frag uB[CB], uL[CB], utB[CB];
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const f32x4 lo = u[2 * cb], hi = u[2 * cb + 1];
         uB[cb] = M::from_acc(lo, hi);
+        if constexpr (std::is_same<TOp, f16>::value) uL[cb] = split_lo(lo, hi, uB[cb]);
         f32x4 lo2, hi2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -508,8 +524,15 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
       for (int mt = 0; mt < CT; ++mt) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-          acc = M::mma(M::load_pi(s.p + (16 * mt + n) * SC + 32 * cb, gq), uB[cb], acc);
+        for (int cb = 0; cb < CB; ++cb) {
+          const frag pA = M::load_pi(s.p + (16 * mt + n) * SC + 32 * cb, gq);
+          if constexpr (std::is_same<TOp, f16>::value) {
+            // P u as P_hi u_hi + P_hi u_lo + P_lo u_hi
+            acc = M::mma(pA, uL[cb], acc);
+            acc = M::mma(M::load_pi(s.plo + (16 * mt + n) * SC + 32 * cb, gq), uB[cb], acc);
+          }
+          acc = M::mma(pA, uB[cb], acc);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * mt + 4 * gq + i;

@@ -64,12 +64,13 @@ struct alignas(16) Smem {
   // SCAN -> OUT: the fp16 state at a chunk start (B-operand fragments, one
   // 16-byte fragment per lane per 32-row block) and u (one fragment).
   f16x8 so[2][NSW][K / 32][64];
-  f16x8 uo[2][NSW][64];
+  f16x8 uo[2][NSW][2][64];   // u split as hi + lo (both fp16)
   // OUT -> SCAN: U = Tu V of the next chunk (accumulator tiles).
   f32x4 uc[2][NSW][2][64];
   f16 kt[NBIG][K * SC];
   f16 vt[NBIG][BV * SC];
   f16 p[NBIG][C * SC];
+  f16 plo[NBIG][C * SC];  // P - (float)P in fp16: P u is formed as hi*hi + hi*lo + lo*hi
   float bb[NBIG][C];    // in-chunk cumsum b
   float eb[NBIG][C];
   float ec[NBIG][C];
@@ -375,7 +376,11 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         const f16x8 utB = M::from_acc(u[0] * ec_lo, u[1] * ec_hi);
 #pragma unroll
         for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * ebC);
-        s.uo[j & 1][cb][lane] = M::from_acc(u[0], u[1]);
+        {
+          const f16x8 uh = M::from_acc(u[0], u[1]);
+          s.uo[j & 1][cb][0][lane] = uh;
+          s.uo[j & 1][cb][1][lane] = split_lo(u[0], u[1], uh);
+        }
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     // o = scale (P u + diag(e^b) Q S) -> o; chunk it+1: U = Tu V -> SCAN.
     // q fragments in the pi layout: two 8-byte pieces per 32-block.
     uint2 qr[2][KB][2];
-    f16x8 pA[2];
+    f16x8 pA[2], pL[2];
     f32x4 ebv[2], oq[NSW][2];
     auto load_q = [&](int j) {
 #pragma unroll
@@ -413,10 +418,16 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     auto store_chunk = [&](int j) {
 #pragma unroll
       for (int c2 = 0; c2 < NSW; ++c2) {
-        const f16x8 uB = s.uo[j & 1][c2][lane];
+        const f16x8 uh = s.uo[j & 1][c2][0][lane];
+        const f16x8 ul = s.uo[j & 1][c2][1][lane];
         f32x4 ov[2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) ov[mt] = (M::mma(pA[mt], uB, z4) + ebv[mt] * oq[c2][mt]) * p.scale;
+        for (int mt = 0; mt < 2; ++mt) {
+          f32x4 pu = M::mma(pA[mt], ul, z4);
+          pu = M::mma(pL[mt], uh, pu);
+          pu = M::mma(pA[mt], uh, pu);
+          ov[mt] = (pu + ebv[mt] * oq[c2][mt]) * p.scale;
+        }
         const int64_t o_col = bi * p.so[0] + hi * p.so[2] + v0 + 16 * c2 + n;
         if (p.o_dtype == GDN_DTYPE_F16)
           store_o<f16>(p.o, o_col, p.so[1], j * C, T, gq, ov);
@@ -429,7 +440,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
     for (int c2 = 0; c2 < NSW; ++c2) oq[c2][0] = oq[c2][1] = z4;
     ebv[0] = ebv[1] = z4;
-    pA[0] = pA[1] = f16x8{};
+    pA[0] = pA[1] = pL[0] = pL[1] = f16x8{};
     for (int it = -8; it < nch; ++it) {
       const int j = it;
       if (j >= 1) store_chunk(j - 1);  // o of chunk j-1 (u_{j-1} written in it-1)
@@ -455,7 +466,10 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         // P and e^b of chunk j for its output in the next iteration
         const int bs = j % NBIG;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) pA[mt] = M::load_pi(s.p[bs] + (16 * mt + n) * SC, gq);
+        for (int mt = 0; mt < 2; ++mt) {
+          pA[mt] = M::load_pi(s.p[bs] + (16 * mt + n) * SC, gq);
+          pL[mt] = M::load_pi(s.plo[bs] + (16 * mt + n) * SC, gq);
+        }
         ebv[0] = *reinterpret_cast<const f32x4*>(&s.eb[bs][4 * gq]);
         ebv[1] = *reinterpret_cast<const f32x4*>(&s.eb[bs][16 + 4 * gq]);
       }
@@ -486,6 +500,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       if (j >= 0 && j < nch) {
         const int bs = j % NBIG;
         f16* sp = s.p[bs];
+        f16* spl = s.plo[bs];
         const float b = scan32(gate_at(j, cr[GW], p.g_dtype), lane);
         const float bC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), C - 1));
         if (lane < C) {
@@ -508,7 +523,10 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
             const int jj = 16 * nt + n;
             if (nt > mt) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) sp[(16 * mt + 4 * gq + i) * SC + jj] = (f16)0.f;
+              for (int i = 0; i < 4; ++i) {
+                sp[(16 * mt + 4 * gq + i) * SC + jj] = (f16)0.f;
+                spl[(16 * mt + 4 * gq + i) * SC + jj] = (f16)0.f;
+              }
               continue;
             }
             f32x4 acc = z4;
@@ -521,7 +539,10 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
               const int t = 16 * mt + 4 * gq + i;
               // mask folded into the exponent: 2^-inf = 0
               const float x = t >= jj ? bt4[i] - bj : -__builtin_inff();
-              sp[t * SC + jj] = (f16)(acc[i] * fexp(x));
+              const float pv = acc[i] * fexp(x);
+              const f16 ph = (f16)pv;
+              sp[t * SC + jj] = ph;
+              spl[t * SC + jj] = (f16)(pv - (float)ph);
             }
           }
         }
