@@ -24,6 +24,21 @@ int auto_block_v(int B, int H, int K, int V, int C, int dtype) {
   return best;
 }
 
+// The pipelined kernel addresses the rows of one chunk as a chunk base plus
+// a 32-bit per-lane offset: C rows of q, k, v, g and beta must span less
+// than 2^31 bytes (and the row strides must not be negative).
+static bool pipe_offsets_fit(const GdnFwdParams& P) {
+  const int64_t eb = elem_bytes(P.qkv_dtype);
+  const int64_t rows = 32;
+  const int64_t lim = 0x7fffffffLL;
+  const int64_t row_strides[5] = {P.q_stride[1] * eb, P.k_stride[1] * eb, P.v_stride[1] * eb,
+                                  P.g_stride[1] * elem_bytes(P.g_dtype),
+                                  P.beta_stride[1] * elem_bytes(P.beta_dtype)};
+  for (int64_t s : row_strides)
+    if (s < 0 || rows * s + (int64_t)P.K * eb + (int64_t)P.V * eb > lim) return false;
+  return true;
+}
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -97,7 +112,8 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
 
   const int grid = (int)units;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (!(P.flags & GDN_FLAG_PHASED_KERNEL) && pipe_supported(P.qkv_dtype, P.K, P.chunk_size, bv)) {
+  if (!(P.flags & GDN_FLAG_PHASED_KERNEL) && pipe_supported(P.qkv_dtype, P.K, P.chunk_size, bv) &&
+      pipe_offsets_fit(P)) {
     if (P.qkv_dtype == GDN_DTYPE_F16) return launch_pipe_f16(a, P.K, bv, grid, s);
     return launch_pipe_bf16(a, P.K, bv, grid, s);
   }

@@ -220,6 +220,16 @@ struct Mma<float> {
   }
 };
 
+// The value of x as one fp32 register: every later use (an fp16 rounding
+// and the residual against it) sees the same rounded value.  Without it the
+// compiler may fuse the product that made x into each use separately (an
+// fp16 conversion of the exact product in one, of the rounded one in the
+// other), and hi + lo then misses x by half an fp16 ulp.
+__device__ __forceinline__ float pin(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // The fp16 rounding residual of two accumulator tiles, as an operand:
 // x - (float)hi, so that hi + lo carries x to about 2^-22 relative.
 __device__ __forceinline__ f16x8 split_lo(const f32x4& lo, const f32x4& hi, const f16x8& h) {
@@ -426,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
           if (mat == 0) {
             s.a[t * C + j] = (t > j) ? acc[i] * expf(s.b[t] - bj) * s.beta[t] : 0.f;
           } else {
-            const float pv = (t >= j) ? acc[i] * expf(s.b[t] - bj) : 0.f;
+            const float pv = pin((t >= j) ? acc[i] * expf(s.b[t] - bj) : 0.f);
             s.p[t * SC + j] = (TOp)pv;
             s.plo[t * SC + j] = (TOp)(pv - (float)(TOp)pv);
           }

@@ -3,49 +3,58 @@
 //
 // The phase-by-phase kernel in gdn_fwd_kernel.h spends a chunk's time in a
 // serial sequence load -> gates -> K K^T -> substitution -> W -> scan, all
-// behind workgroup barriers.  Only u = U + W' S and S <- e^{bC} S + K^T u~
-// depend on the previous chunk, so this kernel runs the state-independent
-// work of later chunks concurrently with the scan of the current one.  A
-// workgroup has 8 waves with fixed roles and exactly one barrier per
-// iteration; iteration `it` scans chunk `it` while the other roles work
-// ahead:
+// behind workgroup barriers.  Only u = U - T diag(beta e^b) K S and
+// S <- e^{bC} S + K^T diag(e^{bC-b}) u depend on the previous chunk, so this
+// kernel runs the state-independent work of later chunks concurrently with
+// the scan of the current one.  A workgroup has 9 + BV/16 waves with fixed
+// roles and exactly one barrier per iteration; iteration `it` scans chunk
+// `it` while the other roles work ahead:
 //
-//   role  wave            chunk   work
-//   SCAN  0 .. NSW-1      it      u = U + W' S, S <- e^{bC} S + K^T diag(e^{bC-b}) u,
-//                                 o = scale (P u + diag(e^b) Q S); then, with
-//                                 the new state, Q S and U = Tu V of chunk
-//                                 it+1 (so only W' and K^T reads sit between
-//                                 the barrier and the state update).
-//                                 16 state columns per wave, the state in
-//                                 accumulator registers for the whole run.
-//   L     NSW             it+2    q rows, K^T and V^T (transposed on the MFMA
-//                                 by an identity operand), P = e^{b_t-b_j} Q K^T
-//                                 (t >= j), e^b, e^{bC-b} -> "big" slot j % 3
-//   WV    NSW+1           it+1    W'^T = K^T Tw^T -> W slot j % 2
-//   E0,E1 NSW+2, NSW+3    it+8    gates + A = beta_t e^{b_t-b_j} K K^T (t > j)
-//                                 -> A slot j % 6; E_e owns chunks j = e
-//                                 (mod 2) and loads them two iterations ahead
-//   S0,S1 NSW+4, NSW+5    pairs   forward substitution T = (I+A)^{-1} for two
-//                                 chunks at once (lanes 0-31 / 32-63, one
-//                                 column per lane, rows of A broadcast from
-//                                 LDS), spread over 4 iterations (rows
-//                                 [0,16), [16,23), [23,28), [28,32)); writes
-//                                 Tw = -T diag(beta e^b) (slot j % 4) and
-//                                 Tu = T diag(beta) (slot j % 6)
+//   role      chunk   work
+//   LOAD0/1   it+5    q, k rows and g of one chunk into registers, whole
+//                     128-byte lines per load (loader e owns chunks of
+//                     parity e, so a load has two iterations to arrive)
+//             it+3    those rows into the staged LDS rings (fp16, swizzled
+//                     16-byte pieces), g as float (zero past T)
+//   E0/E1     it+8    gates, A = beta_t e^{b_t-b_j} K K^T (t > j) stored as
+//                     A^T (E_e owns chunks of parity e; own k loads)
+//   S0/S1     pairs   X = T^T = (I + A^T)^{-1} by substitution, last row
+//                     first, one lane per row of T, two chunks per wave,
+//                     spread over four iterations; writes Tu = T diag(beta)
+//                     and Tw = -T diag(beta e^b) as operand fragments
+//   L         it+2    cumsum b, e^b, e^{bC-b}; P^T = K Q^T with the decay
+//                     and the causal mask, stored as P operand fragments
+//                     (hi and fp16 residual)
+//   WV        it+2    V^T operand fragments (v slice loaded one iteration
+//                     ahead); it+1: K^T operand fragments
+//   SCAN x NSW  it    K S, u = U + Tw (K S), S <- e^{bC} S + K^T (u e^{bC-b});
+//                     16 state columns per wave, kept in accumulators
+//   OUT       it      Q S with the chunk-start state; it-1:
+//                     o = scale (P u + diag(e^b) Q S); it+1: U = Tu V
 //
-// Pair m = (2m, 2m+1) is solved in iterations 2m-6 .. 2m-3 by S_{m%2}.
-// Every slot is written in an earlier iteration than any read of it and is
-// not rewritten before its last read (A: written j-8, last read <= j-3;
-// Tw: written >= j-4, read j-1; Tu: written >= j-4, read j-1; big: written
-// j-2, read j-1 and j; W: written j-1, read j).  Global loads are issued one
-// (L) or two (E) iterations before use, so their latency overlaps other
-// work; rows past T are clamped and zeroed without branches.
+// Every product runs on v_mfma_f32_16x16x32_f16.  Accumulator tiles hold 4
+// consecutive rows of one column per lane, so two row tiles converted to
+// fp16 are directly an operand whose contraction index runs in the order
+// pi(g, s) = {4g..4g+3, 16+4g..16+4g+3}; the kernel keeps every operand
+// pair in matching orders instead of transposing through LDS.  The state's
+// key index is stored in the order rho (sigma32 below) that makes the
+// matching q operand a plain 16-byte row piece.
+//
+// Slot lifetimes (chunk j; every write precedes its reads by a barrier and
+// no slot is rewritten before its last read): staged k written j-3, read
+// j-2 (L), j-1 (WV), j (SCAN); staged q written j-3, read j-2 (L) and, for
+// BV = 16, j (OUT); g j-3 / j-2; A written j-8, read by the substitution in
+// j-7 .. j-3; Tu, Tw written j-4 or j-3, read j-1 (OUT) and j (SCAN); P,
+// gates written j-2, read j-1 and j; V^T written j-2, read j-1; K^T written
+// j-1, read j; U and the state copies are double-buffered.
 //
 // Registers a role carries from one iteration to the next (the state, the
-// substitution's column, prefetched tiles) share one array, so the
-// kernel's register budget is the largest role's, not the sum.
+// substitution's rows, prefetched rows) live in that role's own loop, so
+// the kernel's register budget is the largest role's, not the sum.
 
 #pragma once
+
+#include <type_traits>
 
 #include "gdn_fwd_kernel.h"
 
@@ -54,32 +63,40 @@ namespace gdn {
 namespace pipe {
 
 constexpr int C = 32;
-constexpr int NA = 6, NTW = 4, NTU = 6, NBIG = 3, NWS = 2;
+constexpr int NA = 6, NTW = 5, NTU = 4, NBIG = 3, NKT = 2, NVT = 2, NRK = 4, NRG = 2;
 
 template <int K, int BV>
 struct alignas(16) Smem {
-  static constexpr int SK = K + 8;   // fp16 row stride of [C][K] tiles
-  static constexpr int SC = C + 8;   // fp16 row stride of [*][C] tiles
   static constexpr int NSW = BV / 16;
-  // SCAN -> OUT: the fp16 state at a chunk start (B-operand fragments, one
-  // 16-byte fragment per lane per 32-row block) and u (one fragment).
+  static constexpr int NRQ = BV == 16 ? 4 : 2;  // OUT reads staged q only for BV = 16
+  // SCAN -> OUT: the fp16 state at a chunk start (one B operand fragment per
+  // lane per 32-key block) and u split as hi + lo (both fp16).
   f16x8 so[2][NSW][K / 32][64];
-  f16x8 uo[2][NSW][2][64];   // u split as hi + lo (both fp16)
+  f16x8 uo[2][NSW][2][64];
   // OUT -> SCAN: U = Tu V of the next chunk (accumulator tiles).
   f32x4 uc[2][NSW][2][64];
-  f16 kt[NBIG][K * SC];
-  f16 vt[NBIG][BV * SC];
-  f16 p[NBIG][C * SC];
-  f16 plo[NBIG][C * SC];  // P - (float)P in fp16: P u is formed as hi*hi + hi*lo + lo*hi
-  float bb[NBIG][C];    // in-chunk cumsum b
-  float eb[NBIG][C];
-  float ec[NBIG][C];
-  f16 w[NWS][C * SK];
-  f16 tw[NTW][C * SC];
-  f16 tu[NTU][C * SC];
-  float a[NA][C * C];
-  float ab[NA][C];      // in-chunk cumsum b (for Tw's e^{b_j})
-  float abeta[NA][C];
+  f16x8 kt[NKT][K / 16][64];  // K^T operand fragments (rows rho, t in pi order)
+  // LOAD -> all: q and k rows of a chunk, row-major [C][K] fp16 with the
+  // 16-byte piece c of row r at index swz(r, c); g as float, zero past T.
+  f16x8 rq[NRQ][C][K / 8];
+  f16x8 rk[NRK][C][K / 8];
+  float rg[NRG][C];
+  f16x8 vt[NVT][BV / 16][64];  // V^T operand fragments (j in pi order)
+  // P operand fragments (rows t, j in pi order) as hi + fp16 residual lo:
+  // P u is formed as hi*hi + hi*lo + lo*hi.
+  f16x8 p[NBIG][2][64];
+  f16x8 plo[NBIG][2][64];
+  float bb[NBIG][C];  // in-chunk cumsum b
+  float eb[NBIG][C];  // e^b
+  float ec[NBIG][C];  // e^{bC - b}
+  // Tw = -T diag(beta e^b) and Tu = T diag(beta) as operand fragments (rows
+  // t, j in pi order).
+  f16x8 tw[NTW][2][64];
+  f16x8 tu[NTU][2][64];
+  float a[NA][C * C];  // A^T row-major: a[i][j] = A[j][i]
+  float ab[NA][C];     // in-chunk cumsum b
+  float abeta[NA][C];  // beta
+  float arw[NA][C];    // -beta e^b
 };
 
 __device__ __forceinline__ float fexp(float x) {
@@ -96,22 +113,11 @@ __device__ __forceinline__ float raw_to_float(uint32_t raw, int dtype) {
   return bf16_bits_to_float(raw & 0xffffu);
 }
 
-__device__ __forceinline__ uint32_t load_raw(const void* base, int64_t off, int dtype) {
-  if (dtype == GDN_DTYPE_F32) return static_cast<const uint32_t*>(base)[off];
-  return static_cast<const uint16_t*>(base)[off];
-}
-
 template <typename TIn>
 __device__ __forceinline__ f16x8 to_f16x8(const uint4& r) {
   f16 x[8];
   InTraits<TIn>::to_op(r, x);
   return f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-}
-
-// 8 input elements held as raw 16 bytes in the order they were loaded.
-template <typename TIn>
-__device__ __forceinline__ f16x8 to_f16x8_pairs(const uint4& r) {
-  return to_f16x8<TIn>(r);
 }
 
 __device__ __forceinline__ uint4 cr_get4(const uint32_t* cr, int w) {
@@ -123,16 +129,6 @@ __device__ __forceinline__ void cr_set4(uint32_t* cr, int w, const uint4& v) {
   cr[w + 2] = v.z;
   cr[w + 3] = v.w;
 }
-__device__ __forceinline__ f32x4 cr_getf4(const uint32_t* cr, int w) {
-  return f32x4{__uint_as_float(cr[w]), __uint_as_float(cr[w + 1]), __uint_as_float(cr[w + 2]),
-               __uint_as_float(cr[w + 3])};
-}
-__device__ __forceinline__ void cr_setf4(uint32_t* cr, int w, const f32x4& v) {
-  cr[w] = __float_as_uint(v[0]);
-  cr[w + 1] = __float_as_uint(v[1]);
-  cr[w + 2] = __float_as_uint(v[2]);
-  cr[w + 3] = __float_as_uint(v[3]);
-}
 
 // Inclusive prefix sum over lanes 0..31 (and separately 32..63) with DPP:
 // shifts by 1, 2, 4, 8 inside each row of 16 lanes (lanes shifted in from
@@ -143,7 +139,7 @@ __device__ __forceinline__ float dpp_mov0(float x) {
   return __int_as_float(
       __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, true));
 }
-__device__ __forceinline__ float scan32(float x, int /*lane*/) {
+__device__ __forceinline__ float scan32(float x) {
   x += dpp_mov0<0x111, 0xf>(x);  // row_shr:1
   x += dpp_mov0<0x112, 0xf>(x);  // row_shr:2
   x += dpp_mov0<0x114, 0xf>(x);  // row_shr:4
@@ -152,28 +148,59 @@ __device__ __forceinline__ float scan32(float x, int /*lane*/) {
   return x;                      // row_bcast:15 into rows 1 and 3
 }
 
-// 16 bytes of row min(row, T-1).  Rows past T need no zeroing: their g and
-// beta are zeroed where they are used, which makes their rows of A, T, U, W
-// and u exactly zero, so whatever finite data they hold contributes nothing
-// (and their outputs are not stored).  Not consuming the value here keeps
-// the load in flight until the iteration that uses it.
-template <typename TIn>
-__device__ __forceinline__ uint4 load_row16(const TIn* base, int64_t row_stride, int row, int T,
-                                            int col) {
-  const int rc = row < T ? row : T - 1;
-  return *reinterpret_cast<const uint4*>(base + (int64_t)rc * row_stride + col);
-}
+// The state's keys are kept in an order rho: row rho of a 32-row block holds
+// key sigma32(rho), so that the accumulator rows (4g + i, 16 + 4g + i)
+// packed into one operand are keys 8g .. 8g + 7, the plain 16-byte piece g
+// of a q row.
+__device__ __forceinline__ int sigma32(int r) { return 8 * ((r >> 2) & 3) + 4 * (r >> 4) + (r & 3); }
 
-// Operand that selects columns [16h, 16h+16) of a 32-wide plain-layout
-// block: B[8g + s][n] = (8g + s == 16h + n).  A x I_h is the identity on
-// those columns, which turns row fragments into accumulator tiles of the
-// transpose (exact: one product with 1.0 per output).
-__device__ __forceinline__ f16x8 ident_op(int h, int n, int gq) {
-  const int idx = 16 * h + n - 8 * gq;
+// Operand B[8g + s][n] = (8g + s == sel(n)): X B picks columns sel(n) of a
+// 32-wide plain-layout block X and returns them as accumulator tiles of the
+// transpose (exact: one product with 1.0 per output).  perm_op selects keys
+// sigma32(16h + n) (K^T rows in rho order), ident_op columns 16h + n.
+__device__ __forceinline__ f16x8 select_op(int idx) {
   f16x8 r;
 #pragma unroll
   for (int s = 0; s < 8; ++s) r[s] = (f16)(idx == s ? 1.f : 0.f);
   return r;
+}
+__device__ __forceinline__ f16x8 perm_op(int h, int n, int gq) {
+  return select_op(sigma32(16 * h + n) - 8 * gq);
+}
+__device__ __forceinline__ f16x8 ident_op(int h, int n, int gq) {
+  return select_op(16 * h + n - 8 * gq);
+}
+
+// Index of the 16-byte piece c of row r in a staged [C][K] fp16 tile: the
+// 16 rows of one fragment read land in 16 different bank groups.
+template <int K>
+__device__ __forceinline__ int swz(int r, int c) {
+  constexpr int RCH = K / 8;
+  return c ^ ((r / (16 / RCH)) & (RCH - 1));
+}
+
+// Byte offset of row r of a chunk that starts at row0 (column byte colb).
+// Rows past T re-read row T-1: their g and beta are zeroed where used, which
+// makes their rows of A, T, U, Tw and u exactly zero, so the finite values
+// they hold contribute nothing (and their outputs are not stored).  Without
+// a tail the offset depends on the lane only and is computed once.
+template <bool TAIL>
+__device__ __forceinline__ uint32_t row_off(int r, int row0, int T, uint32_t strideb, uint32_t colb) {
+  if constexpr (TAIL) {
+    const int rr = row0 + r < T ? r : T - 1 - row0;
+    return (uint32_t)rr * strideb + colb;
+  } else {
+    return (uint32_t)r * strideb + colb;
+  }
+}
+
+__device__ __forceinline__ uint4 ld16(const char* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(base + off);
+}
+
+__device__ __forceinline__ uint32_t ld_gate(const char* base, uint32_t off, uint32_t eb) {
+  return eb == 4 ? *reinterpret_cast<const uint32_t*>(base + off)
+                 : *reinterpret_cast<const uint16_t*>(base + off);
 }
 
 template <typename TOut>
@@ -212,36 +239,36 @@ __device__ __forceinline__ void store_o(void* o, int64_t col_off, int64_t row_st
   }
 }
 
-// Rows [LO, HI) of the forward substitution for the column this lane owns:
-// T[i][c] = [i == c] - sum_{j<i} A[i][j] T[j][c].  Row i+1 of A is read
-// from LDS while row i is computed.
+// Rows [LO, HI) of X = T^T = (I + A^T)^{-1}, last row first, for the column
+// c this lane owns (row c of T): X[i][c] = [i == c] - sum_{j>i} A[j][i] X[j][c],
+// i.e. T (I + A) = I solved along row c.  at = A^T row-major; row i-1 is
+// read from LDS while row i is computed.
 template <int LO, int HI>
-__device__ __forceinline__ void solve_rows(const float* arow, int c, float (&tc)[C]) {
-  constexpr int NQ = (HI - 1 + 3) / 4;  // float4s of the longest row
-  f32x4 cur[NQ > 0 ? NQ : 1];
+__device__ __forceinline__ void solve_rows(const float* at, int c, float (&xc)[C]) {
+  f32x4 cur[C / 4];
 #pragma unroll
-  for (int q4 = 0; q4 < (LO + 3) / 4; ++q4)
-    cur[q4] = *reinterpret_cast<const f32x4*>(arow + LO * C + 4 * q4);
+  for (int q4 = HI / 4; q4 < C / 4; ++q4)
+    cur[q4] = *reinterpret_cast<const f32x4*>(at + (HI - 1) * C + 4 * q4);
 #pragma unroll
-  for (int i = LO; i < HI; ++i) {
-    f32x4 nxt[NQ > 0 ? NQ : 1];
-    if (i + 1 < HI) {
+  for (int i = HI - 1; i >= LO; --i) {
+    f32x4 nxt[C / 4];
+    if (i - 1 >= LO) {
 #pragma unroll
-      for (int q4 = 0; q4 < (i + 1 + 3) / 4; ++q4)
-        nxt[q4] = *reinterpret_cast<const f32x4*>(arow + (i + 1) * C + 4 * q4);
+      for (int q4 = i / 4; q4 < C / 4; ++q4)
+        nxt[q4] = *reinterpret_cast<const f32x4*>(at + (i - 1) * C + 4 * q4);
     }
     float a0 = (c == i) ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-    for (int q4 = 0; q4 < (i + 3) / 4; ++q4) {
+    for (int q4 = (i + 1) / 4; q4 < C / 4; ++q4) {
       float& acc = (q4 & 1) ? a1 : a0;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (4 * q4 + e < i) acc = fmaf(-cur[q4][e], tc[4 * q4 + e], acc);
+        if (4 * q4 + e > i) acc = fmaf(-cur[q4][e], xc[4 * q4 + e], acc);
     }
-    tc[i] = a0 + a1;
-    if (i + 1 < HI) {
+    xc[i] = a0 + a1;
+    if (i - 1 >= LO) {
 #pragma unroll
-      for (int q4 = 0; q4 < (i + 1 + 3) / 4; ++q4) cur[q4] = nxt[q4];
+      for (int q4 = i / 4; q4 < C / 4; ++q4) cur[q4] = nxt[q4];
     }
   }
 }
@@ -250,16 +277,16 @@ __device__ __forceinline__ void solve_rows(const float* arow, int c, float (&tc)
 
 template <int BV>
 constexpr int pipe_waves() {
-  return 7 + BV / 16;
+  return 9 + BV / 16;
 }
 
 template <typename TIn, int K, int BV>
 __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(const KArgs p) {
   using M = Mma<f16>;
   using S = Smem<K, BV>;
-  constexpr int SK = S::SK, SC = S::SC;
   constexpr int NSW = BV / 16;
   constexpr int KB = K / 32, KT = K / 16;
+  constexpr int NRQ = S::NRQ;
   static_assert(NSW >= 1 && NSW <= 2, "BV must be 16 or 32");
   static_assert(K == 64 || K == 128, "K must be 64 or 128");
 
@@ -280,40 +307,41 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   const int v0 = vs * BV;
   const int T = p.T;
   const int nch = (T + C - 1) / C;
-
-  const TIn* qg = static_cast<const TIn*>(p.q) + bi * p.sq[0] + hi * p.sq[2];
-  const TIn* kg = static_cast<const TIn*>(p.k) + bi * p.sk[0] + hi * p.sk[2];
-  const TIn* vg = static_cast<const TIn*>(p.v) + bi * p.sv[0] + hi * p.sv[2] + v0;
-  const int64_t g_base = bi * p.sg[0] + hi * p.sg[2];
-  const int64_t b_base = bi * p.sb[0] + hi * p.sb[2];
-  const int64_t sqt = p.sq[1], skt = p.sk[1], svt = p.sv[1];
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-  // Raw g, beta of row min(t0 + (lane & 31), T-1); rows past T are zeroed
-  // where the values are used (gate_at).
-  auto load_gb = [&](uint32_t* dst, int j) {
-    const int t = j * C + (lane & 31);
-    const int tc = t < T ? t : T - 1;
-    dst[0] = load_raw(p.g, g_base + (int64_t)tc * p.sg[1], p.g_dtype);
-    dst[1] = load_raw(p.beta, b_base + (int64_t)tc * p.sb[1], p.beta_dtype);
+  // Per-head base pointers and row strides in bytes; the host checks that C
+  // rows of every input fit 31-bit offsets, so a load is a uniform chunk base
+  // plus a per-lane 32-bit offset.
+  constexpr uint32_t EB = sizeof(TIn);
+  const uint32_t geb = p.g_dtype == GDN_DTYPE_F32 ? 4u : 2u;
+  const uint32_t beb = p.beta_dtype == GDN_DTYPE_F32 ? 4u : 2u;
+  const uint32_t sqb = (uint32_t)p.sq[1] * EB, skb = (uint32_t)p.sk[1] * EB;
+  const uint32_t svb = (uint32_t)p.sv[1] * EB;
+  const uint32_t sgb = (uint32_t)p.sg[1] * geb, sbb = (uint32_t)p.sb[1] * beb;
+  const char* qh = static_cast<const char*>(p.q) + (bi * p.sq[0] + hi * p.sq[2]) * EB;
+  const char* kh = static_cast<const char*>(p.k) + (bi * p.sk[0] + hi * p.sk[2]) * EB;
+  const char* vh = static_cast<const char*>(p.v) + (bi * p.sv[0] + hi * p.sv[2] + v0) * EB;
+  const char* gh = static_cast<const char*>(p.g) + (bi * p.sg[0] + hi * p.sg[2]) * geb;
+  const char* betah = static_cast<const char*>(p.beta) + (bi * p.sb[0] + hi * p.sb[2]) * beb;
+
+  // f(std::bool_constant<tail>) for chunk j: tail is set only for a last,
+  // partial chunk.
+  auto with_tail = [&](int j, auto&& f) {
+    if (j * C + C <= T)
+      f(std::bool_constant<false>{});
+    else
+      f(std::bool_constant<true>{});
   };
+  // g or beta of row j C + (lane & 31) as loaded; zero past T.
   auto gate_at = [&](int j, uint32_t raw, int dtype) {
     const float x = raw_to_float(raw, dtype);
     return j * C + (lane & 31) < T ? x : 0.f;
   };
-  // Row fragments (2 row tiles x KB blocks, plain layout) of a [*, K] input.
-  auto load_rows = [&](uint32_t* dst, const TIn* base, int64_t stride, int j) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        cr_set4(dst, 4 * (mt * KB + kb),
-                load_row16(base, stride, j * C + 16 * mt + n, T, 32 * kb + 8 * gq));
-  };
+  // Fragment (row r, 16-byte piece c) of a staged tile.
+  auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int c) { return tile[r][swz<K>(r, c)]; };
 
-  // Roles, in wave order: SCAN x NSW, OUT, L, E0, WV, S0, S1, E1 (waves map
-  // to SIMDs round-robin, which pairs each heavy role with a lighter one).
-  enum { R_SCAN, R_OUT, R_L, R_E, R_WV, R_S, R_IDLE };
+  // Roles in wave order; waves map to SIMDs round-robin.
+  enum { R_SCAN, R_OUT, R_L, R_E, R_WV, R_S, R_LOAD, R_IDLE };
   int role = R_IDLE, ridx = 0;
   {
     const int w = wave - NSW;
@@ -325,6 +353,8 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     else if (w == 4) { role = R_S; ridx = 0; }
     else if (w == 5) { role = R_S; ridx = 1; }
     else if (w == 6) { role = R_E; ridx = 1; }
+    else if (w == 7) { role = R_LOAD; ridx = 0; }
+    else if (w == 8) { role = R_LOAD; ridx = 1; }
   }
 
   // Each role runs its own copy of the iteration loop, so registers that one
@@ -332,10 +362,12 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   // wave executes exactly one barrier per iteration.
   if (role == R_SCAN) {
     // ================================================================ SCAN
-    // chunk it: u = U + W' S, S <- e^{bC} S + K^T diag(e^{bC-b}) u; hands
-    // u and the new fp16 state to OUT.
+    // chunk it: u = U + Tw (K S), S <- e^{bC} S + K^T diag(e^{bC-b}) u;
+    // hands u and the new fp16 state to OUT.
     const int cb = ridx;
     const int vcol = 16 * cb + n;
+    // accumulator element (r, i) is state row rho = 16 r + 4 gq + i
+    auto key_of = [&](int r, int i) { return 32 * (r >> 1) + 8 * gq + 4 * (r & 1) + i; };
     f32x4 st[KT];
 #pragma unroll
     for (int r = 0; r < KT; ++r) st[r] = z4;
@@ -344,7 +376,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
       for (int r = 0; r < KT; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[r][i] = h0[(16 * r + 4 * gq + i) * p.sh0[2]];
+        for (int i = 0; i < 4; ++i) st[r][i] = h0[key_of(r, i) * p.sh0[2]];
     }
     f16x8 sB[KB];
 #pragma unroll
@@ -356,23 +388,27 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       const int j = it;
       if (j >= 0) {
         const int bs = j % NBIG;
-        const f16* sk = s.kt[bs];
-        const f16* sw = s.w[j & 1];
-        f16x8 wA[2][KB], kA[KT];
+        f16x8 kR[2][KB], kA[KT];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) wA[mt][kb] = M::load_pi(sw + (16 * mt + n) * SK + 32 * kb, gq);
+          for (int kb = 0; kb < KB; ++kb) kR[mt][kb] = staged(s.rk[j % NRK], 16 * mt + n, 4 * kb + gq);
+        const f16x8 tw0 = s.tw[j % NTW][0][lane], tw1 = s.tw[j % NTW][1][lane];
 #pragma unroll
-        for (int r = 0; r < KT; ++r) kA[r] = M::load_pi(sk + (16 * r + n) * SC, gq);
+        for (int r = 0; r < KT; ++r) kA[r] = s.kt[j % NKT][r][lane];
         f32x4 u[2] = {s.uc[j & 1][cb][0][lane], s.uc[j & 1][cb][1][lane]};
         const f32x4 ec_lo = *reinterpret_cast<const f32x4*>(&s.ec[bs][4 * gq]);
         const f32x4 ec_hi = *reinterpret_cast<const f32x4*>(&s.ec[bs][16 + 4 * gq]);
         const float ebC = s.eb[bs][C - 1];
+        // K S has rows t, so its two row tiles form the B operand of Tw
+        f32x4 ks[2] = {z4, z4};
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt) u[mt] = M::mma(wA[mt][kb], sB[kb], u[mt]);
+          for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(kR[mt][kb], sB[kb], ks[mt]);
+        const f16x8 ksB = M::from_acc(ks[0], ks[1]);
+        u[0] = M::mma(tw0, ksB, u[0]);
+        u[1] = M::mma(tw1, ksB, u[1]);
         const f16x8 utB = M::from_acc(u[0] * ec_lo, u[1] * ec_hi);
 #pragma unroll
         for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * ebC);
@@ -393,27 +429,25 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
     for (int r = 0; r < KT; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fs[(16 * r + 4 * gq + i) * p.sfs[2]] = st[r][i];
+      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i];
   } else if (role == R_OUT) {
     // ================================================================ OUT
-    // chunk it: Q S (q from global, S from SCAN); chunk it-1:
-    // o = scale (P u + diag(e^b) Q S) -> o; chunk it+1: U = Tu V -> SCAN.
-    // q fragments in the pi layout: two 8-byte pieces per 32-block.
-    uint2 qr[2][KB][2];
+    // chunk it: Q S (S from SCAN); chunk it-1: o = scale (P u + diag(e^b) Q S);
+    // chunk it+1: U = Tu V -> SCAN.  For BV = 32 q rows come from global
+    // memory (loaded one iteration ahead), for BV = 16 from the staged ring.
+    uint4 qr[2][KB];
     f16x8 pA[2], pL[2];
     f32x4 ebv[2], oq[NSW][2];
     auto load_q = [&](int j) {
+      with_tail(j, [&](auto tl) {
+        constexpr bool TAIL = decltype(tl)::value;
+        const char* base = qh + (int64_t)j * C * sqb;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int row = j * C + 16 * mt + n;
-        const int rc = row < T ? row : T - 1;
-        const TIn* qrow = qg + (int64_t)rc * sqt;
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          qr[mt][kb][0] = *reinterpret_cast<const uint2*>(qrow + 32 * kb + 4 * gq);
-          qr[mt][kb][1] = *reinterpret_cast<const uint2*>(qrow + 32 * kb + 16 + 4 * gq);
-        }
-      }
+          for (int kb = 0; kb < KB; ++kb)
+            qr[mt][kb] = ld16(base, row_off<TAIL>(16 * mt + n, j * C, T, sqb, (32 * kb + 8 * gq) * EB));
+      });
     };
     auto store_chunk = [&](int j) {
 #pragma unroll
@@ -451,8 +485,10 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            const uint4 r4 = {qr[mt][kb][0].x, qr[mt][kb][0].y, qr[mt][kb][1].x, qr[mt][kb][1].y};
-            qA[mt][kb] = to_f16x8_pairs<TIn>(r4);
+            if constexpr (BV == 16)
+              qA[mt][kb] = staged(s.rq[j % NRQ], 16 * mt + n, 4 * kb + gq);
+            else
+              qA[mt][kb] = to_f16x8<TIn>(qr[mt][kb]);
           }
 #pragma unroll
         for (int c2 = 0; c2 < NSW; ++c2)
@@ -467,41 +503,35 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         const int bs = j % NBIG;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          pA[mt] = M::load_pi(s.p[bs] + (16 * mt + n) * SC, gq);
-          pL[mt] = M::load_pi(s.plo[bs] + (16 * mt + n) * SC, gq);
+          pA[mt] = s.p[bs][mt][lane];
+          pL[mt] = s.plo[bs][mt][lane];
         }
         ebv[0] = *reinterpret_cast<const f32x4*>(&s.eb[bs][4 * gq]);
         ebv[1] = *reinterpret_cast<const f32x4*>(&s.eb[bs][16 + 4 * gq]);
       }
       const int jn = it + 1;
       if (jn >= 0 && jn < nch) {
-        const int bs = jn % NBIG;
-        const f16* stu = s.tu[jn % NTU];
-        const f16x8 tu0 = M::load_pi(stu + n * SC, gq);
-        const f16x8 tu1 = M::load_pi(stu + (16 + n) * SC, gq);
+        const f16x8 tu0 = s.tu[jn % NTU][0][lane];
+        const f16x8 tu1 = s.tu[jn % NTU][1][lane];
 #pragma unroll
         for (int c2 = 0; c2 < NSW; ++c2) {
-          const f16x8 vB = M::load_pi(s.vt[bs] + (16 * c2 + n) * SC, gq);
+          const f16x8 vB = s.vt[jn % NVT][c2][lane];
           s.uc[jn & 1][c2][0][lane] = M::mma(tu0, vB, z4);
           s.uc[jn & 1][c2][1][lane] = M::mma(tu1, vB, z4);
         }
-        load_q(jn);
+        if constexpr (BV != 16) load_q(jn);
       }
       __syncthreads();
     }
     if (nch > 0) store_chunk(nch - 1);
   } else if (role == R_L) {
     // ================================================================ L
-    // chunk it+2: gates and P = e^{b_t-b_j} Q K^T (t >= j)
-    constexpr int QW = 0, KW = 8 * KB, GW = 16 * KB;
-    uint32_t cr[16 * KB + 2];
+    // chunk it+2: b = cumsum g, e^b, e^{bC-b}; P = e^{b_t-b_j} Q K^T (t >= j)
     for (int it = -8; it < nch; ++it) {
       const int j = it + 2;
       if (j >= 0 && j < nch) {
         const int bs = j % NBIG;
-        f16* sp = s.p[bs];
-        f16* spl = s.plo[bs];
-        const float b = scan32(gate_at(j, cr[GW], p.g_dtype), lane);
+        const float b = scan32(s.rg[j % NRG][lane & 31]);
         const float bC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), C - 1));
         if (lane < C) {
           s.bb[bs][lane] = b;
@@ -513,98 +543,77 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            qf[mt][kb] = to_f16x8<TIn>(cr_get4(cr, QW + 4 * (mt * KB + kb)));
-            kf[mt][kb] = to_f16x8<TIn>(cr_get4(cr, KW + 4 * (mt * KB + kb)));
+            qf[mt][kb] = staged(s.rq[j % NRQ], 16 * mt + n, 4 * kb + gq);
+            kf[mt][kb] = staged(s.rk[j % NRK], 16 * mt + n, 4 * kb + gq);
           }
+        // P^T tiles (rows j, columns t) = K Q^T: the tiles of rows j in
+        // [0,16) and [16,32) of one column tile form one P operand.
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
+          const int t = 16 * mt + n;
+          const float bt = s.bb[bs][t];
+          f32x4 pt[2] = {z4, z4};
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const int jj = 16 * nt + n;
-            if (nt > mt) {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                sp[(16 * mt + 4 * gq + i) * SC + jj] = (f16)0.f;
-                spl[(16 * mt + 4 * gq + i) * SC + jj] = (f16)0.f;
-              }
-              continue;
-            }
+          for (int a = 0; a <= mt; ++a) {
             f32x4 acc = z4;
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) acc = M::mma(qf[mt][kb], kf[nt][kb], acc);
-            const float bj = s.bb[bs][jj];
-            const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&s.bb[bs][16 * mt + 4 * gq]);
+            for (int kb = 0; kb < KB; ++kb) acc = M::mma(kf[a][kb], qf[mt][kb], acc);
+            const f32x4 bj4 = *reinterpret_cast<const f32x4*>(&s.bb[bs][16 * a + 4 * gq]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int t = 16 * mt + 4 * gq + i;
               // mask folded into the exponent: 2^-inf = 0
-              const float x = t >= jj ? bt4[i] - bj : -__builtin_inff();
-              const float pv = acc[i] * fexp(x);
-              const f16 ph = (f16)pv;
-              sp[t * SC + jj] = ph;
-              spl[t * SC + jj] = (f16)(pv - (float)ph);
+              const float x = t >= 16 * a + 4 * gq + i ? bt - bj4[i] : -__builtin_inff();
+              pt[a][i] = pin(acc[i] * fexp(x));
             }
           }
+          const f16x8 ph = M::from_acc(pt[0], pt[1]);
+          s.p[bs][mt][lane] = ph;
+          s.plo[bs][mt][lane] = split_lo(pt[0], pt[1], ph);
         }
-      }
-      if (j + 1 >= 0 && j + 1 < nch) {
-        load_rows(cr + QW, qg, sqt, j + 1);
-        load_rows(cr + KW, kg, skt, j + 1);
-        load_gb(cr + GW, j + 1);
       }
       __syncthreads();
     }
   } else if (role == R_WV) {
     // ================================================================ WV
-    // chunk it+2: K^T and V^T transposed on the MFMA (X I_h = columns
-    // [16h, 16h+16) of X as accumulator tiles of X^T); chunk it+1:
-    // W'^T = K^T Tw^T.
-    constexpr int KW = 0, VW = 8 * KB;
-    uint32_t cr[8 * KB + 8];
+    // chunk it+2: V^T fragments (transposed on the MFMA by an identity
+    // operand); chunk it+1: K^T fragments from the staged k rows (keys in
+    // rho order via the permutation operand).
+    uint32_t cr[8];
     const f16x8 id0 = ident_op(0, n, gq), id1 = ident_op(1, n, gq);
-    for (int it = -8; it < nch; ++it) {
-      const int jw = it + 1;
-      if (jw >= 0 && jw < nch) {
-        const f16* sk = s.kt[jw % NBIG];
-        const f16* stw = s.tw[jw % NTW];
-        f16* sw = s.w[jw & 1];
-        f16x8 kA[KT], tB[2];
-#pragma unroll
-        for (int mt = 0; mt < KT; ++mt) kA[mt] = M::load_pi(sk + (16 * mt + n) * SC, gq);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) tB[nt] = M::load_pi(stw + (16 * nt + n) * SC, gq);
-#pragma unroll
-        for (int mt = 0; mt < KT; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-            M::store4(sw + (16 * nt + n) * SK + 16 * mt + 4 * gq, M::mma(kA[mt], tB[nt], z4));
-      }
-      const int j = it + 2;
-      if (j >= 0 && j < nch) {
-        const int bs = j % NBIG;
-        f16* sk = s.kt[bs];
-        f16* sv = s.vt[bs];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-          for (int c = 0; c < KT; ++c) {
-            const f16x8 kf = to_f16x8<TIn>(cr_get4(cr, KW + 4 * (mt * KB + (c >> 1))));
-            M::store4(sk + (16 * c + n) * SC + 16 * mt + 4 * gq, M::mma(kf, (c & 1) ? id1 : id0, z4));
-          }
-          const f16x8 vf = to_f16x8<TIn>(cr_get4(cr, VW + 4 * mt));
-#pragma unroll
-          for (int c = 0; c < BV / 16; ++c)
-            M::store4(sv + (16 * c + n) * SC + 16 * mt + 4 * gq, M::mma(vf, (c & 1) ? id1 : id0, z4));
-        }
-      }
-      if (j + 1 >= 0 && j + 1 < nch) {
-        load_rows(cr + KW, kg, skt, j + 1);
-        // v slice: lane (n, gq) reads columns [8 gq, +8); lanes with
-        // 8 gq >= BV read a duplicate the transpose never selects
-        const int cv = 8 * gq < BV ? 8 * gq : BV - 8;
+    const f16x8 pm0 = perm_op(0, n, gq), pm1 = perm_op(1, n, gq);
+    // v slice: lane (n, gq) reads columns [8 gq, +8); lanes with 8 gq >= BV
+    // read a duplicate the transpose never selects
+    const uint32_t cvb = (8 * gq < BV ? 8 * gq : BV - 8) * EB;
+    auto load_v = [&](int j) {
+      with_tail(j, [&](auto tl) {
+        constexpr bool TAIL = decltype(tl)::value;
+        const char* base = vh + (int64_t)j * C * svb;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
-          cr_set4(cr, VW + 4 * mt, load_row16(vg, svt, (j + 1) * C + 16 * mt + n, T, cv));
+          cr_set4(cr, 4 * mt, ld16(base, row_off<TAIL>(16 * mt + n, j * C, T, svb, cvb)));
+      });
+    };
+    for (int it = -8; it < nch; ++it) {
+      const int j = it + 2;
+      if (j >= 0 && j < nch) {
+        const f16x8 vf0 = to_f16x8<TIn>(cr_get4(cr, 0));
+        const f16x8 vf1 = to_f16x8<TIn>(cr_get4(cr, 4));
+#pragma unroll
+        for (int c = 0; c < BV / 16; ++c) {
+          const f16x8 id = (c & 1) ? id1 : id0;
+          s.vt[j % NVT][c][lane] = M::from_acc(M::mma(vf0, id, z4), M::mma(vf1, id, z4));
+        }
+      }
+      if (j + 1 >= 0 && j + 1 < nch) load_v(j + 1);
+      const int jw = it + 1;
+      if (jw >= 0 && jw < nch) {
+#pragma unroll
+        for (int c = 0; c < KT; ++c) {
+          const f16x8 pm = (c & 1) ? pm1 : pm0;
+          const int kb = c >> 1;
+          s.kt[jw % NKT][c][lane] = M::from_acc(M::mma(staged(s.rk[jw % NRK], n, 4 * kb + gq), pm, z4),
+                                                M::mma(staged(s.rk[jw % NRK], 16 + n, 4 * kb + gq), pm, z4));
+        }
       }
       __syncthreads();
     }
@@ -612,28 +621,39 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     // ================================================================ E
     // chunk it+8 (E_e owns chunks = e mod 2): gates, A = beta_t e^{b_t-b_j} K K^T
     const int e = ridx;
-    constexpr int KW = 0, GW = 8 * KB;
+    constexpr int GW = 8 * KB;
     uint32_t cr[8 * KB + 2];
     auto e_load = [&](int j) {
-      load_rows(cr + KW, kg, skt, j);
-      load_gb(cr + GW, j);
+      with_tail(j, [&](auto tl) {
+        constexpr bool TAIL = decltype(tl)::value;
+        const char* base = kh + (int64_t)j * C * skb;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+            cr_set4(cr, 4 * (mt * KB + kb),
+                    ld16(base, row_off<TAIL>(16 * mt + n, j * C, T, skb, (32 * kb + 8 * gq) * EB)));
+        cr[GW] = ld_gate(gh + (int64_t)j * C * sgb, row_off<TAIL>(lane & 31, j * C, T, sgb, 0), geb);
+        cr[GW + 1] = ld_gate(betah + (int64_t)j * C * sbb, row_off<TAIL>(lane & 31, j * C, T, sbb, 0), beb);
+      });
     };
     if (e < nch) e_load(e);
     for (int it = -8; it < nch; ++it) {
       const int j = it + 8;
       if (j >= 0 && j < nch && (j & 1) == e) {
         const int as = j % NA;
-        const float b = scan32(gate_at(j, cr[GW], p.g_dtype), lane);
+        const float b = scan32(gate_at(j, cr[GW], p.g_dtype));
         const float bet = gate_at(j, cr[GW + 1], p.beta_dtype);
         if (lane < C) {
           s.ab[as][lane] = b;
           s.abeta[as][lane] = bet;
+          s.arw[as][lane] = -bet * fexp(b);
         }
         f16x8 kf[2][KB];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) kf[mt][kb] = to_f16x8<TIn>(cr_get4(cr, KW + 4 * (mt * KB + kb)));
+          for (int kb = 0; kb < KB; ++kb) kf[mt][kb] = to_f16x8<TIn>(cr_get4(cr, 4 * (mt * KB + kb)));
         float* sa = s.a[as];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
@@ -646,12 +666,15 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
             const float bj = s.ab[as][jj];
             const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&s.ab[as][16 * mt + 4 * gq]);
             const f32x4 be4 = *reinterpret_cast<const f32x4*>(&s.abeta[as][16 * mt + 4 * gq]);
+            f32x4 av;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int t = 16 * mt + 4 * gq + i;
               const float x = t > jj ? bt4[i] - bj : -__builtin_inff();
-              sa[t * C + jj] = acc[i] * fexp(x) * be4[i];
+              av[i] = acc[i] * fexp(x) * be4[i];
             }
+            // A[t][jj] for 4 consecutive t: a piece of row jj of A^T
+            *reinterpret_cast<f32x4*>(sa + jj * C + 16 * mt + 4 * gq) = av;
           }
         if (j + 2 < nch) e_load(j + 2);
       }
@@ -659,13 +682,14 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     }
   } else if (role == R_S) {
     // ================================================================ S
-    // pair m = (2m, 2m+1) in iterations 2m-6 .. 2m-3; m' = m + 8 keeps the
-    // arithmetic non-negative
+    // pair m = (2m, 2m+1) in iterations 2m-6 .. 2m-3 (S_{m%2}; lanes 0-31
+    // chunk 2m, 32-63 chunk 2m+1); m' = m + 8 keeps the arithmetic
+    // non-negative
     const int sidx = ridx;
     const int h = lane >> 5, c = lane & 31;
-    float tc[C];
+    float xc[C];
 #pragma unroll
-    for (int i = 0; i < C; ++i) tc[i] = 0.f;
+    for (int i = 0; i < C; ++i) xc[i] = 0.f;
     for (int it = -8; it < nch; ++it) {
       const int itp = it + 16;
       int mp = (itp + 4) >> 1;
@@ -673,27 +697,79 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       const int seg = itp + 6 - 2 * mp;  // 0..3
       const int j = 2 * (mp - 8) + h;
       const bool valid = j >= 0 && j < nch;
-      const float* arow = s.a[valid ? j % NA : 0];
+      const float* at = s.a[valid ? j % NA : 0];
+      // rows 31..16, 15..9, 8..4, 3..0: about 120 FMAs per lane each
       if (seg == 0) {
-        solve_rows<0, 16>(arow, c, tc);
+        solve_rows<16, 32>(at, c, xc);
       } else if (seg == 1) {
-        solve_rows<16, 23>(arow, c, tc);
+        solve_rows<9, 16>(at, c, xc);
       } else if (seg == 2) {
-        solve_rows<23, 28>(arow, c, tc);
+        solve_rows<4, 9>(at, c, xc);
       } else {
-        solve_rows<28, 32>(arow, c, tc);
+        solve_rows<0, 4>(at, c, xc);
         if (valid) {
+          // lane c holds row c of T: row t = c of the Tu / Tw operand tile
+          // c / 16, 8 values per lane group g
           const int as = j % NA;
-          const float ru = s.abeta[as][c];
-          const float rw = -ru * fexp(s.ab[as][c]);
-          f16* stw = s.tw[j % NTW];
-          f16* stu = s.tu[j % NTU];
+          const int mt = c >> 4, nl = c & 15;
 #pragma unroll
-          for (int i = 0; i < C; ++i) {
-            stw[i * SC + c] = (f16)(tc[i] * rw);
-            stu[i * SC + c] = (f16)(tc[i] * ru);
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 u0 = *reinterpret_cast<const f32x4*>(&s.abeta[as][4 * g4]);
+            const f32x4 u1 = *reinterpret_cast<const f32x4*>(&s.abeta[as][16 + 4 * g4]);
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(&s.arw[as][4 * g4]);
+            const f32x4 w1 = *reinterpret_cast<const f32x4*>(&s.arw[as][16 + 4 * g4]);
+            f16x8 fu, fw;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              fu[e] = (f16)(xc[4 * g4 + e] * u0[e]);
+              fu[4 + e] = (f16)(xc[16 + 4 * g4 + e] * u1[e]);
+              fw[e] = (f16)(xc[4 * g4 + e] * w0[e]);
+              fw[4 + e] = (f16)(xc[16 + 4 * g4 + e] * w1[e]);
+            }
+            s.tu[j % NTU][mt][16 * g4 + nl] = fu;
+            s.tw[j % NTW][mt][16 * g4 + nl] = fw;
           }
         }
+      }
+      __syncthreads();
+    }
+  } else if (role == R_LOAD) {
+    // ============================================================= LOAD
+    // Loader e owns chunks of parity e: in iteration it (it+3 = e mod 2) it
+    // stages chunk it+3 from its registers and loads chunk it+5 into them.
+    // Each load covers 4 rows x 256 bytes (whole 128-byte lines).
+    constexpr int RCH = K / 8, NI = C * RCH / 64;
+    constexpr int KW = 4 * NI, GW = 8 * NI;
+    uint32_t cr[8 * NI + 1];
+    auto ld = [&](int j) {
+      with_tail(j, [&](auto tl) {
+        constexpr bool TAIL = decltype(tl)::value;
+        cr[GW] = ld_gate(gh + (int64_t)j * C * sgb, row_off<TAIL>(lane & 31, j * C, T, sgb, 0), geb);
+        const char* bq = qh + (int64_t)j * C * sqb;
+        const char* bk = kh + (int64_t)j * C * skb;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int e = 64 * i + lane, r = e / RCH, c = e % RCH;
+          cr_set4(cr, 4 * i, ld16(bq, row_off<TAIL>(r, j * C, T, sqb, 8 * c * EB)));
+          cr_set4(cr, KW + 4 * i, ld16(bk, row_off<TAIL>(r, j * C, T, skb, 8 * c * EB)));
+        }
+      });
+    };
+    auto stage = [&](int j) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int e = 64 * i + lane, r = e / RCH, c = e % RCH;
+        s.rq[j % NRQ][r][swz<K>(r, c)] = to_f16x8<TIn>(cr_get4(cr, 4 * i));
+        s.rk[j % NRK][r][swz<K>(r, c)] = to_f16x8<TIn>(cr_get4(cr, KW + 4 * i));
+      }
+      if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[GW], p.g_dtype);
+    };
+    const int e = ridx;
+    for (int it = -8; it < nch; ++it) {
+      const int j = it + 3;
+      if ((j & 1) == e) {
+        if (j >= 0 && j < nch) stage(j);
+        if (j + 2 >= 0 && j + 2 < nch) ld(j + 2);
       }
       __syncthreads();
     }
