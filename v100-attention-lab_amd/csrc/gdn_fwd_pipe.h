@@ -11,22 +11,19 @@
 // `it` while the other roles work ahead:
 //
 //   role      chunk   work
-//   LOAD0/1   it+5    q, k rows and g of one chunk into registers, whole
-//                     128-byte lines per load (loader e owns chunks of
-//                     parity e, so a load has two iterations to arrive)
-//             it+3    those rows into the staged LDS rings (fp16, swizzled
-//                     16-byte pieces), g as float (zero past T)
-//   E0/E1     it+8    gates, A = beta_t e^{b_t-b_j} K K^T (t > j) stored as
+//   LOAD0     it+4    q rows and g into registers (whole 128-byte lines)
+//             it+3    those into the staged LDS rings (fp16, swizzled
+//                     16-byte pieces; g as float, zero past T)
+//   LOAD1     it+4/3  the same for k rows and the workgroup's v slice
+//   E0/E1     it+10   gates, A = beta_t e^{b_t-b_j} K K^T (t > j) stored as
 //                     A^T (E_e owns chunks of parity e; own k loads)
-//   S0/S1     pairs   X = T^T = (I + A^T)^{-1} by substitution, last row
+//   S0/S1/S2  pairs   X = T^T = (I + A^T)^{-1} by substitution, last row
 //                     first, one lane per row of T, two chunks per wave,
-//                     spread over four iterations; writes Tu = T diag(beta)
+//                     spread over six iterations; writes Tu = T diag(beta)
 //                     and Tw = -T diag(beta e^b) as operand fragments
 //   L         it+2    cumsum b, e^b, e^{bC-b}; P^T = K Q^T with the decay
 //                     and the causal mask, stored as P operand fragments
 //                     (hi and fp16 residual)
-//   WV        it+2    V^T operand fragments (v slice loaded one iteration
-//                     ahead); it+1: K^T operand fragments
 //   SCAN x NSW  it    K S, u = U + Tw (K S), S <- e^{bC} S + K^T (u e^{bC-b});
 //                     16 state columns per wave, kept in accumulators
 //   OUT       it      Q S with the chunk-start state; it-1:
@@ -36,17 +33,19 @@
 // consecutive rows of one column per lane, so two row tiles converted to
 // fp16 are directly an operand whose contraction index runs in the order
 // pi(g, s) = {4g..4g+3, 16+4g..16+4g+3}; the kernel keeps every operand
-// pair in matching orders instead of transposing through LDS.  The state's
-// key index is stored in the order rho (sigma32 below) that makes the
-// matching q operand a plain 16-byte row piece.
+// pair in matching orders.  Operands that need the staged rows transposed
+// (K^T for the state update, V^T for U) are read with ds_read_b64_tr_b16.
+// The state's key index is stored in the order rho (sigma32 below) that
+// makes the q operand a plain 16-byte row piece and the K^T operand four
+// consecutive keys per transposed read.
 //
 // Slot lifetimes (chunk j; every write precedes its reads by a barrier and
 // no slot is rewritten before its last read): staged k written j-3, read
-// j-2 (L), j-1 (WV), j (SCAN); staged q written j-3, read j-2 (L) and, for
-// BV = 16, j (OUT); g j-3 / j-2; A written j-8, read by the substitution in
-// j-7 .. j-3; Tu, Tw written j-4 or j-3, read j-1 (OUT) and j (SCAN); P,
-// gates written j-2, read j-1 and j; V^T written j-2, read j-1; K^T written
-// j-1, read j; U and the state copies are double-buffered.
+// j-2 (L) and j (SCAN); staged q written j-3, read j-2 (L) and, for BV = 16,
+// j (OUT); staged v written j-3, read j-1; g j-3 / j-2; A written j-10,
+// read by the substitution in j-9 .. j-3; Tu, Tw written j-4 or j-3, read
+// j-1 (OUT) and j (SCAN); P, gates written j-2, read j-1 and j; U and the
+// state copies are double-buffered.
 //
 // Registers a role carries from one iteration to the next (the state, the
 // substitution's rows, prefetched rows) live in that role's own loop, so
@@ -63,7 +62,9 @@ namespace gdn {
 namespace pipe {
 
 constexpr int C = 32;
-constexpr int NA = 6, NTW = 5, NTU = 4, NBIG = 3, NKT = 2, NVT = 2, NRK = 4, NRG = 2;
+constexpr int NA = 8, NTW = 5, NTU = 4, NBIG = 3, NRK = 4, NRG = 2, NRV = 3;
+// first iteration: E works 10 chunks ahead of the scan
+constexpr int IT0 = -10;
 
 template <int K, int BV>
 struct alignas(16) Smem {
@@ -75,13 +76,12 @@ struct alignas(16) Smem {
   f16x8 uo[2][NSW][2][64];
   // OUT -> SCAN: U = Tu V of the next chunk (accumulator tiles).
   f32x4 uc[2][NSW][2][64];
-  f16x8 kt[NKT][K / 16][64];  // K^T operand fragments (rows rho, t in pi order)
   // LOAD -> all: q and k rows of a chunk, row-major [C][K] fp16 with the
   // 16-byte piece c of row r at index swz(r, c); g as float, zero past T.
   f16x8 rq[NRQ][C][K / 8];
   f16x8 rk[NRK][C][K / 8];
   float rg[NRG][C];
-  f16x8 vt[NVT][BV / 16][64];  // V^T operand fragments (j in pi order)
+  f16x8 rv[NRV][C][BV / 8];    // staged v slice rows (plain, fp16)
   // P operand fragments (rows t, j in pi order) as hi + fp16 residual lo:
   // P u is formed as hi*hi + hi*lo + lo*hi.
   f16x8 p[NBIG][2][64];
@@ -179,6 +179,23 @@ __device__ __forceinline__ int swz(int r, int c) {
   return c ^ ((r / (16 / RCH)) & (RCH - 1));
 }
 
+// ds_read_b64_tr_b16: within each group of 16 lanes, the 4 fp16 values
+// that lanes 0..15 address form a 16 x 4 matrix M; lane 4a + b receives
+// M[a][b], M[4 + a][b], M[8 + a][b], M[12 + a][b].  With lane m of a group
+// addressing row t0 + m / 4 at column c0 + 4 (m % 4), lane n receives
+// rows t0 .. t0+3 of column c0 + n: four contraction elements of a
+// transposed operand.
+__device__ __forceinline__ f16x4 lds_tr16(const void* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(__attribute__((address_space(3))) void*)p);
+  return __builtin_bit_cast(f16x4, r);
+}
+
+__device__ __forceinline__ f16x8 cat8(const f16x4& lo, const f16x4& hi) {
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // Byte offset of row r of a chunk that starts at row0 (column byte colb).
 // Rows past T re-read row T-1: their g and beta are zeroed where used, which
 // makes their rows of A, T, U, Tw and u exactly zero, so the finite values
@@ -241,10 +258,49 @@ __device__ __forceinline__ void store_o(void* o, int64_t col_off, int64_t row_st
 
 // Rows [LO, HI) of X = T^T = (I + A^T)^{-1}, last row first, for the column
 // c this lane owns (row c of T): X[i][c] = [i == c] - sum_{j>i} A[j][i] X[j][c],
-// i.e. T (I + A) = I solved along row c.  at = A^T row-major; row i-1 is
-// read from LDS while row i is computed.
+// i.e. T (I + A) = I solved along row c.  at = A^T row-major; rows i-1 and
+// i-2 are read from LDS while row i is computed (the short rows finish their
+// FMAs before one LDS read returns).
 template <int LO, int HI>
 __device__ __forceinline__ void solve_rows(const float* at, int c, float (&xc)[C]) {
+  // rows i and i-1 held while row i-2 is read
+  f32x4 r0[C / 4], r1[C / 4];
+#pragma unroll
+  for (int q4 = HI / 4; q4 < C / 4; ++q4) r0[q4] = *reinterpret_cast<const f32x4*>(at + (HI - 1) * C + 4 * q4);
+  if (HI - 2 >= LO) {
+#pragma unroll
+    for (int q4 = (HI - 1) / 4; q4 < C / 4; ++q4) r1[q4] = *reinterpret_cast<const f32x4*>(at + (HI - 2) * C + 4 * q4);
+  }
+#pragma unroll
+  for (int i = HI - 1; i >= LO; --i) {
+    f32x4 r2[C / 4];
+    if (i - 2 >= LO) {
+#pragma unroll
+      for (int q4 = (i - 1) / 4; q4 < C / 4; ++q4)
+        r2[q4] = *reinterpret_cast<const f32x4*>(at + (i - 2) * C + 4 * q4);
+    }
+    float a0 = (c == i) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+    for (int q4 = (i + 1) / 4; q4 < C / 4; ++q4) {
+      float& acc = (q4 & 1) ? a1 : a0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (4 * q4 + e > i) acc = fmaf(-r0[q4][e], xc[4 * q4 + e], acc);
+    }
+    xc[i] = a0 + a1;
+#pragma unroll
+    for (int q4 = i / 4; q4 < C / 4; ++q4) r0[q4] = r1[q4];
+    if (i - 2 >= LO) {
+#pragma unroll
+      for (int q4 = (i - 1) / 4; q4 < C / 4; ++q4) r1[q4] = r2[q4];
+    }
+  }
+}
+
+// The same with one row read ahead (the long rows, where the row's own FMAs
+// cover the read latency and two rows in flight would cost registers).
+template <int LO, int HI>
+__device__ __forceinline__ void solve_rows1(const float* at, int c, float (&xc)[C]) {
   f32x4 cur[C / 4];
 #pragma unroll
   for (int q4 = HI / 4; q4 < C / 4; ++q4)
@@ -341,7 +397,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int c) { return tile[r][swz<K>(r, c)]; };
 
   // Roles in wave order; waves map to SIMDs round-robin.
-  enum { R_SCAN, R_OUT, R_L, R_E, R_WV, R_S, R_LOAD, R_IDLE };
+  enum { R_SCAN, R_OUT, R_L, R_E, R_S, R_LOAD, R_IDLE };
   int role = R_IDLE, ridx = 0;
   {
     const int w = wave - NSW;
@@ -349,12 +405,12 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     else if (w == 0) role = R_OUT;
     else if (w == 1) role = R_L;
     else if (w == 2) { role = R_E; ridx = 0; }
-    else if (w == 3) role = R_WV;
-    else if (w == 4) { role = R_S; ridx = 0; }
-    else if (w == 5) { role = R_S; ridx = 1; }
-    else if (w == 6) { role = R_E; ridx = 1; }
-    else if (w == 7) { role = R_LOAD; ridx = 0; }
-    else if (w == 8) { role = R_LOAD; ridx = 1; }
+    else if (w == 3) { role = R_S; ridx = 0; }
+    else if (w == 4) { role = R_S; ridx = 1; }
+    else if (w == 5) { role = R_E; ridx = 1; }
+    else if (w == 6) { role = R_LOAD; ridx = 0; }
+    else if (w == 7) { role = R_LOAD; ridx = 1; }
+    else if (w == 8) { role = R_S; ridx = 2; }
   }
 
   // Each role runs its own copy of the iteration loop, so registers that one
@@ -384,7 +440,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
       s.so[0][cb][kb][lane] = sB[kb];
     }
-    for (int it = -8; it < nch; ++it) {
+    for (int it = IT0; it < nch; ++it) {
       const int j = it;
       if (j >= 0) {
         const int bs = j % NBIG;
@@ -395,7 +451,15 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
           for (int kb = 0; kb < KB; ++kb) kR[mt][kb] = staged(s.rk[j % NRK], 16 * mt + n, 4 * kb + gq);
         const f16x8 tw0 = s.tw[j % NTW][0][lane], tw1 = s.tw[j % NTW][1][lane];
 #pragma unroll
-        for (int r = 0; r < KT; ++r) kA[r] = s.kt[j % NKT][r][lane];
+        for (int r = 0; r < KT; ++r) {
+          // rows t = 4 gq + (n / 4) (+16), keys sigma-ordered for rho = 16 r + n
+          const int piece = 4 * (r >> 1) + (n & 3);
+          const char* base = reinterpret_cast<const char*>(s.rk[j % NRK]);
+          const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
+          const f16x4 lo = lds_tr16(base + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
+          const f16x4 hi = lds_tr16(base + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
+          kA[r] = cat8(lo, hi);
+        }
         f32x4 u[2] = {s.uc[j & 1][cb][0][lane], s.uc[j & 1][cb][1][lane]};
         const f32x4 ec_lo = *reinterpret_cast<const f32x4*>(&s.ec[bs][4 * gq]);
         const f32x4 ec_hi = *reinterpret_cast<const f32x4*>(&s.ec[bs][16 + 4 * gq]);
@@ -475,7 +539,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     for (int c2 = 0; c2 < NSW; ++c2) oq[c2][0] = oq[c2][1] = z4;
     ebv[0] = ebv[1] = z4;
     pA[0] = pA[1] = pL[0] = pL[1] = f16x8{};
-    for (int it = -8; it < nch; ++it) {
+    for (int it = IT0; it < nch; ++it) {
       const int j = it;
       if (j >= 1) store_chunk(j - 1);  // o of chunk j-1 (u_{j-1} written in it-1)
       if (j >= 0) {
@@ -515,7 +579,10 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
         const f16x8 tu1 = s.tu[jn % NTU][1][lane];
 #pragma unroll
         for (int c2 = 0; c2 < NSW; ++c2) {
-          const f16x8 vB = s.vt[jn % NVT][c2][lane];
+          const char* base = reinterpret_cast<const char*>(s.rv[jn % NRV]);
+          const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
+          const int cb = (16 * c2 + 4 * (n & 3)) * 2;
+          const f16x8 vB = cat8(lds_tr16(base + t0 * (BV * 2) + cb), lds_tr16(base + t1 * (BV * 2) + cb));
           s.uc[jn & 1][c2][0][lane] = M::mma(tu0, vB, z4);
           s.uc[jn & 1][c2][1][lane] = M::mma(tu1, vB, z4);
         }
@@ -527,7 +594,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   } else if (role == R_L) {
     // ================================================================ L
     // chunk it+2: b = cumsum g, e^b, e^{bC-b}; P = e^{b_t-b_j} Q K^T (t >= j)
-    for (int it = -8; it < nch; ++it) {
+    for (int it = IT0; it < nch; ++it) {
       const int j = it + 2;
       if (j >= 0 && j < nch) {
         const int bs = j % NBIG;
@@ -573,53 +640,9 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       }
       __syncthreads();
     }
-  } else if (role == R_WV) {
-    // ================================================================ WV
-    // chunk it+2: V^T fragments (transposed on the MFMA by an identity
-    // operand); chunk it+1: K^T fragments from the staged k rows (keys in
-    // rho order via the permutation operand).
-    uint32_t cr[8];
-    const f16x8 id0 = ident_op(0, n, gq), id1 = ident_op(1, n, gq);
-    const f16x8 pm0 = perm_op(0, n, gq), pm1 = perm_op(1, n, gq);
-    // v slice: lane (n, gq) reads columns [8 gq, +8); lanes with 8 gq >= BV
-    // read a duplicate the transpose never selects
-    const uint32_t cvb = (8 * gq < BV ? 8 * gq : BV - 8) * EB;
-    auto load_v = [&](int j) {
-      with_tail(j, [&](auto tl) {
-        constexpr bool TAIL = decltype(tl)::value;
-        const char* base = vh + (int64_t)j * C * svb;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          cr_set4(cr, 4 * mt, ld16(base, row_off<TAIL>(16 * mt + n, j * C, T, svb, cvb)));
-      });
-    };
-    for (int it = -8; it < nch; ++it) {
-      const int j = it + 2;
-      if (j >= 0 && j < nch) {
-        const f16x8 vf0 = to_f16x8<TIn>(cr_get4(cr, 0));
-        const f16x8 vf1 = to_f16x8<TIn>(cr_get4(cr, 4));
-#pragma unroll
-        for (int c = 0; c < BV / 16; ++c) {
-          const f16x8 id = (c & 1) ? id1 : id0;
-          s.vt[j % NVT][c][lane] = M::from_acc(M::mma(vf0, id, z4), M::mma(vf1, id, z4));
-        }
-      }
-      if (j + 1 >= 0 && j + 1 < nch) load_v(j + 1);
-      const int jw = it + 1;
-      if (jw >= 0 && jw < nch) {
-#pragma unroll
-        for (int c = 0; c < KT; ++c) {
-          const f16x8 pm = (c & 1) ? pm1 : pm0;
-          const int kb = c >> 1;
-          s.kt[jw % NKT][c][lane] = M::from_acc(M::mma(staged(s.rk[jw % NRK], n, 4 * kb + gq), pm, z4),
-                                                M::mma(staged(s.rk[jw % NRK], 16 + n, 4 * kb + gq), pm, z4));
-        }
-      }
-      __syncthreads();
-    }
   } else if (role == R_E) {
     // ================================================================ E
-    // chunk it+8 (E_e owns chunks = e mod 2): gates, A = beta_t e^{b_t-b_j} K K^T
+    // chunk it+10 (E_e owns chunks = e mod 2): gates, A = beta_t e^{b_t-b_j} K K^T
     const int e = ridx;
     constexpr int GW = 8 * KB;
     uint32_t cr[8 * KB + 2];
@@ -638,8 +661,8 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       });
     };
     if (e < nch) e_load(e);
-    for (int it = -8; it < nch; ++it) {
-      const int j = it + 8;
+    for (int it = IT0; it < nch; ++it) {
+      const int j = it + 10;
       if (j >= 0 && j < nch && (j & 1) == e) {
         const int as = j % NA;
         const float b = scan32(gate_at(j, cr[GW], p.g_dtype));
@@ -682,31 +705,37 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     }
   } else if (role == R_S) {
     // ================================================================ S
-    // pair m = (2m, 2m+1) in iterations 2m-6 .. 2m-3 (S_{m%2}; lanes 0-31
-    // chunk 2m, 32-63 chunk 2m+1); m' = m + 8 keeps the arithmetic
-    // non-negative
+    // lanes 0-31 solve chunk 2m, lanes 32-63 chunk 2m+1 of pair m
     const int sidx = ridx;
     const int h = lane >> 5, c = lane & 31;
     float xc[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) xc[i] = 0.f;
-    for (int it = -8; it < nch; ++it) {
-      const int itp = it + 16;
-      int mp = (itp + 4) >> 1;
-      if ((mp & 1) != sidx) ++mp;
-      const int seg = itp + 6 - 2 * mp;  // 0..3
-      const int j = 2 * (mp - 8) + h;
+    for (int it = IT0; it < nch; ++it) {
+      // pair m = (2m, 2m+1) is solved by S_{m mod 3} in iterations
+      // 2m-8 .. 2m-3 (segment it - (2m - 8)); mp = m + 12 keeps the
+      // arithmetic non-negative
+      const int itp = it + 24;
+      const int mpl = (itp + 4) >> 1;
+      const int rr = (mpl - sidx) % 3;
+      const int mp = rr == 0 ? mpl : mpl + 3 - rr;
+      const int seg = itp + 8 - 2 * mp;  // 0..5
+      const int j = 2 * (mp - 12) + h;
       const bool valid = j >= 0 && j < nch;
       const float* at = s.a[valid ? j % NA : 0];
-      // rows 31..16, 15..9, 8..4, 3..0: about 120 FMAs per lane each
+      // rows 31..19, 18..13, 12..9, 8..6, 5..3, 2..0: 72 to 93 FMAs each
       if (seg == 0) {
-        solve_rows<16, 32>(at, c, xc);
+        solve_rows<19, 32>(at, c, xc);
       } else if (seg == 1) {
-        solve_rows<9, 16>(at, c, xc);
+        solve_rows<13, 19>(at, c, xc);
       } else if (seg == 2) {
-        solve_rows<4, 9>(at, c, xc);
+        solve_rows<9, 13>(at, c, xc);
+      } else if (seg == 3) {
+        solve_rows1<6, 9>(at, c, xc);
+      } else if (seg == 4) {
+        solve_rows1<3, 6>(at, c, xc);
       } else {
-        solve_rows<0, 4>(at, c, xc);
+        solve_rows1<0, 3>(at, c, xc);
         if (valid) {
           // lane c holds row c of T: row t = c of the Tu / Tw operand tile
           // c / 16, 8 values per lane group g
@@ -735,46 +764,76 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     }
   } else if (role == R_LOAD) {
     // ============================================================= LOAD
-    // Loader e owns chunks of parity e: in iteration it (it+3 = e mod 2) it
-    // stages chunk it+3 from its registers and loads chunk it+5 into them.
-    // Each load covers 4 rows x 256 bytes (whole 128-byte lines).
+    // Loader 0 handles q rows and g, loader 1 k rows and the v slice: in
+    // iteration it each stages chunk it+3 from its registers and loads chunk
+    // it+4 into them.  q and k loads cover 4 rows x 256 bytes (whole 128-byte
+    // lines).
     constexpr int RCH = K / 8, NI = C * RCH / 64;
-    constexpr int KW = 4 * NI, GW = 8 * NI;
-    uint32_t cr[8 * NI + 1];
-    auto ld = [&](int j) {
-      with_tail(j, [&](auto tl) {
-        constexpr bool TAIL = decltype(tl)::value;
-        cr[GW] = ld_gate(gh + (int64_t)j * C * sgb, row_off<TAIL>(lane & 31, j * C, T, sgb, 0), geb);
-        const char* bq = qh + (int64_t)j * C * sqb;
-        const char* bk = kh + (int64_t)j * C * skb;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const int e = 64 * i + lane, r = e / RCH, c = e % RCH;
-          cr_set4(cr, 4 * i, ld16(bq, row_off<TAIL>(r, j * C, T, sqb, 8 * c * EB)));
-          cr_set4(cr, KW + 4 * i, ld16(bk, row_off<TAIL>(r, j * C, T, skb, 8 * c * EB)));
-        }
-      });
-    };
-    auto stage = [&](int j) {
+    constexpr int VCH = BV / 8, NIV = C * VCH / 64;
+    // rows q / k of chunk j into cr[0 .. 4 NI)
+    auto ld_rows = [&](uint32_t* cr, const char* head, uint32_t strb, auto tl, int j) {
+      constexpr bool TAIL = decltype(tl)::value;
+      const char* base = head + (int64_t)j * C * strb;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int e = 64 * i + lane, r = e / RCH, c = e % RCH;
-        s.rq[j % NRQ][r][swz<K>(r, c)] = to_f16x8<TIn>(cr_get4(cr, 4 * i));
-        s.rk[j % NRK][r][swz<K>(r, c)] = to_f16x8<TIn>(cr_get4(cr, KW + 4 * i));
+        cr_set4(cr, 4 * i, ld16(base, row_off<TAIL>(r, j * C, T, strb, 8 * c * EB)));
       }
-      if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[GW], p.g_dtype);
     };
-    const int e = ridx;
-    for (int it = -8; it < nch; ++it) {
-      const int j = it + 3;
-      if ((j & 1) == e) {
-        if (j >= 0 && j < nch) stage(j);
-        if (j + 2 >= 0 && j + 2 < nch) ld(j + 2);
+    auto st_rows = [&](const uint32_t* cr, f16x8 (*tile)[K / 8]) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int e = 64 * i + lane, r = e / RCH, c = e % RCH;
+        tile[r][swz<K>(r, c)] = to_f16x8<TIn>(cr_get4(cr, 4 * i));
       }
-      __syncthreads();
+    };
+    if (ridx == 0) {
+      uint32_t cr[4 * NI + 1];
+      for (int it = IT0; it < nch; ++it) {
+        const int j = it + 3;
+        if (j >= 0 && j < nch) {
+          st_rows(cr, s.rq[j % NRQ]);
+          if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[4 * NI], p.g_dtype);
+        }
+        if (j + 1 >= 0 && j + 1 < nch) {
+          with_tail(j + 1, [&](auto tl) {
+            constexpr bool TAIL = decltype(tl)::value;
+            ld_rows(cr, qh, sqb, tl, j + 1);
+            cr[4 * NI] = ld_gate(gh + (int64_t)(j + 1) * C * sgb,
+                                 row_off<TAIL>(lane & 31, (j + 1) * C, T, sgb, 0), geb);
+          });
+        }
+        __syncthreads();
+      }
+    } else {
+      uint32_t cr[4 * NI + 4 * NIV];
+      for (int it = IT0; it < nch; ++it) {
+        const int j = it + 3;
+        if (j >= 0 && j < nch) {
+          st_rows(cr, s.rk[j % NRK]);
+#pragma unroll
+          for (int i = 0; i < NIV; ++i) {
+            const int e = 64 * i + lane, r = e / VCH, c = e % VCH;
+            s.rv[j % NRV][r][c] = to_f16x8<TIn>(cr_get4(cr, 4 * NI + 4 * i));
+          }
+        }
+        if (j + 1 >= 0 && j + 1 < nch) {
+          with_tail(j + 1, [&](auto tl) {
+            constexpr bool TAIL = decltype(tl)::value;
+            ld_rows(cr, kh, skb, tl, j + 1);
+            const char* bv = vh + (int64_t)(j + 1) * C * svb;
+#pragma unroll
+            for (int i = 0; i < NIV; ++i) {
+              const int e = 64 * i + lane, r = e / VCH, c = e % VCH;
+              cr_set4(cr, 4 * NI + 4 * i, ld16(bv, row_off<TAIL>(r, (j + 1) * C, T, svb, 8 * c * EB)));
+            }
+          });
+        }
+        __syncthreads();
+      }
     }
   } else {
-    for (int it = -8; it < nch; ++it) __syncthreads();
+    for (int it = IT0; it < nch; ++it) __syncthreads();
   }
 }
 

@@ -101,24 +101,51 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
 
 _KERNELS = {"auto": 0, "phased": _lib.FLAG_PHASED_KERNEL}
 
+# Launch plans keyed by everything but the data pointers: shapes, strides,
+# dtypes, devices and options.  A call whose signature was seen before skips
+# the Python validation (it passed for that signature) and copies a
+# prefilled parameter block, so the host cost per launch stays small next
+# to the kernel.
+_PLANS = {}
+_PLANS_MAX = 256
 
-def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v, kernel="auto"):
-    lib = _lib.load_library()
-    B, T, H, K = q.shape
-    V = v.shape[-1]
+
+class _Plan:
+    __slots__ = ("shape_o", "shape_fs", "out_dtype", "fs_vk", "params")
+
+
+def _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
+    hs = None if h0 is None else (h0.shape, h0.stride(), h0.dtype, h0.device)
+    return (q.shape, q.stride(), q.dtype, q.device, k.shape, k.stride(), k.dtype, k.device,
+            v.shape, v.stride(), v.dtype, v.device, g.shape, g.stride(), g.dtype, g.device,
+            beta.shape, beta.stride(), beta.dtype, beta.device, hs, float(scale), chunk_size,
+            block_v, output_dtype, kernel, fs_vk)
+
+
+def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
+    B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v)
+    if kernel not in _KERNELS:
+        raise ValueError(f"kernel={kernel!r} must be one of {sorted(_KERNELS)}")
+    out_dtype = q.dtype if output_dtype is None else output_dtype
+    if out_dtype not in _DTYPE_CODE:
+        raise ValueError(f"output_dtype {out_dtype} not supported")
+    plan = _Plan()
+    plan.shape_o = (B, T, H, V)
+    plan.shape_fs = (B, H, V, K) if fs_vk else (B, H, K, V)
+    plan.out_dtype = out_dtype
+    plan.fs_vk = fs_vk
     P = _lib.GdnFwdParams()
-    P.q, P.k, P.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
-    P.g, P.beta = g.data_ptr(), beta.data_ptr()
-    P.h0 = h0.data_ptr() if h0 is not None else None
-    P.o, P.final_state = o.data_ptr(), fs.data_ptr()
     P.q_stride[:] = q.stride()[:3]
     P.k_stride[:] = k.stride()[:3]
     P.v_stride[:] = v.stride()[:3]
     P.g_stride[:] = g.stride()
     P.beta_stride[:] = beta.stride()
-    P.o_stride[:] = o.stride()[:3]
+    P.o_stride[:] = (T * H * V, H * V, V)          # o is allocated contiguous
     P.h0_stride[:] = h0.stride() if h0 is not None else (0, 0, 0, 0)
-    P.fs_stride[:] = fs_stride
+    if fs_vk:   # [B, H, V, K] tensor written through (b, h, k, v) strides
+        P.fs_stride[:] = (H * V * K, V * K, 1, K)
+    else:
+        P.fs_stride[:] = (H * K * V, K * V, V, 1)
     P.B, P.T, P.H, P.K, P.V = B, T, H, K, V
     P.scale = float(scale)
     P.chunk_size = int(chunk_size)
@@ -126,13 +153,47 @@ def _launch(q, k, v, g, beta, h0, o, fs, fs_stride, scale, chunk_size, block_v, 
     P.qkv_dtype = _DTYPE_CODE[q.dtype]
     P.g_dtype = _DTYPE_CODE[g.dtype]
     P.beta_dtype = _DTYPE_CODE[beta.dtype]
-    P.o_dtype = _DTYPE_CODE[o.dtype]
+    P.o_dtype = _DTYPE_CODE[out_dtype]
     P.flags = _KERNELS[kernel]
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        status = lib.gdn_fwd_launch(ctypes.byref(P), ctypes.c_void_p(stream))
+    plan.params = bytes(P)
+    return plan
+
+
+def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
+    try:
+        key = _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
+                         kernel, fs_vk)
+        plan = _PLANS.get(key)
+    except (AttributeError, TypeError):   # not tensors: _validate says which
+        key, plan = None, None
+    if plan is None:
+        plan = _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
+                          kernel, fs_vk)
+        if key is not None:
+            if len(_PLANS) >= _PLANS_MAX:
+                _PLANS.clear()
+            _PLANS[key] = plan
+    dev = q.device
+    qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    if plan.shape_o[1] > 0 and (qp | kp | vp) & 15:
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            _check_rows(t, name)
+    o = torch.empty(plan.shape_o, dtype=plan.out_dtype, device=dev)
+    fs = torch.empty(plan.shape_fs, dtype=torch.float32, device=dev)
+    P = _lib.GdnFwdParams.from_buffer_copy(plan.params)
+    P.q, P.k, P.v = qp, kp, vp
+    P.g, P.beta = g.data_ptr(), beta.data_ptr()
+    P.h0 = h0.data_ptr() if h0 is not None else None
+    P.o, P.final_state = o.data_ptr(), fs.data_ptr()
+    lib = _lib.load_library()
+    if dev.index == torch.cuda.current_device():
+        status = lib.gdn_fwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
+    else:
+        with torch.cuda.device(dev):
+            status = lib.gdn_fwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
     if status != 0:
         raise RuntimeError(f"gdn_fwd_launch failed ({status}): {_lib.status_string(status)}")
+    return o, fs
 
 
 def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
@@ -164,16 +225,7 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     Semantics are the reference's (gdn_ref.py:3-9): per step
     ``S = e^{g} S; u = beta (v - S^T k); S += k u^T; o = scale S^T q``.
     """
-    B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v)
-    if kernel not in _KERNELS:
-        raise ValueError(f"kernel={kernel!r} must be one of {sorted(_KERNELS)}")
-    out_dtype = q.dtype if output_dtype is None else output_dtype
-    if out_dtype not in _DTYPE_CODE:
-        raise ValueError(f"output_dtype {out_dtype} not supported")
-    o = torch.empty(B, T, H, V, dtype=out_dtype, device=q.device)
-    fs = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    _launch(q, k, v, g, beta, h0, o, fs, fs.stride(), scale, chunk_size, block_v, kernel)
-    return o, fs
+    return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False)
 
 
 def gdn_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
@@ -186,13 +238,7 @@ def gdn_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch
     Any T is accepted: the trailing partial chunk is masked in-kernel, which
     equals the reference's zero padding (gdn_triton.py:121-125).
     """
-    B, T, H, K, V = _validate(q, k, v, g, beta, None, 32, None)
-    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
-    hf = torch.empty(B, H, V, K, dtype=torch.float32, device=q.device)
-    # Write the K x V state straight into the V x K tensor: (b, h, k, v) strides.
-    fs_stride = (hf.stride(0), hf.stride(1), hf.stride(3), hf.stride(2))
-    _launch(q, k, v, g, beta, None, o, hf, fs_stride, 1.0, 32, None)
-    return o, hf
+    return _run(q, k, v, g, beta, None, 1.0, 32, None, None, "auto", True)
 
 
 def auto_block_v(B: int, H: int, K: int, V: int, chunk_size: int = 32,
