@@ -11,10 +11,11 @@
 // `it` while the other roles work ahead:
 //
 //   role      chunk   work
-//   LOAD0     it+4    q rows and g into registers (whole 128-byte lines)
-//             it+3    those into the staged LDS rings (fp16, swizzled
+//   LOAD0     it+4    q rows, the workgroup's v slice and g into registers
+//                     (q in whole 128-byte lines)
+//             it+3    those into the staged LDS rings (fp16; q in swizzled
 //                     16-byte pieces; g as float, zero past T)
-//   LOAD1     it+4/3  the same for k rows and the workgroup's v slice
+//   LOAD1     it+4/3  the same for k rows
 //   E0/E1     it+10   gates, A = beta_t e^{b_t-b_j} K K^T (t > j) stored as
 //                     A^T (E_e owns chunks of parity e; own k loads)
 //   S0/S1/S2  pairs   X = T^T = (I + A^T)^{-1} by substitution, last row
@@ -764,7 +765,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
     }
   } else if (role == R_LOAD) {
     // ============================================================= LOAD
-    // Loader 0 handles q rows and g, loader 1 k rows and the v slice: in
+    // Loader 0 handles q rows, the v slice and g, loader 1 k rows: in
     // iteration it each stages chunk it+3 from its registers and loads chunk
     // it+4 into them.  q and k loads cover 4 rows x 256 bytes (whole 128-byte
     // lines).
@@ -788,46 +789,41 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
       }
     };
     if (ridx == 0) {
-      uint32_t cr[4 * NI + 1];
+      uint32_t cr[4 * NI + 4 * NIV + 1];
       for (int it = IT0; it < nch; ++it) {
         const int j = it + 3;
         if (j >= 0 && j < nch) {
           st_rows(cr, s.rq[j % NRQ]);
-          if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[4 * NI], p.g_dtype);
-        }
-        if (j + 1 >= 0 && j + 1 < nch) {
-          with_tail(j + 1, [&](auto tl) {
-            constexpr bool TAIL = decltype(tl)::value;
-            ld_rows(cr, qh, sqb, tl, j + 1);
-            cr[4 * NI] = ld_gate(gh + (int64_t)(j + 1) * C * sgb,
-                                 row_off<TAIL>(lane & 31, (j + 1) * C, T, sgb, 0), geb);
-          });
-        }
-        __syncthreads();
-      }
-    } else {
-      uint32_t cr[4 * NI + 4 * NIV];
-      for (int it = IT0; it < nch; ++it) {
-        const int j = it + 3;
-        if (j >= 0 && j < nch) {
-          st_rows(cr, s.rk[j % NRK]);
 #pragma unroll
           for (int i = 0; i < NIV; ++i) {
             const int e = 64 * i + lane, r = e / VCH, c = e % VCH;
             s.rv[j % NRV][r][c] = to_f16x8<TIn>(cr_get4(cr, 4 * NI + 4 * i));
           }
+          if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[4 * NI + 4 * NIV], p.g_dtype);
         }
         if (j + 1 >= 0 && j + 1 < nch) {
           with_tail(j + 1, [&](auto tl) {
             constexpr bool TAIL = decltype(tl)::value;
-            ld_rows(cr, kh, skb, tl, j + 1);
+            ld_rows(cr, qh, sqb, tl, j + 1);
             const char* bv = vh + (int64_t)(j + 1) * C * svb;
 #pragma unroll
             for (int i = 0; i < NIV; ++i) {
               const int e = 64 * i + lane, r = e / VCH, c = e % VCH;
               cr_set4(cr, 4 * NI + 4 * i, ld16(bv, row_off<TAIL>(r, (j + 1) * C, T, svb, 8 * c * EB)));
             }
+            cr[4 * NI + 4 * NIV] = ld_gate(gh + (int64_t)(j + 1) * C * sgb,
+                                           row_off<TAIL>(lane & 31, (j + 1) * C, T, sgb, 0), geb);
           });
+        }
+        __syncthreads();
+      }
+    } else {
+      uint32_t cr[4 * NI];
+      for (int it = IT0; it < nch; ++it) {
+        const int j = it + 3;
+        if (j >= 0 && j < nch) st_rows(cr, s.rk[j % NRK]);
+        if (j + 1 >= 0 && j + 1 < nch) {
+          with_tail(j + 1, [&](auto tl) { ld_rows(cr, kh, skb, tl, j + 1); });
         }
         __syncthreads();
       }
