@@ -29,6 +29,13 @@
  *   - h0 may be NULL (zero initial state).
  *   - T may be any value >= 0; a trailing partial chunk is masked in-kernel
  *     (equivalent to the reference's zero padding, gdn_ref.py:102-114).
+ *   - cu_seqlens (optional, the variable-length form of FLA's
+ *     chunk_gated_delta_rule, called at bench_gdn.py:169-172): B sequences
+ *     packed along t of one batch.  Sequence i is rows
+ *     [cu_seqlens[i], cu_seqlens[i+1]) of batch 0 of every [B,T,H,*] tensor
+ *     (their b stride is unused), with its own h0[i] / final_state[i]; T is
+ *     the packed length.  The offsets live in device memory and are not read
+ *     on the host; each kernel clamps them to [0, T].
  */
 #ifndef GDN_MI355X_H
 #define GDN_MI355X_H
@@ -39,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GDN_MI355X_ABI_VERSION 2
+#define GDN_MI355X_ABI_VERSION 3
 
 /* Element types of the tensors crossing the boundary. */
 enum GdnDtype {
@@ -97,6 +104,8 @@ typedef struct GdnFwdParams {
   int32_t beta_dtype;       /* GdnDtype of beta */
   int32_t o_dtype;          /* GdnDtype of o */
   int32_t flags;            /* GdnFlags; 0 = default */
+  /* nullable: B + 1 int64 row offsets of packed sequences (device memory) */
+  const int64_t* cu_seqlens;
 } GdnFwdParams;
 
 /* Enqueue one fused chunked GDN forward on `stream` (a hipStream_t; NULL =
@@ -109,6 +118,50 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  * whose autotuner picks BV at run time (gdn_triton.py:18-28). */
 int gdn_fwd_auto_block_v(int B, int H, int K, int V, int chunk_size,
                          int qkv_dtype);
+
+/* Fused input preparation, the step before the path: one launch that
+ * L2-normalises q and k rows and applies the gate activations of the
+ * benchmark's input recipe.  Replaces the reference's _l2norm
+ * (gdn_ref.py:24-25: x / sqrt(sum x^2 + eps), the sum in fp32, the
+ * denominator rounded to x's dtype before the division; called by
+ * bench_gdn.py:35-36) and the beta / g activations of the input recipe
+ * (beta = sigmoid(x), g = logsigmoid(x)).
+ *   - Each input may be NULL (that output is skipped); an output may alias
+ *     its input (in-place).
+ *   - q/k in and out: [B,T,H,K], qk_dtype, innermost dim contiguous, 16-byte
+ *     aligned rows; K in {32, 64, 128, 256}.
+ *   - gates: [B,T,H], any strides, each with its own in / out dtype.
+ *   - B * T * H < 2^31.  Same launch contract as gdn_fwd_launch. */
+typedef struct GdnPrepParams {
+  const void* q_in;
+  void* q_out;
+  const void* k_in;
+  void* k_out;
+  const void* beta_in;      /* beta_out = sigmoid(beta_in) */
+  void* beta_out;
+  const void* g_in;         /* g_out = logsigmoid(g_in) */
+  void* g_out;
+  /* strides in elements, (b, t, h) */
+  int64_t q_in_stride[3];
+  int64_t q_out_stride[3];
+  int64_t k_in_stride[3];
+  int64_t k_out_stride[3];
+  int64_t beta_in_stride[3];
+  int64_t beta_out_stride[3];
+  int64_t g_in_stride[3];
+  int64_t g_out_stride[3];
+  int32_t B, T, H, K;
+  int32_t qk_dtype;         /* GdnDtype of q, k (in and out) */
+  int32_t beta_in_dtype;
+  int32_t beta_out_dtype;
+  int32_t g_in_dtype;
+  int32_t g_out_dtype;
+  float eps;                /* 1e-6 in the reference */
+} GdnPrepParams;
+
+/* Enqueue the input preparation on `stream`; returns a GdnStatus /
+ * hipError_t value. */
+int gdn_prep_launch(const GdnPrepParams* params, void* stream);
 
 /* Human-readable text for a status code. */
 const char* gdn_fwd_status_string(int status);

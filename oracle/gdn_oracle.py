@@ -9,6 +9,9 @@ It restates, in plain PyTorch on the CPU, the semantics of the reference's
 ``gdn_ref.py``:
 
 * ``l2norm``          -- gdn_ref.py:24-25
+* ``sigmoid``, ``logsigmoid``, ``prep_inputs`` -- the gate activations of
+                         the BASELINE.json input recipe and the fused input
+                         preparation built on them (fp64, textbook forms)
 * ``recurrent``       -- gdn_ref.py:28-45  (the definition, gdn_ref.py:3-9)
 * ``chunked_ut``      -- gdn_ref.py:48-99  (the chunked UT transform; same op
                          order, including the two unit-triangular solves and
@@ -43,7 +46,7 @@ from typing import Optional, Tuple
 import torch
 
 __all__ = [
-    "l2norm", "recurrent", "chunked_ut", "pad_to_multiple", "rel_err",
+    "l2norm", "sigmoid", "logsigmoid", "prep_inputs", "recurrent", "chunked_ut", "pad_to_multiple", "rel_err",
     "make_inputs_reference", "make_inputs_baseline", "to_kv", "to_vk",
     "BaselineConfig", "BASELINE_CONFIGS", "algorithmic_bytes",
     "algorithmic_flops",
@@ -62,6 +65,28 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """
     denom = torch.sqrt(x.float().pow(2).sum(-1, keepdim=True) + eps)
     return x / denom.to(x.dtype)
+
+
+def sigmoid(x: torch.Tensor) -> torch.Tensor:
+    """``1 / (1 + e^{-x})`` in fp64 (beta of the BASELINE input recipe)."""
+    return 1.0 / (1.0 + torch.exp(-x.double()))
+
+
+def logsigmoid(x: torch.Tensor) -> torch.Tensor:
+    """``log(sigmoid(x))`` in fp64, as ``min(x, 0) - log1p(e^{-|x|})`` (finite
+    for every x; g of the BASELINE input recipe)."""
+    x = x.double()
+    return torch.clamp(x, max=0.0) - torch.log1p(torch.exp(-x.abs()))
+
+
+def prep_inputs(q=None, k=None, beta=None, g=None, eps: float = 1e-6,
+                gate_dtype=torch.float32):
+    """The fused input preparation: ``l2norm`` of q and k (in their dtype),
+    ``sigmoid(beta)`` and ``logsigmoid(g)`` cast to ``gate_dtype``.  Any
+    argument may be None."""
+    return (None if q is None else l2norm(q, eps), None if k is None else l2norm(k, eps),
+            None if beta is None else sigmoid(beta).to(gate_dtype),
+            None if g is None else logsigmoid(g).to(gate_dtype))
 
 
 def recurrent(q, k, v, beta, g, initial_state=None, dtype=torch.float64):

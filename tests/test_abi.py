@@ -51,18 +51,20 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_fwd_abi_version() == 2
+    assert lib.gdn_fwd_abi_version() == 3
 
 
-def test_struct_layout_matches_header(tmp_path):
+@pytest.mark.parametrize("struct", ["GdnFwdParams", "GdnPrepParams"])
+def test_struct_layout_matches_header(tmp_path, struct):
     """Compile a probe against the header with gcc and compare offsets."""
     from importlib import import_module
     L = import_module("v100-attention-lab_amd._lib")
-    fields = [f for f, _ in L.GdnFwdParams._fields_]
+    S = getattr(L, struct)
+    fields = [f for f, _ in S._fields_]
     src = tmp_path / "layout.c"
-    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(GdnFwdParams, {f}));' for f in fields)
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof({struct}, {f}));' for f in fields)
     src.write_text(f"#include <stddef.h>\n#include <stdio.h>\n#include \"gdn_mi355x.h\"\n"
-                   f"int main(void) {{\n{body}\n  printf(\"sizeof %zu\\n\", sizeof(GdnFwdParams));\n"
+                   f"int main(void) {{\n{body}\n  printf(\"sizeof %zu\\n\", sizeof({struct}));\n"
                    f"  return 0;\n}}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{os.path.dirname(HEADER)}", str(src),
@@ -70,8 +72,8 @@ def test_struct_layout_matches_header(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
     c_layout = dict(zip(out[0::2], map(int, out[1::2])))
     for f in fields:
-        assert getattr(L.GdnFwdParams, f).offset == c_layout[f], f
-    assert ctypes.sizeof(L.GdnFwdParams) == c_layout["sizeof"]
+        assert getattr(S, f).offset == c_layout[f], f
+    assert ctypes.sizeof(S) == c_layout["sizeof"]
 
 
 def _params(L, **kw):
@@ -189,3 +191,95 @@ def test_missing_library_raises_importerror(tmp_path):
             L.load_library(str(tmp_path / "nope.so"))
     finally:
         L._lib = saved
+
+
+# --------------------------------------------------------------------------
+# input preparation entry point: argument errors before any launch
+# --------------------------------------------------------------------------
+
+def _prep_params(L, **kw):
+    P = L.GdnPrepParams()
+    fake = 0x1000  # never dereferenced: every case below returns before a launch
+    P.q_in = P.q_out = P.k_in = P.k_out = fake
+    P.beta_in = P.beta_out = P.g_in = P.g_out = fake
+    for name in ("q_in", "q_out", "k_in", "k_out"):
+        getattr(P, name + "_stride")[:] = (4096 * 16 * 128, 16 * 128, 128)
+    for name in ("beta_in", "beta_out", "g_in", "g_out"):
+        getattr(P, name + "_stride")[:] = (4096 * 16, 16, 1)
+    P.B, P.T, P.H, P.K = 2, 4096, 16, 128
+    P.qk_dtype = 1
+    P.eps = 1e-6
+    for k_, v_ in kw.items():
+        setattr(P, k_, v_)
+    return P
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), 1002), (dict(T=1 << 20, H=4096), 1002), (dict(K=96), 1003),
+    (dict(qk_dtype=9), 1005), (dict(g_out_dtype=3), 1005), (dict(q_out=None), 1001),
+    (dict(beta_out=None), 1001), (dict(k_in=0x1004), 1004),
+])
+def test_prep_rejects_bad_arguments(lib, kw, code):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    P = _prep_params(L, **kw)
+    assert lib.gdn_prep_launch(ctypes.byref(P), None) == code
+    assert lib.gdn_prep_launch(None, None) == 1001
+
+
+def test_prep_misaligned_stride_and_empty(lib):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    P = _prep_params(L)
+    P.q_out_stride[2] = 129
+    assert lib.gdn_prep_launch(ctypes.byref(P), None) == 1004
+    # nothing to do: success without touching the device
+    assert lib.gdn_prep_launch(ctypes.byref(_prep_params(L, T=0)), None) == 0
+
+
+# --------------------------------------------------------------------------
+# FLA surface, varlen and prep: host-side validation
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cu,msg", [
+    (torch.tensor([0, 10, 64]), None),
+    (torch.tensor([0, 10, 64], dtype=torch.int32), None),
+    (torch.tensor([1, 10, 64]), "rise from 0"),
+    (torch.tensor([0, 30, 20, 64]), "rise from 0"),
+    (torch.tensor([0, 10, 63]), "rise from 0"),
+    (torch.tensor([0]), "N \\+ 1"),
+    (torch.tensor([[0, 64]]), "N \\+ 1"),
+    (torch.tensor([0.0, 64.0]), "int64 or int32"),
+])
+def test_cu_seqlens_validation(pkg, cu, msg):
+    from importlib import import_module
+    ops = import_module("v100-attention-lab_amd.ops")
+    if msg is None:
+        c, n = ops._check_cu_seqlens(cu, 64, torch.device("cpu"))
+        assert c.dtype == torch.int64 and n == len(cu) - 1
+    else:
+        with pytest.raises(ValueError, match=msg):
+            ops._check_cu_seqlens(cu, 64, torch.device("cpu"))
+
+
+def test_varlen_needs_one_packed_batch(pkg):
+    q, k, v, g, b = _cpu_inputs(B=2)
+    with pytest.raises(ValueError, match="B must be 1"):
+        pkg.gdn_fwd(q, k, v, g, b, cu_seqlens=torch.tensor([0, 30, 64]))
+    q, k, v, g, b = _cpu_inputs(B=1)
+    with pytest.raises(ValueError, match="h0 must be \\[N"):
+        pkg.gdn_fwd(q, k, v, g, b, torch.zeros(1, 2, 64, 32), cu_seqlens=torch.tensor([0, 30, 64]))
+
+
+def test_fla_surface_and_prep_reject_cpu_tensors(pkg):
+    q, k, v, g, b = _cpu_inputs()
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.chunk_gated_delta_rule(q=q, k=k, v=v, g=g, beta=b, scale=1.0)
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.gdn_prep(q=q, k=k, beta=b, g=g)
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.l2norm(q)
+    with pytest.raises(ValueError, match="head_first"):
+        pkg.chunk_gated_delta_rule(q, k, v, g[..., None], b, head_first=True)
+    with pytest.raises(ValueError, match="K=96"):
+        pkg.gdn_prep(q=torch.zeros(1, 4, 2, 96))

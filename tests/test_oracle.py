@@ -304,3 +304,81 @@ def test_roofline_arithmetic_matches_baseline_md():
     assert ref.algorithmic_flops(1, 1, 1, 128, 128, 64) == 147456
     assert ref.algorithmic_bytes(4, 4096, 16, 128, 128, 2, with_h0=True) / 1e6 == \
         pytest.approx(278.9, abs=0.1)
+
+
+# --------------------------------------------------------------------------
+# input preparation: l2norm (gdn_ref.py:24-25) and the gate activations
+# --------------------------------------------------------------------------
+
+def test_l2norm_closed_form_norm():
+    """|l2norm(x)| = |x| / sqrt(|x|^2 + eps) (eps inside the sqrt), to fp32
+    accuracy: the reference squares and sums in fp32 (``x.float()``) whatever
+    x's dtype."""
+    x = torch.randn(3, 5, 2, 64, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    ss = (x * x).sum(-1)
+    y = ref.l2norm(x)
+    assert torch.allclose(y.norm(dim=-1), ss.sqrt() / (ss + 1e-6).sqrt(), rtol=1e-6, atol=0)
+    xs = x * 1e-4   # |x|^2 ~ 6e-7, comparable to eps
+    ss = (xs * xs).sum(-1)
+    assert torch.allclose(ref.l2norm(xs).norm(dim=-1), ss.sqrt() / (ss + 1e-6).sqrt(),
+                          rtol=1e-6, atol=0)
+
+
+def test_l2norm_eps_inside_sqrt_and_zero_rows():
+    """A row with |x|^2 = eps is halved in norm by sqrt(2) (eps under the root,
+    not added to the root); an all-zero row stays zero (no NaN)."""
+    x = torch.zeros(1, 1, 2, 32, dtype=torch.float64)
+    x[0, 0, 0, 0] = 1e-3
+    y = ref.l2norm(x)
+    assert abs(y[0, 0, 0, 0].item() - 1e-3 / math.sqrt(2e-6)) < 1e-6   # 0.7071, not 0.999
+    assert torch.equal(y[0, 0, 1], torch.zeros(32, dtype=torch.float64))
+
+
+def test_l2norm_fp16_rounds_the_denominator():
+    """gdn_ref.py:25 casts sqrt(sum + eps) to x.dtype before dividing.  On
+    fp16 rows where that rounding changes the quotient, the oracle matches the
+    rounded-denominator quotient and not the fp32 one (values computed here
+    with numpy's own float16 arithmetic)."""
+    import numpy as np
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(4096, 8, generator=gen).to(torch.float16)
+    y = ref.l2norm(x).numpy()
+    xn = x.numpy().astype(np.float64)
+    den32 = np.sqrt((xn * xn).sum(-1, keepdims=True).astype(np.float32) + np.float32(1e-6))
+    rounded = (x.numpy() / den32.astype(np.float16)).astype(np.float16)
+    unrounded = (xn / den32.astype(np.float64)).astype(np.float16)
+    differ = rounded != unrounded
+    assert differ.sum() > 50
+    assert np.array_equal(y[differ], rounded[differ])
+
+
+def test_sigmoid_logsigmoid_closed_forms():
+    x = torch.tensor([-1000.0, -30.0, -2.5, -1e-8, 0.0, 1e-8, 0.7, 30.0, 1000.0], dtype=torch.float64)
+    s = ref.sigmoid(x)
+    ls = ref.logsigmoid(x)
+    assert s[4].item() == 0.5 and ls[4].item() == -math.log(2.0)
+    assert torch.allclose(s + ref.sigmoid(-x), torch.ones_like(x), rtol=0, atol=1e-15)
+    assert torch.allclose(s, torch.sigmoid(x), rtol=1e-15, atol=0)
+    assert torch.isfinite(ls).all()
+    assert ls[0].item() == -1000.0 and ls[-1].item() == 0.0
+    mid = slice(1, 7)   # where log(sigmoid) is itself accurate
+    assert torch.allclose(ls[mid], torch.log(s[mid]), rtol=1e-14, atol=1e-300)
+    # log sigmoid(x) - log sigmoid(-x) = x
+    assert torch.allclose(ls - ref.logsigmoid(-x), x, rtol=1e-14, atol=1e-12)
+
+
+def test_prep_inputs_matches_baseline_recipe():
+    """The BASELINE recipe draws q, k, v, beta, g and applies l2norm, sigmoid
+    and logsigmoid; prep_inputs on the same raw draws gives the same values."""
+    B, T, H, K, V = 1, 64, 2, 32, 32
+    q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=5, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(5)
+    qr = torch.randn(B, T, H, K, generator=gen)
+    kr = torch.randn(B, T, H, K, generator=gen)
+    torch.randn(B, T, H, V, generator=gen)
+    br = torch.randn(B, T, H, generator=gen)
+    gr = torch.randn(B, T, H, generator=gen)
+    qp, kp, bp, gp = ref.prep_inputs(qr, kr, br, gr)
+    assert torch.equal(qp, q) and torch.equal(kp, k)
+    assert torch.allclose(bp, beta, rtol=2e-7, atol=0)
+    assert torch.allclose(gp, g, rtol=2e-7, atol=1e-7)

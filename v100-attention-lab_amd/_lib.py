@@ -9,7 +9,7 @@ import threading
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libgdn_mi355x.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum GdnDtype
 DTYPE_F32 = 0
@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "gdn_fwd_auto_block_v",
     "gdn_fwd_status_string",
     "gdn_fwd_abi_version",
+    "gdn_prep_launch",
 )
 
 _I64x3 = ctypes.c_int64 * 3
@@ -72,6 +73,40 @@ class GdnFwdParams(ctypes.Structure):
         ("beta_dtype", ctypes.c_int32),
         ("o_dtype", ctypes.c_int32),
         ("flags", ctypes.c_int32),
+        ("cu_seqlens", ctypes.c_void_p),
+    ]
+
+
+class GdnPrepParams(ctypes.Structure):
+    """Mirror of ``GdnPrepParams`` in include/gdn_mi355x.h."""
+
+    _fields_ = [
+        ("q_in", ctypes.c_void_p),
+        ("q_out", ctypes.c_void_p),
+        ("k_in", ctypes.c_void_p),
+        ("k_out", ctypes.c_void_p),
+        ("beta_in", ctypes.c_void_p),
+        ("beta_out", ctypes.c_void_p),
+        ("g_in", ctypes.c_void_p),
+        ("g_out", ctypes.c_void_p),
+        ("q_in_stride", _I64x3),
+        ("q_out_stride", _I64x3),
+        ("k_in_stride", _I64x3),
+        ("k_out_stride", _I64x3),
+        ("beta_in_stride", _I64x3),
+        ("beta_out_stride", _I64x3),
+        ("g_in_stride", _I64x3),
+        ("g_out_stride", _I64x3),
+        ("B", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("K", ctypes.c_int32),
+        ("qk_dtype", ctypes.c_int32),
+        ("beta_in_dtype", ctypes.c_int32),
+        ("beta_out_dtype", ctypes.c_int32),
+        ("g_in_dtype", ctypes.c_int32),
+        ("g_out_dtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
     ]
 
 
@@ -100,6 +135,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         lib.gdn_fwd_auto_block_v.restype = ctypes.c_int
         lib.gdn_fwd_status_string.argtypes = [ctypes.c_int]
         lib.gdn_fwd_status_string.restype = ctypes.c_char_p
+        lib.gdn_prep_launch.argtypes = [ctypes.POINTER(GdnPrepParams), ctypes.c_void_p]
+        lib.gdn_prep_launch.restype = ctypes.c_int
         lib.gdn_fwd_abi_version.argtypes = []
         lib.gdn_fwd_abi_version.restype = ctypes.c_int
         ver = lib.gdn_fwd_abi_version()

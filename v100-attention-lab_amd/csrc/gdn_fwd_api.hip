@@ -109,6 +109,7 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   a.scale = P.scale;
   a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.o_dtype = P.o_dtype;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+  a.cu = P.cu_seqlens;
 
   const int grid = (int)units;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -285,7 +285,32 @@ struct KArgs {
   float scale;
   int g_dtype, beta_dtype, o_dtype;
   int xcd_remap;
+  const int64_t* cu;  // nullable: B + 1 row offsets of packed sequences
 };
+
+// Rows of work unit bi.  Without cu: rows [0, T) of batch bi.  With cu
+// (sequences packed along t of batch 0): rows [cu[bi], cu[bi + 1]) of batch
+// 0, clamped to [0, T] so that malformed offsets never address memory
+// outside the tensors.
+struct RowSpan {
+  int64_t b;   // batch index
+  int64_t t0;  // first row
+  int T;       // number of rows
+};
+
+__device__ __forceinline__ RowSpan row_span(const KArgs& p, int bi) {
+  if (p.cu == nullptr) return RowSpan{bi, 0, p.T};
+  int64_t lo = p.cu[bi], hi = p.cu[bi + 1];
+  lo = lo < 0 ? 0 : (lo > p.T ? p.T : lo);
+  hi = hi < lo ? lo : (hi > p.T ? p.T : hi);
+  return RowSpan{0, lo, (int)(hi - lo)};
+}
+
+// Element offset of the first row of head h in a [B, T, H, *] tensor with
+// (b, t, h) strides s.
+__device__ __forceinline__ int64_t head_base(const RowSpan& r, int h, const int64_t* s) {
+  return r.b * s[0] + r.t0 * s[1] + h * s[2];
+}
 
 // ---------------------------------------------------------------------------
 // the kernel
@@ -322,13 +347,14 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
   const int bi = bh / p.H;
   const int hi = bh % p.H;
   const int v0 = vs * BV;
-  const int T = p.T;
+  const RowSpan rs = row_span(p, bi);
+  const int T = rs.T;
 
-  const TIn* qg = static_cast<const TIn*>(p.q) + bi * p.sq[0] + hi * p.sq[2];
-  const TIn* kg = static_cast<const TIn*>(p.k) + bi * p.sk[0] + hi * p.sk[2];
-  const TIn* vg = static_cast<const TIn*>(p.v) + bi * p.sv[0] + hi * p.sv[2] + v0;
-  const int64_t g_base = bi * p.sg[0] + hi * p.sg[2];
-  const int64_t b_base = bi * p.sb[0] + hi * p.sb[2];
+  const TIn* qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  const int64_t g_base = head_base(rs, hi, p.sg);
+  const int64_t b_base = head_base(rs, hi, p.sb);
 
   // State slice S[:, v0 + 16*wave + n] in D layout: tile r holds rows
   // 16r + 4gq + i.
@@ -529,7 +555,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         utB[cb] = M::from_acc(lo2, hi2);
       }
 
-      const int64_t o_col = bi * p.so[0] + hi * p.so[2] + v0 + vcol;
+      const int64_t o_col = head_base(rs, hi, p.so) + v0 + vcol;
 #pragma unroll
       for (int mt = 0; mt < CT; ++mt) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};

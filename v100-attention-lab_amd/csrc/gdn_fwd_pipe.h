@@ -362,7 +362,8 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   const int bi = bh / p.H;
   const int hi = bh % p.H;
   const int v0 = vs * BV;
-  const int T = p.T;
+  const RowSpan rs = row_span(p, bi);
+  const int T = rs.T;
   const int nch = (T + C - 1) / C;
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
@@ -375,11 +376,11 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   const uint32_t sqb = (uint32_t)p.sq[1] * EB, skb = (uint32_t)p.sk[1] * EB;
   const uint32_t svb = (uint32_t)p.sv[1] * EB;
   const uint32_t sgb = (uint32_t)p.sg[1] * geb, sbb = (uint32_t)p.sb[1] * beb;
-  const char* qh = static_cast<const char*>(p.q) + (bi * p.sq[0] + hi * p.sq[2]) * EB;
-  const char* kh = static_cast<const char*>(p.k) + (bi * p.sk[0] + hi * p.sk[2]) * EB;
-  const char* vh = static_cast<const char*>(p.v) + (bi * p.sv[0] + hi * p.sv[2] + v0) * EB;
-  const char* gh = static_cast<const char*>(p.g) + (bi * p.sg[0] + hi * p.sg[2]) * geb;
-  const char* betah = static_cast<const char*>(p.beta) + (bi * p.sb[0] + hi * p.sb[2]) * beb;
+  const char* qh = static_cast<const char*>(p.q) + head_base(rs, hi, p.sq) * EB;
+  const char* kh = static_cast<const char*>(p.k) + head_base(rs, hi, p.sk) * EB;
+  const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
+  const char* gh = static_cast<const char*>(p.g) + head_base(rs, hi, p.sg) * geb;
+  const char* betah = static_cast<const char*>(p.beta) + head_base(rs, hi, p.sb) * beb;
 
   // f(std::bool_constant<tail>) for chunk j: tail is set only for a last,
   // partial chunk.
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
           pu = M::mma(pA[mt], uh, pu);
           ov[mt] = (pu + ebv[mt] * oq[c2][mt]) * p.scale;
         }
-        const int64_t o_col = bi * p.so[0] + hi * p.so[2] + v0 + 16 * c2 + n;
+        const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2 + n;
         if (p.o_dtype == GDN_DTYPE_F16)
           store_o<f16>(p.o, o_col, p.so[1], j * C, T, gq, ov);
         else if (p.o_dtype == GDN_DTYPE_BF16)

@@ -51,7 +51,9 @@ def _check_rows(t: torch.Tensor, name: str) -> None:
                          f"b/t/h strides {t.stride()[:3]}); call .contiguous()")
 
 
-def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
+def _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq=None):
+    """Checks the call; returns (units B, packed T, H, K, V).  With n_seq
+    (cu_seqlens given) the tensors hold one packed batch of n_seq sequences."""
     for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor")
@@ -66,9 +68,13 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v):
     for name, t in (("g", g), ("beta", beta)):
         if tuple(t.shape) != (B, T, H):
             raise ValueError(f"{name} must be [B, T, H] = ({B}, {T}, {H}), got {tuple(t.shape)}")
+    if n_seq is not None:
+        if B != 1:
+            raise ValueError(f"with cu_seqlens the inputs hold one packed batch: B must be 1, got {B}")
+        B = n_seq
     if h0 is not None:
         if tuple(h0.shape) != (B, H, K, V):
-            raise ValueError(f"h0 must be [B, H, K, V] = ({B}, {H}, {K}, {V}), got {tuple(h0.shape)}")
+            raise ValueError(f"h0 must be [N, H, K, V] = ({B}, {H}, {K}, {V}), got {tuple(h0.shape)}")
         if h0.dtype != torch.float32:
             raise ValueError(f"h0 must be float32, got {h0.dtype}")
     if q.dtype != k.dtype or q.dtype != v.dtype:
@@ -111,36 +117,43 @@ _PLANS_MAX = 256
 
 
 class _Plan:
-    __slots__ = ("shape_o", "shape_fs", "out_dtype", "fs_vk", "params")
+    __slots__ = ("shape_o", "shape_fs", "out_dtype", "fs_vk", "o_hf", "params")
 
 
-def _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
+def _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
+               n_seq, o_hf):
     hs = None if h0 is None else (h0.shape, h0.stride(), h0.dtype, h0.device)
     return (q.shape, q.stride(), q.dtype, q.device, k.shape, k.stride(), k.dtype, k.device,
             v.shape, v.stride(), v.dtype, v.device, g.shape, g.stride(), g.dtype, g.device,
             beta.shape, beta.stride(), beta.dtype, beta.device, hs, float(scale), chunk_size,
-            block_v, output_dtype, kernel, fs_vk)
+            block_v, output_dtype, kernel, fs_vk, n_seq, o_hf)
 
 
-def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
-    B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v)
+def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
+               n_seq, o_hf):
+    B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq)
     if kernel not in _KERNELS:
         raise ValueError(f"kernel={kernel!r} must be one of {sorted(_KERNELS)}")
     out_dtype = q.dtype if output_dtype is None else output_dtype
     if out_dtype not in _DTYPE_CODE:
         raise ValueError(f"output_dtype {out_dtype} not supported")
     plan = _Plan()
-    plan.shape_o = (B, T, H, V)
+    BO = q.shape[0]     # batches of o: 1 when packed
+    plan.shape_o = (BO, H, T, V) if o_hf else (BO, T, H, V)
     plan.shape_fs = (B, H, V, K) if fs_vk else (B, H, K, V)
     plan.out_dtype = out_dtype
     plan.fs_vk = fs_vk
+    plan.o_hf = o_hf
     P = _lib.GdnFwdParams()
     P.q_stride[:] = q.stride()[:3]
     P.k_stride[:] = k.stride()[:3]
     P.v_stride[:] = v.stride()[:3]
     P.g_stride[:] = g.stride()
     P.beta_stride[:] = beta.stride()
-    P.o_stride[:] = (T * H * V, H * V, V)          # o is allocated contiguous
+    if o_hf:    # o allocated contiguous [B, H, T, V], written through (b, t, h) strides
+        P.o_stride[:] = (H * T * V, V, T * V)
+    else:       # o allocated contiguous [B, T, H, V]
+        P.o_stride[:] = (T * H * V, H * V, V)
     P.h0_stride[:] = h0.stride() if h0 is not None else (0, 0, 0, 0)
     if fs_vk:   # [B, H, V, K] tensor written through (b, h, k, v) strides
         P.fs_stride[:] = (H * V * K, V * K, 1, K)
@@ -159,16 +172,40 @@ def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, k
     return plan
 
 
-def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk):
+def _check_cu_seqlens(cu, T, dev):
+    """Validates FLA-style packed-sequence offsets; returns (int64 tensor, N).
+    Reads the offsets on the host (one small copy), as FLA's own varlen
+    preparation does."""
+    if not isinstance(cu, torch.Tensor) or cu.dim() != 1 or cu.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor of N + 1 row offsets (N >= 1)")
+    if cu.dtype not in (torch.int64, torch.int32):
+        raise ValueError(f"cu_seqlens must be int64 or int32, got {cu.dtype}")
+    if cu.device != dev:
+        raise ValueError(f"cu_seqlens must be on {dev}, got {cu.device}")
+    c = cu.tolist()
+    if c[0] != 0 or c[-1] != T or any(b < a for a, b in zip(c, c[1:])):
+        raise ValueError(f"cu_seqlens must rise from 0 to T={T} without decreasing, got {c}")
+    if cu.dtype != torch.int64 or not cu.is_contiguous():
+        cu = cu.to(torch.int64).contiguous()
+    return cu, len(c) - 1
+
+
+def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
+         cu_seqlens=None, o_hf=False):
+    n_seq = None
+    if cu_seqlens is not None:
+        if not isinstance(q, torch.Tensor) or q.dim() != 4:
+            raise ValueError("q, k must be [B, T, H, K] and v [B, T, H, V]")
+        cu_seqlens, n_seq = _check_cu_seqlens(cu_seqlens, q.shape[1], q.device)
     try:
         key = _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
-                         kernel, fs_vk)
+                         kernel, fs_vk, n_seq, o_hf)
         plan = _PLANS.get(key)
     except (AttributeError, TypeError):   # not tensors: _validate says which
         key, plan = None, None
     if plan is None:
         plan = _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
-                          kernel, fs_vk)
+                          kernel, fs_vk, n_seq, o_hf)
         if key is not None:
             if len(_PLANS) >= _PLANS_MAX:
                 _PLANS.clear()
@@ -185,6 +222,7 @@ def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
     P.g, P.beta = g.data_ptr(), beta.data_ptr()
     P.h0 = h0.data_ptr() if h0 is not None else None
     P.o, P.final_state = o.data_ptr(), fs.data_ptr()
+    P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
     lib = _lib.load_library()
     if dev.index == torch.cuda.current_device():
         status = lib.gdn_fwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
@@ -200,7 +238,8 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
             beta: torch.Tensor, h0: Optional[torch.Tensor] = None, scale: float = 1.0,
             chunk_size: int = 32, *, block_v: Optional[int] = None,
             output_dtype: Optional[torch.dtype] = None,
-            kernel: str = "auto") -> Tuple[torch.Tensor, torch.Tensor]:
+            kernel: str = "auto",
+            cu_seqlens: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Fused chunked Gated DeltaNet forward on an MI355X.
 
     Args:
@@ -218,6 +257,10 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
       kernel: ``"auto"`` runs the software-pipelined kernel where it applies
         (fp16/bf16, chunk 32, K in {64, 128}, block_v 16/32) and the
         phase-by-phase kernel elsewhere; ``"phased"`` forces the latter.
+      cu_seqlens: optional int64 ``[N + 1]`` row offsets: N sequences
+        packed along t of a batch of one (B = 1); sequence i is rows
+        ``cu_seqlens[i]:cu_seqlens[i+1]`` with its own ``h0[i]`` and
+        ``final_state[i]`` (h0 and final_state are then ``[N, H, K, V]``).
 
     Returns:
       ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.
@@ -225,7 +268,8 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     Semantics are the reference's (gdn_ref.py:3-9): per step
     ``S = e^{g} S; u = beta (v - S^T k); S += k u^T; o = scale S^T q``.
     """
-    return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False)
+    return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False,
+                cu_seqlens)
 
 
 def gdn_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
@@ -245,3 +289,151 @@ def auto_block_v(B: int, H: int, K: int, V: int, chunk_size: int = 32,
                  dtype: torch.dtype = torch.float16) -> int:
     """The V-slice width the launcher picks for this shape (-1: unsupported)."""
     return _lib.load_library().gdn_fwd_auto_block_v(B, H, K, V, chunk_size, _DTYPE_CODE[dtype])
+
+
+# ---------------------------------------------------------------------------
+# input preparation (the step before the path)
+# ---------------------------------------------------------------------------
+
+def _bth_strides(t: torch.Tensor):
+    return t.stride()[:3]
+
+
+def gdn_prep(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
+             beta: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
+             eps: float = 1e-6, *, out_gate_dtype: torch.dtype = torch.float32,
+             inplace: bool = False):
+    """One fused launch preparing the forward's inputs.
+
+    * ``q, k [B, T, H, K]`` -> ``x / sqrt(sum(x^2) + eps)`` over K, the sum in
+      fp32 and the denominator rounded to x's dtype before the division, as
+      the reference's ``_l2norm`` (gdn_ref.py:24-25);
+    * ``beta [B, T, H]`` (logits) -> ``sigmoid(beta)``;
+    * ``g [B, T, H]`` (logits) -> ``logsigmoid(g)``;
+
+    Any argument may be None (its result is None).  Outputs are new
+    contiguous tensors (q/k in their dtype, gates in ``out_gate_dtype``), or
+    the inputs themselves when ``inplace``.
+    """
+    rows = [t for t in (q, k) if t is not None]
+    gts = [t for t in (beta, g) if t is not None]
+    if not rows and not gts:
+        return None, None, None, None
+    ref = rows[0] if rows else gts[0]
+    if not isinstance(ref, torch.Tensor):
+        raise TypeError("gdn_prep inputs must be torch tensors")
+    dev = ref.device
+    if rows:
+        if q is not None and k is not None and (q.shape != k.shape or q.dtype != k.dtype):
+            raise ValueError(f"q and k must share shape and dtype ({tuple(q.shape)} {q.dtype} vs "
+                             f"{tuple(k.shape)} {k.dtype})")
+        if ref.dim() != 4:
+            raise ValueError("q, k must be [B, T, H, K]")
+        B, T, H, K = ref.shape
+        if K not in SUPPORTED_K:
+            raise ValueError(f"K={K} not supported (K in {SUPPORTED_K})")
+    else:
+        if ref.dim() != 3:
+            raise ValueError("beta, g must be [B, T, H]")
+        B, T, H = ref.shape
+        K = 0
+    for name, t in (("beta", beta), ("g", g)):
+        if t is not None and tuple(t.shape) != (B, T, H):
+            raise ValueError(f"{name} must be [B, T, H] = ({B}, {T}, {H}), got {tuple(t.shape)}")
+    for t in rows + gts:
+        _code(t, "input")
+        if t.device != dev:
+            raise ValueError("all inputs must be on the same device")
+    if out_gate_dtype not in _DTYPE_CODE:
+        raise ValueError(f"out_gate_dtype {out_gate_dtype} not supported")
+    if dev.type != "cuda":
+        raise ValueError(f"gdn_prep runs on a ROCm GPU (got {dev}); there is no CPU path")
+    P = _lib.GdnPrepParams()
+    P.B, P.T, P.H, P.K = B, T, H, K
+    P.eps = float(eps)
+    outs = []
+    for name, t in (("q", q), ("k", k)):
+        if t is None:
+            outs.append(None)
+            continue
+        if T > 0:
+            _check_rows(t, name)
+        o = t if inplace else torch.empty(t.shape, dtype=t.dtype, device=dev)
+        setattr(P, f"{name}_in", t.data_ptr())
+        setattr(P, f"{name}_out", o.data_ptr())
+        getattr(P, f"{name}_in_stride")[:] = _bth_strides(t)
+        getattr(P, f"{name}_out_stride")[:] = _bth_strides(o)
+        P.qk_dtype = _DTYPE_CODE[t.dtype]
+        outs.append(o)
+    for name, t in (("beta", beta), ("g", g)):
+        if t is None:
+            outs.append(None)
+            continue
+        if inplace and t.dtype != out_gate_dtype:
+            raise ValueError(f"inplace needs {name} in out_gate_dtype {out_gate_dtype}")
+        o = t if inplace else torch.empty(t.shape, dtype=out_gate_dtype, device=dev)
+        setattr(P, f"{name}_in", t.data_ptr())
+        setattr(P, f"{name}_out", o.data_ptr())
+        getattr(P, f"{name}_in_stride")[:] = t.stride()
+        getattr(P, f"{name}_out_stride")[:] = o.stride()
+        setattr(P, f"{name}_in_dtype", _DTYPE_CODE[t.dtype])
+        setattr(P, f"{name}_out_dtype", _DTYPE_CODE[o.dtype])
+        outs.append(o)
+    lib = _lib.load_library()
+    with torch.cuda.device(dev):
+        status = lib.gdn_prep_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
+    if status != 0:
+        raise RuntimeError(f"gdn_prep_launch failed ({status}): {_lib.status_string(status)}")
+    return tuple(outs)
+
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``x / sqrt(sum(x^2) + eps)`` over the last dim on the GPU
+    (gdn_ref.py:24-25), for ``[B, T, H, K]`` tensors."""
+    return gdn_prep(q=x, eps=eps)[0]
+
+
+# ---------------------------------------------------------------------------
+# FLA's keyword surface
+# ---------------------------------------------------------------------------
+
+def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                           beta: torch.Tensor, scale: Optional[float] = None,
+                           initial_state: Optional[torch.Tensor] = None,
+                           output_final_state: bool = False,
+                           cu_seqlens: Optional[torch.Tensor] = None,
+                           head_first: bool = False,
+                           use_qk_l2norm_in_kernel: bool = False):
+    """Drop-in for FLA's ``chunk_gated_delta_rule`` (FLA 0.6.0, the comparator
+    the reference calls by keyword at bench_gdn.py:169-172 and
+    bench_zoo.py:38-42), on this build's kernel.
+
+    Args follow FLA: ``q, k [B, T, H, K]``, ``v [B, T, H, V]``, ``g, beta
+    [B, T, H]`` (``[B, H, T, *]`` with ``head_first``); ``scale`` defaults to
+    ``K ** -0.5``; ``initial_state [N, H, K, V]``; ``cu_seqlens`` int64
+    ``[N + 1]`` offsets of N sequences packed along t (B = 1);
+    ``use_qk_l2norm_in_kernel`` L2-normalises q and k first (one fused
+    preparation launch).
+
+    Returns ``(o, final_state)``: ``o`` like ``v`` (``[B, H, T, V]`` with
+    ``head_first``) in q's dtype, ``final_state [N, H, K, V]`` float32 when
+    ``output_final_state`` else None.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+    if head_first:
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or g.dim() != 3 or beta.dim() != 3:
+            raise ValueError("head_first: q, k [B, H, T, K], v [B, H, T, V], g, beta [B, H, T]")
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        g, beta = g.transpose(1, 2), beta.transpose(1, 2)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    if use_qk_l2norm_in_kernel:
+        q, k, _, _ = gdn_prep(q=q, k=k)
+    h0 = initial_state
+    if h0 is not None and h0.dtype != torch.float32:
+        h0 = h0.float()
+    o, fs = _run(q, k, v, g, beta, h0, scale, 32, None, None, "auto", False, cu_seqlens,
+                 head_first)
+    return o, (fs if output_final_state else None)
