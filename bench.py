@@ -8,10 +8,12 @@ baseline (the oracle's chunked-UT restatement of gdn_ref.py:48-99 on this
 host's cores).
 
 A "step" is one ``gdn_fwd`` call over the whole batch (one kernel launch).
-Extra fields report the C=64 variant and a cold-cache timing (caches flushed
+Extra fields report the C=64 variant, a cold-cache timing (caches flushed
 with a 512 MiB write between launches, each launch timed with its own
-events).  ``--config`` selects another BASELINE config for exploration;
-the driver's line is the default.
+events) and the fused input preparation (``gdn_prep``: L2-norm of q and k,
+sigmoid beta, logsigmoid g) on the same shapes.  ``--config`` selects
+another BASELINE config for exploration and ``--workload prep`` times only
+the input preparation; the driver's line is the default.
 """
 
 from __future__ import annotations
@@ -73,6 +75,51 @@ def algorithmic_flops(B, T, H, K, V, C):
     """MFMA flops: per head-token 4CK (K K^T, Q K^T) + 2CV (P u) + 6KV
     (W S, Q S, K^T u)."""
     return B * T * H * (4 * C * K + 2 * C * V + 6 * K * V)
+
+
+def make_raw_inputs(B, T, H, K, dtype, device, seed=0):
+    """Un-normalised q, k (``dtype``) and gate logits (fp32): the inputs of
+    the fused preparation."""
+    gen = torch.Generator().manual_seed(seed)
+    qr = torch.randn(B, T, H, K, generator=gen).to(dtype).to(device)
+    kr = torch.randn(B, T, H, K, generator=gen).to(dtype).to(device)
+    br = torch.randn(B, T, H, generator=gen).to(device)
+    gr = torch.randn(B, T, H, generator=gen).to(device)
+    return qr, kr, br, gr
+
+
+def prep_bytes(B, T, H, K, in_bytes):
+    """Algorithmic bytes of one preparation launch: q and k read and written
+    once, beta and g logits read and written once in fp32."""
+    return 4 * B * T * H * K * in_bytes + 4 * B * T * H * 4
+
+
+def time_prep(pkg, B, T, H, K, dtype, steps, warmup):
+    """Times the preparation kernel through the C ABI with a prebuilt
+    parameter block (outputs allocated once), so that the events bracket
+    back-to-back kernels rather than Python argument handling."""
+    import ctypes
+    ops = importlib.import_module("v100-attention-lab_amd.ops")
+    qr, kr, br, gr = make_raw_inputs(B, T, H, K, dtype, torch.device("cuda:0"))
+    outs = pkg.gdn_prep(qr, kr, br, gr)          # validates; allocates the outputs
+    params, _ = ops._prep_plan(qr, kr, br, gr, 1e-6, torch.float32, False)
+    P = pkg._lib.GdnPrepParams.from_buffer_copy(params)
+    for name, t, o in zip(("q", "k", "beta", "g"), (qr, kr, br, gr), outs):
+        setattr(P, f"{name}_in", t.data_ptr())
+        setattr(P, f"{name}_out", o.data_ptr())
+    lib = pkg.load_library()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch():
+        status = lib.gdn_prep_launch(ctypes.byref(P), stream)
+        if status != 0:
+            raise RuntimeError(f"gdn_prep_launch failed ({status})")
+
+    ms = time_steps(launch, steps, warmup)
+    nb = prep_bytes(B, T, H, K, torch.finfo(dtype).bits // 8)
+    gbs = nb / (ms / 1e3) / 1e9
+    return {"ms_per_step": round(ms, 5), "bytes_per_launch": nb, "achieved_gbs": round(gbs, 2),
+            "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 5)}
 
 
 def time_steps(fn, steps, warmup):
@@ -165,6 +212,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--block-v", type=int, default=None)
+    ap.add_argument("--workload", default="fwd", choices=["fwd", "prep"],
+                    help="fwd: the GDN forward (default); prep: only the fused input preparation")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -195,6 +244,18 @@ def main():
     pkg = importlib.import_module("v100-attention-lab_amd")
     dev = torch.device("cuda:0")
     B, T, H, K, V, dtype, C, with_h0 = CONFIGS[args.config]
+    if args.workload == "prep":
+        r = time_prep(pkg, B, T, H, K, dtype, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "GDN input prep bytes/s (l2norm q,k; sigmoid beta; logsigmoid g)",
+            "value": round(r["bytes_per_launch"] / (r["ms_per_step"] / 1e3), 1), "unit": "B/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": DTYPE_NAME[dtype], "data": "synthetic (seed 0)",
+            "config": {"workload": f"gdn_prep {args.config}", "B": B, "T": T, "H": H, "K": K},
+            "roofline": {"bound": "hbm", "achieved": r["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": r["frac"], "traffic": None}}), flush=True)
+        return
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
 
     def step(chunk=C):
@@ -252,6 +313,7 @@ def main():
         step()
         torch.cuda.synchronize()
         line["peak_hbm_delta_bytes"] = torch.cuda.max_memory_allocated() - base
+        line["prep"] = time_prep(pkg, B, T, H, K, dtype, max(5, args.steps // 2), 5)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(B, T, H, K, V, dtype, C)

@@ -13,7 +13,8 @@ namespace gdn {
 namespace prep {
 
 constexpr int kPrepThreads = 256;
-constexpr int kRowUnroll = 4;  // row groups per lane in flight
+constexpr int kRowUnroll = 4;     // row groups per lane in flight
+constexpr int kMaxRowWg = 1024;   // workgroups per row tensor (grid stride beyond)
 
 struct PArgs {
   // row tensors ([B,T,H,K]), compacted: the first nx of {q, k} given
@@ -246,7 +247,7 @@ extern "C" int gdn_prep_launch(const GdnPrepParams* prm, void* stream) {
   const int K = (nx > 0) ? P.K : 128;
   const int lanes = K * (nx > 0 ? elem_bytes(P.qk_dtype) : 2) / 16;
   const int64_t rows_per_pass = (int64_t)(kPrepThreads / 64) * (64 / lanes) * kRowUnroll;
-  a.nbr = nx > 0 ? (int)std::min<int64_t>((R + rows_per_pass - 1) / rows_per_pass, 2048) : 0;
+  a.nbr = nx > 0 ? (int)std::min<int64_t>((R + rows_per_pass - 1) / rows_per_pass, kMaxRowWg) : 0;
   a.nbg = any_gate ? (int)std::min<int64_t>((R + kPrepThreads - 1) / kPrepThreads, 512) : 0;
   const int grid = nx * a.nbr + a.nbg;
   if (grid == 0) return GDN_OK;

@@ -299,26 +299,11 @@ def _bth_strides(t: torch.Tensor):
     return t.stride()[:3]
 
 
-def gdn_prep(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
-             beta: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
-             eps: float = 1e-6, *, out_gate_dtype: torch.dtype = torch.float32,
-             inplace: bool = False):
-    """One fused launch preparing the forward's inputs.
-
-    * ``q, k [B, T, H, K]`` -> ``x / sqrt(sum(x^2) + eps)`` over K, the sum in
-      fp32 and the denominator rounded to x's dtype before the division, as
-      the reference's ``_l2norm`` (gdn_ref.py:24-25);
-    * ``beta [B, T, H]`` (logits) -> ``sigmoid(beta)``;
-    * ``g [B, T, H]`` (logits) -> ``logsigmoid(g)``;
-
-    Any argument may be None (its result is None).  Outputs are new
-    contiguous tensors (q/k in their dtype, gates in ``out_gate_dtype``), or
-    the inputs themselves when ``inplace``.
-    """
+def _prep_plan(q, k, beta, g, eps, out_gate_dtype, inplace):
+    """Validates a preparation call and builds its parameter block (pointers
+    left zero); returns (params bytes, output specs)."""
     rows = [t for t in (q, k) if t is not None]
     gts = [t for t in (beta, g) if t is not None]
-    if not rows and not gts:
-        return None, None, None, None
     ref = rows[0] if rows else gts[0]
     if not isinstance(ref, torch.Tensor):
         raise TypeError("gdn_prep inputs must be torch tensors")
@@ -351,40 +336,90 @@ def gdn_prep(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
     P = _lib.GdnPrepParams()
     P.B, P.T, P.H, P.K = B, T, H, K
     P.eps = float(eps)
-    outs = []
+    specs = []   # per output: None, or (shape, dtype) of a new contiguous tensor
     for name, t in (("q", q), ("k", k)):
         if t is None:
-            outs.append(None)
+            specs.append(None)
             continue
         if T > 0:
             _check_rows(t, name)
-        o = t if inplace else torch.empty(t.shape, dtype=t.dtype, device=dev)
-        setattr(P, f"{name}_in", t.data_ptr())
-        setattr(P, f"{name}_out", o.data_ptr())
         getattr(P, f"{name}_in_stride")[:] = _bth_strides(t)
-        getattr(P, f"{name}_out_stride")[:] = _bth_strides(o)
+        getattr(P, f"{name}_out_stride")[:] = (_bth_strides(t) if inplace else
+                                               (T * H * K, H * K, K))
         P.qk_dtype = _DTYPE_CODE[t.dtype]
-        outs.append(o)
+        specs.append((tuple(t.shape), t.dtype))
     for name, t in (("beta", beta), ("g", g)):
         if t is None:
-            outs.append(None)
+            specs.append(None)
             continue
         if inplace and t.dtype != out_gate_dtype:
             raise ValueError(f"inplace needs {name} in out_gate_dtype {out_gate_dtype}")
-        o = t if inplace else torch.empty(t.shape, dtype=out_gate_dtype, device=dev)
-        setattr(P, f"{name}_in", t.data_ptr())
-        setattr(P, f"{name}_out", o.data_ptr())
         getattr(P, f"{name}_in_stride")[:] = t.stride()
-        getattr(P, f"{name}_out_stride")[:] = o.stride()
+        getattr(P, f"{name}_out_stride")[:] = t.stride() if inplace else (T * H, H, 1)
         setattr(P, f"{name}_in_dtype", _DTYPE_CODE[t.dtype])
-        setattr(P, f"{name}_out_dtype", _DTYPE_CODE[o.dtype])
-        outs.append(o)
+        setattr(P, f"{name}_out_dtype", _DTYPE_CODE[out_gate_dtype])
+        specs.append((tuple(t.shape), out_gate_dtype))
+    return bytes(P), specs
+
+
+_PREP_PLANS = {}
+
+
+def gdn_prep(q: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
+             beta: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
+             eps: float = 1e-6, *, out_gate_dtype: torch.dtype = torch.float32,
+             inplace: bool = False):
+    """One fused launch preparing the forward's inputs.
+
+    * ``q, k [B, T, H, K]`` -> ``x / sqrt(sum(x^2) + eps)`` over K, the sum in
+      fp32 and the denominator rounded to x's dtype before the division, as
+      the reference's ``_l2norm`` (gdn_ref.py:24-25);
+    * ``beta [B, T, H]`` (logits) -> ``sigmoid(beta)``;
+    * ``g [B, T, H]`` (logits) -> ``logsigmoid(g)``;
+
+    Any argument may be None (its result is None).  Outputs are new
+    contiguous tensors (q/k in their dtype, gates in ``out_gate_dtype``), or
+    the inputs themselves when ``inplace``.  Launch plans are cached by
+    shapes, strides and dtypes, as for ``gdn_fwd``.
+    """
+    ins = (q, k, beta, g)
+    if all(t is None for t in ins):
+        return None, None, None, None
+    try:
+        key = tuple(None if t is None else (t.shape, t.stride(), t.dtype, t.device) for t in ins)
+        key += (float(eps), out_gate_dtype, inplace)
+        plan = _PREP_PLANS.get(key)
+    except (AttributeError, TypeError):
+        key, plan = None, None
+    if plan is None:
+        plan = _prep_plan(q, k, beta, g, eps, out_gate_dtype, inplace)
+        if key is not None:
+            if len(_PREP_PLANS) >= _PLANS_MAX:
+                _PREP_PLANS.clear()
+            _PREP_PLANS[key] = plan
+    params, specs = plan
+    rows = [t for t in (q, k) if t is not None]
+    if rows and rows[0].shape[1] > 0 and any(t.data_ptr() & 15 for t in rows):
+        for name, t in (("q", q), ("k", k)):
+            if t is not None:
+                _check_rows(t, name)
+    dev = next(t for t in ins if t is not None).device
+    outs = tuple(None if sp is None else (t if inplace else torch.empty(sp[0], dtype=sp[1], device=dev))
+                 for t, sp in zip(ins, specs))
+    P = _lib.GdnPrepParams.from_buffer_copy(params)
+    for name, t, o in zip(("q", "k", "beta", "g"), ins, outs):
+        if t is not None:
+            setattr(P, f"{name}_in", t.data_ptr())
+            setattr(P, f"{name}_out", o.data_ptr())
     lib = _lib.load_library()
-    with torch.cuda.device(dev):
+    if dev.index == torch.cuda.current_device():
         status = lib.gdn_prep_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
+    else:
+        with torch.cuda.device(dev):
+            status = lib.gdn_prep_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
     if status != 0:
         raise RuntimeError(f"gdn_prep_launch failed ({status}): {_lib.status_string(status)}")
-    return tuple(outs)
+    return outs
 
 
 def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
