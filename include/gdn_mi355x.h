@@ -64,7 +64,8 @@ enum GdnStatus {
   GDN_ERR_BAD_SHAPE = 1002,
   GDN_ERR_UNSUPPORTED = 1003,
   GDN_ERR_MISALIGNED = 1004,
-  GDN_ERR_BAD_DTYPE = 1005
+  GDN_ERR_BAD_DTYPE = 1005,
+  GDN_ERR_WORKSPACE = 1006
 };
 
 /* Launch options (bit flags). */
@@ -162,6 +163,69 @@ typedef struct GdnPrepParams {
 /* Enqueue the input preparation on `stream`; returns a GdnStatus /
  * hipError_t value. */
 int gdn_prep_launch(const GdnPrepParams* params, void* stream);
+
+/* Backward of the forward above: gradients of q, k, v, g, beta and h0 given
+ * d_o (the gradient of o) and d_final_state.  No counterpart in the
+ * reference, whose README lists the backward as future work
+ * (README.md:259); it is the gradient of the recurrence gdn_ref.py:3-9 and
+ * is checked against reverse-mode differentiation of that recurrence.
+ *   - Same tensors, strides and varlen convention as GdnFwdParams; the
+ *     chunk length is 32.  K in {32, 64, 128}; V a multiple of 16.
+ *   - dq, dk, dv take q's dtype layout rules (16-byte rows not required);
+ *     dg, dbeta any strides; dh0 [B,H,K,V] fp32 (nullable: not written).
+ *   - d_final_state nullable (zero).  h0 nullable (zero).
+ *   - workspace: device memory of at least gdn_bwd_workspace_size(...)
+ *     bytes, 256-byte aligned, owned by the caller; its contents need no
+ *     initialisation and are undefined afterwards.
+ *   - Enqueues two kernels on `stream`; no allocation, no synchronisation. */
+typedef struct GdnBwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;           /* nullable */
+  const void* d_o;           /* [B,T,H,V] */
+  const float* d_final_state;/* nullable, [B,H,K,V] */
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dg;
+  void* dbeta;
+  float* dh0;                /* nullable */
+  void* workspace;
+  /* strides in elements, (b, t, h) */
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t g_stride[3];
+  int64_t beta_stride[3];
+  int64_t do_stride[3];
+  int64_t dq_stride[3];
+  int64_t dk_stride[3];
+  int64_t dv_stride[3];
+  int64_t dg_stride[3];
+  int64_t dbeta_stride[3];
+  /* strides in elements, (b, h, k, v) */
+  int64_t h0_stride[4];
+  int64_t dfs_stride[4];
+  int64_t dh0_stride[4];
+  int32_t B, T, H, K, V;
+  float scale;
+  int32_t qkv_dtype;         /* q, k, v and dq, dk, dv */
+  int32_t g_dtype;           /* g and dg */
+  int32_t beta_dtype;        /* beta and dbeta */
+  int32_t do_dtype;
+  const int64_t* cu_seqlens; /* nullable, as in GdnFwdParams */
+  int64_t workspace_bytes;
+} GdnBwdParams;
+
+/* Bytes of workspace gdn_bwd_launch needs for these sizes (n_seq: the
+ * number of sequences with cu_seqlens, else 0); -1 if unsupported. */
+int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq);
+
+/* Enqueue the backward on `stream`; returns a GdnStatus / hipError_t. */
+int gdn_bwd_launch(const GdnBwdParams* params, void* stream);
 
 /* Human-readable text for a status code. */
 const char* gdn_fwd_status_string(int status);

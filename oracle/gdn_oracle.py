@@ -17,6 +17,12 @@ It restates, in plain PyTorch on the CPU, the semantics of the reference's
                          order, including the two unit-triangular solves and
                          the K x K state update, so that timing it is a fair
                          CPU baseline)
+* ``recurrent_grads`` -- gradients of ``recurrent`` by reverse-mode
+                         differentiation (torch.autograd, fp64); the
+                         reference has no backward (README.md:259)
+* ``chunked_bwd``     -- the chunked backward the HIP kernel implements,
+                         restated per head in fp64 (pinned against
+                         ``recurrent_grads``)
 * ``pad_to_multiple`` -- gdn_ref.py:102-114
 * ``rel_err``         -- bench_gdn.py:89-94 (max-norm relative error)
 * ``make_inputs_*``   -- bench_gdn.py:33-40 (reference recipe) and the
@@ -46,7 +52,8 @@ from typing import Optional, Tuple
 import torch
 
 __all__ = [
-    "l2norm", "sigmoid", "logsigmoid", "prep_inputs", "recurrent", "chunked_ut", "pad_to_multiple", "rel_err",
+    "l2norm", "sigmoid", "logsigmoid", "prep_inputs", "recurrent", "recurrent_grads",
+    "chunked_bwd", "chunked_ut", "pad_to_multiple", "rel_err",
     "make_inputs_reference", "make_inputs_baseline", "to_kv", "to_vk",
     "BaselineConfig", "BASELINE_CONFIGS", "algorithmic_bytes",
     "algorithmic_flops",
@@ -122,6 +129,109 @@ def recurrent(q, k, v, beta, g, initial_state=None, dtype=torch.float64):
         h = h + u.unsqueeze(-1) * kt.unsqueeze(-2)     # rank-1 write
         o[:, t] = (h @ q[:, t].unsqueeze(-1)).squeeze(-1)
     return o, h
+
+
+def recurrent_grads(q, k, v, beta, g, initial_state, do, dfinal, scale=1.0):
+    """Gradients of ``L = <o, do> + <final_state, dfinal>`` with respect to
+    (q, k, v, beta, g, initial_state) for ``o = scale * recurrent(...)``,
+    by torch.autograd through the fp64 step recurrence.
+
+    Shapes as ``recurrent``; ``initial_state`` and ``dfinal`` in the K x V
+    layout ``[B, H, K, V]`` (None = zero).  Returns fp64 tensors
+    ``(dq, dk, dv, dbeta, dg, dh0)``.
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    h0 = torch.zeros(B, H, K, V, dtype=torch.float64) if initial_state is None else initial_state
+    xs = [t.detach().double().requires_grad_(True) for t in (q, k, v, beta, g, h0)]
+    o, h = recurrent(xs[0], xs[1], xs[2], xs[3], xs[4], to_vk(xs[5]), dtype=torch.float64)
+    loss = (scale * o * do.double()).sum()
+    if dfinal is not None:
+        loss = loss + (to_kv(h) * dfinal.double()).sum()
+    return torch.autograd.grad(loss, xs)
+
+
+def chunked_bwd(q, k, v, beta, g, initial_state, do, dfinal, scale=1.0, C=32):
+    """The chunked backward, one head at a time, in fp64: pass 1 stores the
+    state at each chunk start, pass 2 walks the chunks backward carrying the
+    state gradient (the algebra of csrc/gdn_bwd.hip's header).  Same
+    arguments and returns as ``recurrent_grads``."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    f = lambda t: t.double()
+    outs = [torch.zeros(B, T, H, K, dtype=torch.float64), torch.zeros(B, T, H, K, dtype=torch.float64),
+            torch.zeros(B, T, H, V, dtype=torch.float64), torch.zeros(B, T, H, dtype=torch.float64),
+            torch.zeros(B, T, H, dtype=torch.float64), torch.zeros(B, H, K, V, dtype=torch.float64)]
+    eye = torch.eye(C, dtype=torch.float64)
+    for b in range(B):
+        for hh in range(H):
+            S = (torch.zeros(K, V, dtype=torch.float64) if initial_state is None
+                 else f(initial_state[b, hh]))
+            nch = (T + C - 1) // C
+
+            def chunk(c):
+                sl = slice(c * C, min(c * C + C, T))
+                n = sl.stop - sl.start
+                pad = lambda x, w: torch.cat([f(x), torch.zeros((C - n,) + tuple(x.shape[1:]),
+                                                                dtype=torch.float64)]) if w else f(x)
+                Q = pad(q[b, sl, hh], True)
+                Kc = pad(k[b, sl, hh], True)
+                Vc = pad(v[b, sl, hh], True)
+                dO = pad(do[b, sl, hh], True)
+                gg = pad(g[b, sl, hh], True)
+                bt = pad(beta[b, sl, hh], True)
+                return sl, n, Q, Kc, Vc, dO, gg, bt
+
+            def ut(Kc, Vc, gg, bt, S):
+                bb = gg.cumsum(0)
+                gam, D, gC = bb.exp(), (bb[-1] - bb).exp(), bb[-1].exp()
+                M = torch.tril((bb[:, None] - bb[None, :]).exp())
+                KK = Kc @ Kc.T
+                A = torch.tril(bt[:, None] * M * KK, -1)
+                Tm = torch.linalg.solve_triangular(eye + A, eye, upper=False, unitriangular=True)
+                W = Tm @ ((bt * gam)[:, None] * Kc)
+                u = Tm @ (bt[:, None] * Vc) - W @ S
+                return gam, D, gC, M, KK, A, Tm, W, u
+
+            starts = []
+            for c in range(nch):
+                sl, n, Q, Kc, Vc, dO, gg, bt = chunk(c)
+                starts.append(S)
+                gam, D, gC, M, KK, A, Tm, W, u = ut(Kc, Vc, gg, bt, S)
+                S = gC * S + Kc.T @ (D[:, None] * u)
+            dS = (torch.zeros(K, V, dtype=torch.float64) if dfinal is None else f(dfinal[b, hh]))
+            for c in reversed(range(nch)):
+                sl, n, Q, Kc, Vc, dO, gg, bt = chunk(c)
+                S = starts[c]
+                gam, D, gC, M, KK, A, Tm, W, u = ut(Kc, Vc, gg, bt, S)
+                QK = Q @ Kc.T
+                KdS = Kc @ dS
+                du = scale * (M * QK).T @ dO + D[:, None] * KdS
+                dQK = M * (scale * dO @ u.T)
+                dD = (u * KdS).sum(1)
+                dgam = scale * (dO * (Q @ S)).sum(1)
+                dgC = (dS * S).sum()
+                dW = -du @ S.T
+                dT = du @ (bt[:, None] * Vc).T + dW @ ((bt * gam)[:, None] * Kc).T
+                dWt, dUt = Tm.T @ dW, Tm.T @ du
+                dbt = (Vc * dUt).sum(1) + gam * (Kc * dWt).sum(1)
+                dgam = dgam + bt * (Kc * dWt).sum(1)
+                dA = torch.tril(-(Tm.T @ dT @ Tm.T), -1)
+                dKK = dA * bt[:, None] * M
+                dbt = dbt + (dA * M * KK).sum(1)
+                dQQ, dAA = dQK * QK, dA * A
+                db = dgam * gam - dD * D + dQQ.sum(1) - dQQ.sum(0) + dAA.sum(1) - dAA.sum(0)
+                db[C - 1] += (dD * D).sum() + dgC * gC
+                dgc = db.flip(0).cumsum(0).flip(0)
+                outs[0][b, sl, hh] = (dQK @ Kc + scale * gam[:, None] * (dO @ S.T))[:n]
+                outs[1][b, sl, hh] = (dQK.T @ Q + D[:, None] * (u @ dS.T) + (bt * gam)[:, None] * dWt
+                                      + (dKK + dKK.T) @ Kc)[:n]
+                outs[2][b, sl, hh] = (bt[:, None] * dUt)[:n]
+                outs[3][b, sl, hh] = dbt[:n]
+                outs[4][b, sl, hh] = dgc[:n]
+                dS = scale * Q.T @ (gam[:, None] * dO) + gC * dS - W.T @ du
+            outs[5][b, hh] = dS
+    return tuple(outs)
 
 
 def chunked_ut(q, k, v, beta, g, C=64, initial_state=None):

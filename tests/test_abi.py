@@ -54,7 +54,7 @@ def test_abi_version(lib):
     assert lib.gdn_fwd_abi_version() == 3
 
 
-@pytest.mark.parametrize("struct", ["GdnFwdParams", "GdnPrepParams"])
+@pytest.mark.parametrize("struct", ["GdnFwdParams", "GdnPrepParams", "GdnBwdParams"])
 def test_struct_layout_matches_header(tmp_path, struct):
     """Compile a probe against the header with gcc and compare offsets."""
     from importlib import import_module
@@ -283,3 +283,59 @@ def test_fla_surface_and_prep_reject_cpu_tensors(pkg):
         pkg.chunk_gated_delta_rule(q, k, v, g[..., None], b, head_first=True)
     with pytest.raises(ValueError, match="K=96"):
         pkg.gdn_prep(q=torch.zeros(1, 4, 2, 96))
+
+
+# --------------------------------------------------------------------------
+# backward entry points: sizes and argument errors before any launch
+# --------------------------------------------------------------------------
+
+def test_bwd_workspace_size(lib):
+    # cfg2 with 16-column slices: chunk states + partial dq/dk/dg/dbeta
+    nv, nch, R = 128 // 16, 4096 // 32, 2 * 4096
+    want = (2 * nch * 16 * nv * 128 * 16 * 4 + 2 * nv * R * 16 * 128 * 4 + 2 * nv * R * 16 * 4)
+    got = lib.gdn_bwd_workspace_size(2, 4096, 16, 128, 128, 0)
+    assert want <= got <= want + 5 * 256
+    assert lib.gdn_bwd_workspace_size(2, 4096, 16, 256, 128, 0) == -1
+    assert lib.gdn_bwd_workspace_size(2, 4096, 16, 128, 120, 0) == -1
+    # packed sequences: chunk slots ceil(T / C) + N
+    assert lib.gdn_bwd_workspace_size(3, 100, 2, 64, 32, 3) > 0
+
+
+def _bwd_params(L, **kw):
+    P = L.GdnBwdParams()
+    fake = 0x1000  # never dereferenced: every case below returns before a launch
+    for n in ("q", "k", "v", "g", "beta", "d_o", "dq", "dk", "dv", "dg", "dbeta"):
+        setattr(P, n, fake)
+    P.B, P.T, P.H, P.K, P.V = 2, 64, 2, 64, 32
+    P.workspace = 0x100000
+    P.workspace_bytes = 1 << 40
+    P.qkv_dtype, P.g_dtype, P.beta_dtype, P.do_dtype = 1, 0, 0, 1
+    P.scale = 1.0
+    for k_, v_ in kw.items():
+        setattr(P, k_, v_)
+    return P
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(K=256), 1003), (dict(V=24), 1002), (dict(B=0), 1002), (dict(do_dtype=4), 1005),
+    (dict(d_o=None), 1001), (dict(dg=None), 1001), (dict(workspace=None), 1006),
+    (dict(workspace=0x100010), 1006), (dict(workspace_bytes=1024), 1006),
+])
+def test_bwd_rejects_bad_arguments(lib, kw, code):
+    from importlib import import_module
+    L = import_module("v100-attention-lab_amd._lib")
+    assert lib.gdn_bwd_launch(ctypes.byref(_bwd_params(L, **kw)), None) == code
+    assert lib.gdn_bwd_launch(None, None) == 1001
+    assert "workspace" in lib.gdn_fwd_status_string(1006).decode()
+
+
+def test_bwd_python_validation(pkg):
+    q, k, v, g, b = _cpu_inputs(K=256)
+    with pytest.raises(ValueError, match="K=256"):
+        pkg.gdn_bwd(q, k, v, g, b, None, torch.zeros(1, 64, 2, 32, dtype=torch.float16))
+    q, k, v, g, b = _cpu_inputs()
+    with pytest.raises(ValueError, match="do must"):
+        pkg.gdn_bwd(q, k, v, g, b, None, torch.zeros(1, 64, 2, 16, dtype=torch.float16))
+    with pytest.raises(ValueError, match="dfinal"):
+        pkg.gdn_bwd(q, k, v, g, b, None, torch.zeros(1, 64, 2, 32, dtype=torch.float16),
+                    torch.zeros(1, 2, 64, 32, dtype=torch.float16))

@@ -1,0 +1,164 @@
+"""GPU parity of the HIP backward (``gdn_bwd``, autograd through ``gdn_fwd``).
+
+The reference has no backward (README.md:259); the gradients are those of
+its recurrence (gdn_ref.py:3-9).  They are checked against reverse-mode
+differentiation of the oracle's fp64 step recurrence (``recurrent_grads``)
+on the same (cast) inputs, with the max-norm relative error of
+bench_gdn.py:89-94:
+  * fp32 inputs: <= 2e-5 (the kernel computes in fp32);
+  * fp16 / bf16 inputs: <= 1e-3 plus one rounding of the gradient to its
+    storage dtype (2^-11 / 2^-8).
+At the full cfg2 shape one head is compared with the oracle's fp64 chunked
+backward, and packed sequences are compared bit for bit with separate runs.
+"""
+
+import pytest
+import torch
+
+from oracle import gdn_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("dq", "dk", "dv", "dbeta", "dg", "dh0")
+
+
+def _inputs(B, T, H, K, V, dtype, seed, gate=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    q = ref.l2norm(torch.randn(B, T, H, K, generator=gen)).to(dtype)
+    k = ref.l2norm(torch.randn(B, T, H, K, generator=gen)).to(dtype)
+    v = torch.randn(B, T, H, V, generator=gen).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    g = gate * torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen))
+    h0 = 0.1 * torch.randn(B, H, K, V, generator=gen)
+    do = torch.randn(B, T, H, V, generator=gen).to(dtype)
+    dfin = torch.randn(B, H, K, V, generator=gen)
+    return q, k, v, g, beta, h0, do, dfin
+
+
+def _tol(dtype):
+    if dtype == torch.float32:
+        return 2e-5
+    return 1e-3 + (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11)
+
+
+def _compare(got, want, dtype, label):
+    errs = {}
+    for name, a, b in zip(NAMES, got, want):
+        if a is None:
+            continue
+        errs[name] = ref.rel_err(b, a.cpu().double())
+    print(f"[bwd] {label}: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    for name, e in errs.items():
+        tol = 2e-5 if name == "dh0" and dtype == torch.float32 else _tol(dtype)
+        if name == "dh0" and dtype != torch.float32:
+            tol = 1e-3        # dh0 is fp32 for every input dtype
+        assert e <= tol, (label, name, e)
+
+
+@pytest.mark.parametrize("T,K,V,gate", [(64, 32, 16, 1.0), (77, 64, 32, 1.0), (33, 128, 16, 1.0),
+                                        (130, 128, 48, 3.0), (5, 32, 16, 1.0), (256, 64, 64, 0.1)])
+def test_bwd_fp32_vs_autograd(pkg, cuda, T, K, V, gate):
+    B, H = 2, 2
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, torch.float32, seed=T + K, gate=gate)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] fp32 T={T} K={K} V={V} gate={gate}", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=0.7)
+    torch.cuda.synchronize()
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=0.7)
+    got = (got[0], got[1], got[2], got[4], got[3], got[5])   # -> dq dk dv dbeta dg dh0
+    _compare(got, want, torch.float32, f"fp32 T={T} K={K} V={V}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_bwd_lowp_vs_autograd(pkg, cuda, dtype):
+    B, T, H, K, V = 1, 200, 3, 128, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=5)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] {dtype}", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=1.0)
+    torch.cuda.synchronize()
+    assert got[0].dtype == dtype and got[2].dtype == dtype and got[3].dtype == torch.float32
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin)
+    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, str(dtype))
+
+
+def test_autograd_through_gdn_fwd(pkg, cuda):
+    """loss.backward() through gdn_fwd (pipelined forward, HIP backward)
+    equals the oracle's gradients; gdn_chunk_fwd's V x K state and FLA's
+    head_first layout backpropagate through their strides."""
+    B, T, H, K, V = 2, 96, 2, 64, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, torch.float16, seed=9)
+    leaves = [t.to(cuda).requires_grad_(True) for t in (q, k, v, g, beta, h0)]
+    print("[bwd] autograd gdn_fwd", flush=True)
+    o, fs = pkg.gdn_fwd(*leaves, scale=0.5)
+    (o.float() * do.to(cuda).float()).sum().backward(inputs=leaves, retain_graph=False)
+    fs_loss = None
+    got = [t.grad for t in leaves]
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, None, scale=0.5)
+    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, torch.float16, "autograd")
+
+    # gdn_chunk_fwd: h [B,H,V,K]; gradient through the final state only
+    leaves2 = [t.to(cuda).requires_grad_(True) for t in (q, k, v, beta, g)]
+    o2, hf = pkg.gdn_chunk_fwd(*leaves2)
+    (hf * dfin.transpose(2, 3).to(cuda)).sum().backward()
+    want2 = ref.recurrent_grads(q, k, v, beta, g, None, torch.zeros_like(do), dfin)
+    got2 = [leaves2[0].grad, leaves2[1].grad, leaves2[2].grad, leaves2[3].grad, leaves2[4].grad, None]
+    _compare(got2, want2, torch.float16, "gdn_chunk_fwd state grad")
+
+    # FLA head_first: gradients come back in the [B, H, T, *] layout
+    hf_ = lambda t: t.transpose(1, 2).contiguous()
+    leaves3 = [hf_(t).to(cuda).requires_grad_(True) for t in (q, k, v, g, beta)]
+    o3, _ = pkg.chunk_gated_delta_rule(*leaves3, scale=0.5, head_first=True)
+    (o3.float() * hf_(do).to(cuda).float()).sum().backward()
+    want3 = ref.recurrent_grads(q, k, v, beta, g, None, do, None, scale=0.5)
+    got3 = [leaves3[0].grad.transpose(1, 2), leaves3[1].grad.transpose(1, 2),
+            leaves3[2].grad.transpose(1, 2), leaves3[4].grad.transpose(1, 2),
+            leaves3[3].grad.transpose(1, 2), None]
+    _compare(got3, want3, torch.float16, "head_first")
+
+
+def test_bwd_varlen_equals_separate_runs(pkg, cuda):
+    lens = [40, 0, 1, 64, 75]
+    H, K, V = 2, 64, 32
+    T = sum(lens)
+    q, k, v, g, beta, _, do, _ = _inputs(1, T, H, K, V, torch.float32, seed=12)
+    n = len(lens)
+    gen = torch.Generator().manual_seed(13)
+    h0 = 0.1 * torch.randn(n, H, K, V, generator=gen)
+    dfin = torch.randn(n, H, K, V, generator=gen)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int64)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] varlen {lens}", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=0.9,
+                      cu_seqlens=d(cu))
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+        sl = lambda t: t[:, a:b].contiguous()
+        sep = pkg.gdn_bwd(d(sl(q)), d(sl(k)), d(sl(v)), d(sl(g)), d(sl(beta)), d(h0[i:i + 1]),
+                          d(sl(do)), d(dfin[i:i + 1]), scale=0.9)
+        torch.cuda.synchronize()
+        for j in range(5):
+            assert torch.equal(got[j][:, a:b].cpu(), sep[j].cpu()), (i, j)
+        assert torch.equal(got[5][i:i + 1].cpu(), sep[5].cpu()), (i, "dh0")
+
+
+def test_bwd_full_size_one_head(pkg, cuda):
+    """cfg2 shape (fp16 B2 H16 T4096 K=V=128): the whole backward runs, and
+    head (b=1, h=5) matches the oracle's fp64 chunked backward."""
+    B, T, H, K, V = 2, 4096, 16, 128, 128
+    q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=0)
+    gen = torch.Generator().manual_seed(1)
+    do = torch.randn(B, T, H, V, generator=gen).half()
+    d = lambda t: t.to(cuda)
+    print("[bwd] cfg2 full size", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), None, d(do), None, scale=1.0,
+                      need_dh0=False)
+    torch.cuda.synchronize()
+    for t in got[:5]:
+        assert torch.isfinite(t.float()).all()
+    b, h = 1, 5
+    sel = lambda t: t[b:b + 1, :, h:h + 1]
+    want = ref.chunked_bwd(sel(q), sel(k), sel(v), sel(beta), sel(g), None, sel(do), None)
+    mine = (sel(got[0].cpu()), sel(got[1].cpu()), sel(got[2].cpu()), sel(got[4].cpu()),
+            sel(got[3].cpu()), None)
+    _compare(mine, want, torch.float16, "cfg2 head (1,5)")

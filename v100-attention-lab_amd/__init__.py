@@ -13,9 +13,9 @@ import sys as _sys
 
 from ._lib import load_library, status_string, LIB_PATH  # noqa: F401
 from .ops import (gdn_fwd, gdn_chunk_fwd, auto_block_v, gdn_prep, l2norm,  # noqa: F401
-                  chunk_gated_delta_rule)
+                  chunk_gated_delta_rule, gdn_bwd)
 
 _sys.modules.setdefault("v100_attention_lab_amd", _sys.modules[__name__])
 
 __all__ = ["gdn_fwd", "gdn_chunk_fwd", "chunk_gated_delta_rule", "gdn_prep", "l2norm",
-           "auto_block_v", "load_library", "status_string"]
+           "gdn_bwd", "auto_block_v", "load_library", "status_string"]

@@ -23,6 +23,7 @@ GDN_ERR_BAD_SHAPE = 1002
 GDN_ERR_UNSUPPORTED = 1003
 GDN_ERR_MISALIGNED = 1004
 GDN_ERR_BAD_DTYPE = 1005
+GDN_ERR_WORKSPACE = 1006
 
 # enum GdnFlags
 FLAG_PHASED_KERNEL = 1
@@ -34,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "gdn_fwd_status_string",
     "gdn_fwd_abi_version",
     "gdn_prep_launch",
+    "gdn_bwd_workspace_size",
+    "gdn_bwd_launch",
 )
 
 _I64x3 = ctypes.c_int64 * 3
@@ -110,6 +113,22 @@ class GdnPrepParams(ctypes.Structure):
     ]
 
 
+class GdnBwdParams(ctypes.Structure):
+    """Mirror of ``GdnBwdParams`` in include/gdn_mi355x.h."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "q", "k", "v", "g", "beta", "h0", "d_o", "d_final_state",
+        "dq", "dk", "dv", "dg", "dbeta", "dh0", "workspace")] + \
+        [(n, _I64x3) for n in (
+            "q_stride", "k_stride", "v_stride", "g_stride", "beta_stride", "do_stride",
+            "dq_stride", "dk_stride", "dv_stride", "dg_stride", "dbeta_stride")] + \
+        [(n, _I64x4) for n in ("h0_stride", "dfs_stride", "dh0_stride")] + \
+        [(n, ctypes.c_int32) for n in ("B", "T", "H", "K", "V")] + \
+        [("scale", ctypes.c_float)] + \
+        [(n, ctypes.c_int32) for n in ("qkv_dtype", "g_dtype", "beta_dtype", "do_dtype")] + \
+        [("cu_seqlens", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64)]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -137,6 +156,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         lib.gdn_fwd_status_string.restype = ctypes.c_char_p
         lib.gdn_prep_launch.argtypes = [ctypes.POINTER(GdnPrepParams), ctypes.c_void_p]
         lib.gdn_prep_launch.restype = ctypes.c_int
+        lib.gdn_bwd_launch.argtypes = [ctypes.POINTER(GdnBwdParams), ctypes.c_void_p]
+        lib.gdn_bwd_launch.restype = ctypes.c_int
+        lib.gdn_bwd_workspace_size.argtypes = [ctypes.c_int] * 6
+        lib.gdn_bwd_workspace_size.restype = ctypes.c_int64
         lib.gdn_fwd_abi_version.argtypes = []
         lib.gdn_fwd_abi_version.restype = ctypes.c_int
         ver = lib.gdn_fwd_abi_version()

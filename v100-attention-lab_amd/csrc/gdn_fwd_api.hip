@@ -63,6 +63,8 @@ const char* gdn_fwd_status_string(int status) {
     case GDN_ERR_MISALIGNED:
       return "gdn_fwd: q/k/v rows must be 16-byte aligned with a contiguous last dimension";
     case GDN_ERR_BAD_DTYPE: return "gdn_fwd: unknown dtype code";
+    case GDN_ERR_WORKSPACE:
+      return "gdn_fwd: workspace missing, misaligned or smaller than gdn_bwd_workspace_size()";
     default: return hipGetErrorString((hipError_t)status);
   }
 }

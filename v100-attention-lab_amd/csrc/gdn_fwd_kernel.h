@@ -298,13 +298,15 @@ struct RowSpan {
   int T;       // number of rows
 };
 
-__device__ __forceinline__ RowSpan row_span(const KArgs& p, int bi) {
-  if (p.cu == nullptr) return RowSpan{bi, 0, p.T};
-  int64_t lo = p.cu[bi], hi = p.cu[bi + 1];
-  lo = lo < 0 ? 0 : (lo > p.T ? p.T : lo);
-  hi = hi < lo ? lo : (hi > p.T ? p.T : hi);
+__device__ __forceinline__ RowSpan row_span(const int64_t* cu, int T, int bi) {
+  if (cu == nullptr) return RowSpan{bi, 0, T};
+  int64_t lo = cu[bi], hi = cu[bi + 1];
+  lo = lo < 0 ? 0 : (lo > T ? T : lo);
+  hi = hi < lo ? lo : (hi > T ? T : hi);
   return RowSpan{0, lo, (int)(hi - lo)};
 }
+
+__device__ __forceinline__ RowSpan row_span(const KArgs& p, int bi) { return row_span(p.cu, p.T, bi); }
 
 // Element offset of the first row of head h in a [B, T, H, *] tensor with
 // (b, t, h) strides s.

@@ -51,7 +51,7 @@ def _check_rows(t: torch.Tensor, name: str) -> None:
                          f"b/t/h strides {t.stride()[:3]}); call .contiguous()")
 
 
-def _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq=None):
+def _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq=None, check_device=True):
     """Checks the call; returns (units B, packed T, H, K, V).  With n_seq
     (cu_seqlens given) the tensors hold one packed batch of n_seq sequences."""
     for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta)):
@@ -92,17 +92,22 @@ def _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq=None):
         raise ValueError(f"chunk_size={chunk_size} not supported {SUPPORTED_CHUNKS}")
     if block_v is not None and (block_v not in SUPPORTED_BLOCK_V or V % block_v):
         raise ValueError(f"block_v={block_v} must be one of {SUPPORTED_BLOCK_V} and divide V={V}")
-    dev = q.device
-    if dev.type != "cuda":
-        raise ValueError("gdn_fwd runs on a ROCm GPU: inputs must be on a cuda device "
-                         f"(got {dev}); there is no CPU path")
-    others = (k, v, g, beta) + ((h0,) if h0 is not None else ())
-    if any(t.device != dev for t in others):
-        raise ValueError("all inputs must be on the same device")
+    if check_device:
+        _check_devices(q, k, v, g, beta, h0)
     if T > 0:
         for name, t in (("q", q), ("k", k), ("v", v)):
             _check_rows(t, name)
     return B, T, H, K, V
+
+
+def _check_devices(q, *others):
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("gdn_fwd runs on a ROCm GPU: inputs must be on a cuda device "
+                         f"(got {dev}); there is no CPU path")
+    others = tuple(t for t in others if t is not None)
+    if any(t.device != dev for t in others):
+        raise ValueError("all inputs must be on the same device")
 
 
 _KERNELS = {"auto": 0, "phased": _lib.FLAG_PHASED_KERNEL}
@@ -263,11 +268,16 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         ``final_state[i]`` (h0 and final_state are then ``[N, H, K, V]``).
 
     Returns:
-      ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.
+      ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.  When an
+      input requires grad (and grad mode is on) both outputs are
+      differentiable; the backward runs ``gdn_bwd`` (K in {32, 64, 128}).
 
     Semantics are the reference's (gdn_ref.py:3-9): per step
     ``S = e^{g} S; u = beta (v - S^T k); S += k u^T; o = scale S^T q``.
     """
+    if _needs_grad(q, k, v, g, beta, h0):
+        return _GdnFunction.apply(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
+                                  kernel, False, cu_seqlens, False)
     return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False,
                 cu_seqlens)
 
@@ -282,6 +292,9 @@ def gdn_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch
     Any T is accepted: the trailing partial chunk is masked in-kernel, which
     equals the reference's zero padding (gdn_triton.py:121-125).
     """
+    if _needs_grad(q, k, v, g, beta):
+        return _GdnFunction.apply(q, k, v, g, beta, None, 1.0, 32, None, None, "auto", True,
+                                  None, False)
     return _run(q, k, v, g, beta, None, 1.0, 32, None, None, "auto", True)
 
 
@@ -465,10 +478,128 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g:
     if scale is None:
         scale = q.shape[-1] ** -0.5
     if use_qk_l2norm_in_kernel:
+        if _needs_grad(q, k):
+            raise NotImplementedError("use_qk_l2norm_in_kernel with gradients through q, k is not "
+                                      "supported: normalise with gdn_prep / l2norm first")
         q, k, _, _ = gdn_prep(q=q, k=k)
     h0 = initial_state
     if h0 is not None and h0.dtype != torch.float32:
         h0 = h0.float()
-    o, fs = _run(q, k, v, g, beta, h0, scale, 32, None, None, "auto", False, cu_seqlens,
-                 head_first)
+    if _needs_grad(q, k, v, g, beta, h0):
+        o, fs = _GdnFunction.apply(q, k, v, g, beta, h0, scale, 32, None, None, "auto", False,
+                                   cu_seqlens, head_first)
+    else:
+        o, fs = _run(q, k, v, g, beta, h0, scale, 32, None, None, "auto", False, cu_seqlens,
+                     head_first)
     return o, (fs if output_final_state else None)
+
+
+# ---------------------------------------------------------------------------
+# backward
+# ---------------------------------------------------------------------------
+
+BWD_SUPPORTED_K = (32, 64, 128)
+
+
+def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+            beta: torch.Tensor, h0: Optional[torch.Tensor], do: torch.Tensor,
+            dfinal: Optional[torch.Tensor] = None, scale: float = 1.0,
+            cu_seqlens: Optional[torch.Tensor] = None, need_dh0: bool = True):
+    """Gradients of ``gdn_fwd`` (the recurrence gdn_ref.py:3-9) with respect to
+    ``q, k, v, g, beta, h0``, given ``do`` (the gradient of ``o``, ``[B,T,H,V]``)
+    and ``dfinal`` (the gradient of ``final_state``, ``[B,H,K,V]`` fp32, or
+    None for zero).
+
+    Returns ``(dq, dk, dv, dg, dbeta, dh0)`` in the inputs' dtypes (``dh0``
+    fp32, None unless ``need_dh0``).  K in {32, 64, 128}, V a multiple of 16;
+    same strides, dtypes and ``cu_seqlens`` convention as the forward.  One
+    call enqueues the backward kernel and the slice reduction on the current
+    stream; the workspace (chunk-start states and per-slice partial sums) is
+    allocated here and released when the call returns.
+    """
+    n_seq = None
+    if cu_seqlens is not None:
+        cu_seqlens, n_seq = _check_cu_seqlens(cu_seqlens, q.shape[1], q.device)
+    B, T, H, K, V = _validate(q, k, v, g, beta, h0, 32, None, n_seq, check_device=False)
+    if K not in BWD_SUPPORTED_K:
+        raise ValueError(f"K={K} not supported by the backward (K in {BWD_SUPPORTED_K})")
+    if not isinstance(do, torch.Tensor) or tuple(do.shape) != tuple(v.shape):
+        raise ValueError(f"do must have o's shape {tuple(v.shape)}")
+    _code(do, "do")
+    if dfinal is not None:
+        if tuple(dfinal.shape) != (B, H, K, V) or dfinal.dtype != torch.float32:
+            raise ValueError(f"dfinal must be float32 [{B}, {H}, {K}, {V}]")
+    _check_devices(q, k, v, g, beta, h0, do, dfinal)
+    dev = q.device
+    lib = _lib.load_library()
+    ws_bytes = lib.gdn_bwd_workspace_size(B, T, H, K, V, n_seq or 0)
+    if ws_bytes < 0:
+        raise ValueError(f"backward does not support B={B} T={T} H={H} K={K} V={V}")
+    dq = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=dev)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=dev)
+    dg = torch.empty(g.shape, dtype=g.dtype, device=dev)
+    dbeta = torch.empty(beta.shape, dtype=beta.dtype, device=dev)
+    dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    P = _lib.GdnBwdParams()
+    P.q, P.k, P.v, P.g, P.beta = q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr()
+    P.h0 = h0.data_ptr() if h0 is not None else None
+    P.d_o = do.data_ptr()
+    P.d_final_state = dfinal.data_ptr() if dfinal is not None else None
+    P.dq, P.dk, P.dv, P.dg, P.dbeta = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr()
+    P.dh0 = dh0.data_ptr() if dh0 is not None else None
+    P.workspace, P.workspace_bytes = ws.data_ptr(), ws.numel()
+    for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("dq", dq), ("dk", dk), ("dv", dv)):
+        getattr(P, f"{name}_stride")[:] = t.stride()[:3]
+    for name, t in (("g", g), ("beta", beta), ("dg", dg), ("dbeta", dbeta)):
+        getattr(P, f"{name}_stride")[:] = t.stride()
+    P.h0_stride[:] = h0.stride() if h0 is not None else (0, 0, 0, 0)
+    P.dfs_stride[:] = dfinal.stride() if dfinal is not None else (0, 0, 0, 0)
+    P.dh0_stride[:] = dh0.stride() if dh0 is not None else (0, 0, 0, 0)
+    P.B, P.T, P.H, P.K, P.V = B, T, H, K, V
+    P.scale = float(scale)
+    P.qkv_dtype = _DTYPE_CODE[q.dtype]
+    P.g_dtype = _DTYPE_CODE[g.dtype]
+    P.beta_dtype = _DTYPE_CODE[beta.dtype]
+    P.do_dtype = _DTYPE_CODE[do.dtype]
+    P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
+    with torch.cuda.device(dev):
+        status = lib.gdn_bwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
+    if status != 0:
+        raise RuntimeError(f"gdn_bwd_launch failed ({status}): {_lib.status_string(status)}")
+    return dq, dk, dv, dg, dbeta, dh0
+
+
+class _GdnFunction(torch.autograd.Function):
+    """``_run`` with the HIP backward: o, final_state differentiable in
+    q, k, v, g, beta and h0."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
+                fs_vk, cu_seqlens, o_hf):
+        o, fs = _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
+                     fs_vk, cu_seqlens, o_hf)
+        ctx.save_for_backward(q, k, v, g, beta, h0, cu_seqlens)
+        ctx.scale, ctx.fs_vk, ctx.o_hf = scale, fs_vk, o_hf
+        return o, fs
+
+    @staticmethod
+    def backward(ctx, do, dfs):
+        q, k, v, g, beta, h0, cu = ctx.saved_tensors
+        if do is None:
+            shape = (v.shape[0], v.shape[2], v.shape[1], v.shape[3]) if ctx.o_hf else v.shape
+            do = torch.zeros(shape, dtype=q.dtype, device=q.device)
+        do_bthv = do.transpose(1, 2) if ctx.o_hf else do
+        dfs_kv = None if dfs is None else (dfs.transpose(2, 3) if ctx.fs_vk else dfs)
+        if dfs_kv is not None and dfs_kv.dtype != torch.float32:
+            dfs_kv = dfs_kv.float()
+        need_dh0 = h0 is not None and ctx.needs_input_grad[5]
+        dq, dk, dv, dg, dbeta, dh0 = gdn_bwd(q, k, v, g, beta, h0, do_bthv, dfs_kv, ctx.scale,
+                                             cu_seqlens=cu, need_dh0=need_dh0)
+        return dq, dk, dv, dg, dbeta, dh0, None, None, None, None, None, None, None, None
+
+
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad
+                                           for t in ts)
