@@ -21,13 +21,14 @@
 // (checked against reverse-mode differentiation of the step recurrence
 // gdn_ref.py:3-9).
 //
-// One workgroup per (b, h, 16-column V-slice), 256 threads, everything in
+// One workgroup per (b, h, 16-column V-slice), 512 threads, everything in
 // fp32 in LDS.  Pass 1 walks the chunks forward from h0 and stores the state
 // at each chunk start in the workspace; pass 2 walks them backward carrying
 // dS.  The K-side terms (dq, dk, dbeta, dg) are sums over V, so each slice
 // writes its partial sums to the workspace and a second kernel adds the
-// slices (fixed order: deterministic).  Products are register-tiled FMA
-// loops over LDS (the forward's MFMA pipeline is not reused here).
+// slices (fixed order: deterministic).  Products run on fp32 MFMA with
+// operands read from LDS through accessors (the forward's fp16 pipeline is
+// not reused here).
 
 #include "gdn_fwd_kernel.h"
 
@@ -36,7 +37,9 @@ namespace bwd {
 
 constexpr int C = 32;
 constexpr int BV = 16;
-constexpr int NT = 256;
+constexpr int NT = 512;  // 8 waves: 2 per SIMD (256 VGPRs each)
+constexpr int RL = NT / C;  // lanes per row in row reductions
+static_assert(RL >= 1 && RL <= 64 && (RL & (RL - 1)) == 0, "row lanes");
 
 struct BArgs {
   const void* q;
@@ -100,6 +103,27 @@ __device__ __forceinline__ float ldx(const void* base, int64_t off) {
   else return bf16_bits_to_float(static_cast<const uint16_t*>(base)[off]);
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes of TIn -> 16 / sizeof(TIn) floats.
+template <typename TIn>
+__device__ __forceinline__ void unpack16(const u32x4& r, float* x) {
+  if constexpr (std::is_same<TIn, float>::value) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(r[e]);
+  } else if constexpr (std::is_same<TIn, f16>::value) {
+    const f16x8 h = __builtin_bit_cast(f16x8, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)h[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __uint_as_float(r[e] << 16);
+      x[2 * e + 1] = __uint_as_float(r[e] & 0xffff0000u);
+    }
+  }
+}
+
 template <typename TIn>
 __device__ __forceinline__ void stx(void* base, int64_t off, float x) {
   if constexpr (std::is_same<TIn, float>::value) static_cast<float*>(base)[off] = x;
@@ -118,56 +142,82 @@ __device__ __forceinline__ Seg<KD, FA, FB> seg(FA a, FB b) {
   return Seg<KD, FA, FB>{a, b};
 }
 
-template <int TM, int TN, int NM, int NN, int KD, typename FA, typename FB>
-__device__ __forceinline__ void seg_acc(float (&acc)[TM][TN], int tm, int tn, const Seg<KD, FA, FB>& s) {
-#pragma unroll 4
-  for (int kk = 0; kk < KD; ++kk) {
-    float av[TM], bv[TN];
+// out(m, n, sum over the segments) for an M x N result on the matrix cores
+// (v_mfma_f32_16x16x4_f32, full fp32): 16 x 16 output tiles dealt round-robin
+// to the waves, up to G of them in
+// flight per wave so that their operand loads and MFMA chains overlap.
+// Lane l supplies a(m0 + l % 16, k0 + l / 16) and b(k0 + l / 16, n0 + l % 16)
+// and receives rows m0 + 4 (l / 16) + i, column n0 + l % 16 of a tile.
+template <int G, int KD, typename FA, typename FB>
+__device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], const int (&n0)[G],
+                                         int ng, int r, int kq, const Seg<KD, FA, FB>& s) {
+  static_assert(KD % 4 == 0, "contraction length");
+#pragma unroll 2
+  for (int k0 = 0; k0 < KD; k0 += 4) {
+    float av[G], bv[G];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) av[i] = s.a(tm + i * NM, kk);
+    for (int g = 0; g < G; ++g) {
+      av[g] = g < ng ? s.a(m0[g] + r, k0 + kq) : 0.f;
+      bv[g] = g < ng ? s.b(k0 + kq, n0[g] + r) : 0.f;
+    }
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bv[j] = s.b(kk, tn + j * NN);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+    for (int g = 0; g < G; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[g], bv[g], acc[g], 0, 0, 0);
   }
 }
 
-// out(m, n, sum over the segments) for an M x N result.  Each thread holds a
-// TM x TN tile with interleaved rows (tm + i M/TM) and columns (tn + j N/TN):
-// a wave's lanes read consecutive columns of b and a few rows of a.
-template <int M, int N, int TM, int TN, typename FO, typename... Segs>
-__device__ __forceinline__ void mm(FO&& out, const Segs&... segs) {
-  static_assert(M % TM == 0 && N % TN == 0, "tile");
-  constexpr int NM = M / TM, NN = N / TN;
-  for (int tile = threadIdx.x; tile < NM * NN; tile += NT) {
-    const int tm = tile / NN, tn = tile % NN;
-    float acc[TM][TN];
+template <int M, int N, typename FO, typename... Segs>
+__device__ __forceinline__ void mmx(int tid, FO&& out, const Segs&... segs) {
+  static_assert(M % 16 == 0 && N % 16 == 0, "16 x 16 tiles");
+  constexpr int TNt = N / 16, NTILE = (M / 16) * TNt, NW = NT / 64;
+  constexpr int G = NTILE >= 4 * NW ? 4 : (NTILE >= 2 * NW ? 2 : 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int r = lane & 15, kq = lane >> 4;
+  for (int base = wave; base < NTILE; base += NW * G) {
+    int m0[G], n0[G], ng = 0;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int g = 0; g < G; ++g) {
+      const int tile = base + g * NW;
+      m0[g] = tile < NTILE ? (tile / TNt) * 16 : 0;
+      n0[g] = tile < NTILE ? (tile % TNt) * 16 : 0;
+      if (tile < NTILE) ng = g + 1;
+    }
+    f32x4 acc[G];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = 0.f;
-    (seg_acc<TM, TN, NM, NN>(acc, tm, tn, segs), ...);
+    for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    (seg_mfma<G>(acc, m0, n0, ng, r, kq, segs), ...);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int g = 0; g < G; ++g)
+      if (g < ng) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) out(tm + i * NM, tn + j * NN, acc[i][j]);
+        for (int i = 0; i < 4; ++i) out(m0[g] + 4 * kq + i, n0[g] + r, acc[g][i]);
+      }
   }
+}
+
+// sum_{i < LEN} f(r, i) for row r = tid / RL, computed by the RL lanes of
+// the row (a power of two inside one wave) and returned to all of them.
+template <int LEN, typename F>
+__device__ __forceinline__ float row_sum(int tid, F&& f) {
+  const int r = tid / RL, part = tid % RL;
+  float acc = 0.f;
+  for (int i = part; i < LEN; i += RL) acc += f(r, i);
+#pragma unroll
+  for (int o = RL / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  return acc;
 }
 
 template <typename TIn, int K>
 __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
   using Sm = BSmem<K>;
   constexpr int BD = Sm::BD;
-  // register tiles: C x K, K x BV, C x C, C x BV results over 256 threads
-  constexpr int TKM = (K == 32) ? 2 : 4, TKN = (K == 128) ? 4 : 2;
-  constexpr int SVM = (K == 128) ? 4 : 2, SVN = (K == 32) ? 1 : 2;
   static_assert(K == 32 || K == 64 || K == 128, "K");
 
   __shared__ Sm s;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // The thread index is re-read as an opaque value at the top of every
+  // chunk iteration, so that per-thread LDS addresses are recomputed there
+  // instead of being hoisted out of the chunk loops and held in registers.
+  const int tid0 = threadIdx.x;
+  const int lane = tid0 & 63, wave = tid0 >> 6;
 
   int unit = blockIdx.x;
   if (p.xcd_remap) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
@@ -185,39 +235,96 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
   const int64_t vb = head_base(rs, hi, p.sv) + v0, dob = head_base(rs, hi, p.sdo) + v0;
   const int64_t gb = head_base(rs, hi, p.sg), bb = head_base(rs, hi, p.sb);
   const int64_t dvb = head_base(rs, hi, p.sdv) + v0;
-  // rows of the partial buffers ([nv][R][H](K)): b T + t
+  // rows of the partial buffers ([nv][R][H](K)): b T + t; row t of this
+  // chunk sequence starts at pq_h + t H K (pg_h + t H for the gates)
   const int64_t prow0 = rs.b * p.T + rs.t0;
+  const int64_t hk = (int64_t)p.H * K;
+  float* const pq_h = p.pq + ((int64_t)vs * p.R + prow0) * hk + (int64_t)hi * K;
+  float* const pk_h = p.pk + ((int64_t)vs * p.R + prow0) * hk + (int64_t)hi * K;
+  float* const pg_h = p.pg + ((int64_t)vs * p.R + prow0) * p.H + hi;
+  float* const pb_h = p.pb + ((int64_t)vs * p.R + prow0) * p.H + hi;
   // chunk-start states: slot (chunk) x H x nv x [K][BV]; packed sequence i
   // starts at slot floor(t0 / C) + i, which keeps sequences disjoint.
   const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * ((p.T + C - 1) / C);
   const int64_t ck_stride = (int64_t)p.H * p.nv * K * BV;
   float* const ck0 = p.ckpt + ((slot0 * p.H + hi) * p.nv + vs) * (int64_t)(K * BV);
 
-  auto load_chunk = [&](int c, bool full) __attribute__((always_inline)) {
+  // Chunk rows -> LDS as fp32.  q, k, v move as 16-byte vectors (their rows
+  // are 16-byte aligned: the host checks it); every global load of the
+  // chunk is issued before the first LDS store.
+  constexpr int VEC = 16 / (int)sizeof(TIn);
+  constexpr int RVK = K / VEC, NVK = (C * RVK + NT - 1) / NT;
+  constexpr int RVV = BV / VEC;
+  constexpr int NDO = (C * BV + NT - 1) / NT;
+  static_assert(C * RVV <= NT, "v vectors");
+  const TIn* const qg = static_cast<const TIn*>(p.q) + qb;
+  const TIn* const kg = static_cast<const TIn*>(p.k) + kb;
+  const TIn* const vg = static_cast<const TIn*>(p.v) + vb;
+  auto load_chunk = [&](int tid, int c, bool full) __attribute__((always_inline)) {
     const int t0 = c * C;
-    for (int e = tid; e < C * K; e += NT) {
-      const int t = e / K, kk = e % K;
-      const bool ok = t0 + t < Tn;
-      s.k[t][kk] = ok ? ldx<TIn>(p.k, kb + (int64_t)(t0 + t) * p.sk[1] + kk) : 0.f;
-      if (full) s.q[t][kk] = ok ? ldx<TIn>(p.q, qb + (int64_t)(t0 + t) * p.sq[1] + kk) : 0.f;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    u32x4 rk[NVK], rq[NVK], rv = z;
+    float rdo[NDO], rg = 0.f, rb = 0.f;
+#pragma unroll
+    for (int i = 0; i < NVK; ++i) {
+      const int e = tid + i * NT, t = e / RVK, col = (e % RVK) * VEC;
+      const bool ok = e < C * RVK && t0 + t < Tn;
+      rk[i] = ok ? *reinterpret_cast<const u32x4*>(kg + (int64_t)(t0 + t) * p.sk[1] + col) : z;
+      rq[i] = (ok && full) ? *reinterpret_cast<const u32x4*>(qg + (int64_t)(t0 + t) * p.sq[1] + col) : z;
     }
-    for (int e = tid; e < C * BV; e += NT) {
-      const int t = e / BV, c2 = e % BV;
-      const bool ok = t0 + t < Tn;
-      s.v[t][c2] = ok ? ldx<TIn>(p.v, vb + (int64_t)(t0 + t) * p.sv[1] + c2) : 0.f;
-      if (full)
-        s.dO[t][c2] = ok ? load_scalar(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype) : 0.f;
+    if (tid < C * RVV) {
+      const int t = tid / RVV, col = (tid % RVV) * VEC;
+      if (t0 + t < Tn) rv = *reinterpret_cast<const u32x4*>(vg + (int64_t)(t0 + t) * p.sv[1] + col);
+    }
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int e = tid + i * NT, t = e / BV, c2 = e % BV;
+      rdo[i] = (full && e < C * BV && t0 + t < Tn)
+                   ? load_scalar(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype)
+                   : 0.f;
+    }
+    if (tid < C && t0 + tid < Tn) {
+      rg = load_scalar(p.g, gb + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
+      rb = load_scalar(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
+    }
+#pragma unroll
+    for (int i = 0; i < NVK; ++i) {
+      const int e = tid + i * NT, t = e / RVK, col = (e % RVK) * VEC;
+      if (e < C * RVK) {
+        float x[VEC];
+        unpack16<TIn>(rk[i], x);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) s.k[t][col + j] = x[j];
+        if (full) {
+          unpack16<TIn>(rq[i], x);
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) s.q[t][col + j] = x[j];
+        }
+      }
+    }
+    if (tid < C * RVV) {
+      const int t = tid / RVV, col = (tid % RVV) * VEC;
+      float x[VEC];
+      unpack16<TIn>(rv, x);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) s.v[t][col + j] = x[j];
+    }
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < NDO; ++i) {
+        const int e = tid + i * NT;
+        if (e < C * BV) s.dO[e / BV][e % BV] = rdo[i];
+      }
     }
     if (tid < C) {
-      const bool ok = t0 + tid < Tn;
-      s.gl[tid] = ok ? load_scalar(p.g, gb + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype) : 0.f;
-      s.bt[tid] = ok ? load_scalar(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0.f;
+      s.gl[tid] = rg;
+      s.bt[tid] = rb;
     }
   };
 
   // Gates, M, K K^T (and Q K^T), A, T = (I + A)^-1, W, U, u.  Leaves
   // U in u2.  Starts and ends on a barrier.
-  auto chunk_forward = [&](bool full) __attribute__((always_inline)) {
+  auto chunk_forward = [&](int tid, bool full) __attribute__((always_inline)) {
     if (tid < C) {
       float bt = 0.f, bc = 0.f;
       for (int j = 0; j < C; ++j) {
@@ -229,10 +336,10 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
       s.D[tid] = expf(bc - bt);
       if (tid == C - 1) s.gC = expf(bc);
     }
-    mm<C, C, 2, 2>([&](int m, int n, float x) { s.kk[m][n] = x; },
+    mmx<C, C>(tid, [&](int m, int n, float x) { s.kk[m][n] = x; },
                    seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
     if (full)
-      mm<C, C, 2, 2>([&](int m, int n, float x) { s.qk[m][n] = x; },
+      mmx<C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
                      seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
     __syncthreads();
     for (int e = tid; e < C * C; e += NT) {
@@ -243,7 +350,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
     }
     __syncthreads();
     if (tid < C) {
-      // column tid of T by forward substitution
+      // column tid of T by forward substitution, the column in registers
       const int c = tid;
       float col[C];
 #pragma unroll
@@ -252,76 +359,96 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
 #pragma unroll
         for (int j = 0; j < i; ++j) x = __builtin_fmaf(-s.a[i][j], col[j], x);
         col[i] = x;
-        s.t[i][c] = x;
       }
+#pragma unroll
+      for (int i = 0; i < C; ++i) s.t[i][c] = col[i];
     }
     __syncthreads();
-    mm<C, K, TKM, TKN>([&](int m, int n, float x) { s.w[m][n] = x; },
+    mmx<C, K>(tid, [&](int m, int n, float x) { s.w[m][n] = x; },
                        seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                               [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.u2[m][n] = x; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
                     seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                            [&](int kk, int n) { return s.bt[kk] * s.v[kk][n]; }));
     __syncthreads();
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.u[m][n] = s.u2[m][n] - x; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u[m][n] = s.u2[m][n] - x; },
                     seg<K>([&](int m, int kk) { return s.w[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
     __syncthreads();
   };
 
   // ---------------- pass 1: chunk-start states ----------------
-  for (int e = tid; e < K * BV; e += NT) {
+  for (int e = tid0; e < K * BV; e += NT) {
     const int kk = e / BV, c2 = e % BV;
     s.S[kk][c2] = p.h0 ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]] : 0.f;
   }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
     float* ck = ck0 + c * ck_stride;
-    for (int e = tid; e < K * BV; e += NT) ck[e] = s.S[e / BV][e % BV];
-    load_chunk(c, false);
+    for (int e = 4 * tid; e < K * BV; e += 4 * NT) {
+      const int kk = e / BV, c2 = e % BV;
+      *reinterpret_cast<f32x4*>(ck + e) = f32x4{s.S[kk][c2], s.S[kk][c2 + 1], s.S[kk][c2 + 2], s.S[kk][c2 + 3]};
+    }
+    load_chunk(tid, c, false);
     __syncthreads();
-    chunk_forward(false);
-    mm<K, BV, SVM, SVN>([&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
+    chunk_forward(tid, false);
+    mmx<K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
                         seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
                                [&](int kk, int n) { return s.u[kk][n]; }));
     __syncthreads();
   }
 
   // ---------------- pass 2: gradients, last chunk first ----------------
-  for (int e = tid; e < K * BV; e += NT) {
+  for (int e = tid0; e < K * BV; e += NT) {
     const int kk = e / BV, c2 = e % BV;
     s.dS[kk][c2] =
         p.dfs ? p.dfs[bi * p.sdfs[0] + hi * p.sdfs[1] + kk * p.sdfs[2] + (v0 + c2) * p.sdfs[3]] : 0.f;
   }
   float* const xs = &s.x[0][0];
   for (int c = nch - 1; c >= 0; --c) {
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
     const int t0 = c * C;
     const float* ck = ck0 + c * ck_stride;
-    for (int e = tid; e < K * BV; e += NT) s.S[e / BV][e % BV] = ck[e];
-    load_chunk(c, true);
+    {
+      constexpr int NCK = (K * BV / 4 + NT - 1) / NT;
+      f32x4 r4[NCK];
+#pragma unroll
+      for (int i = 0; i < NCK; ++i)
+        if (4 * (tid + i * NT) < K * BV) r4[i] = *reinterpret_cast<const f32x4*>(ck + 4 * (tid + i * NT));
+#pragma unroll
+      for (int i = 0; i < NCK; ++i) {
+        const int e = 4 * (tid + i * NT), kk = e / BV, c2 = e % BV;
+        if (e < K * BV) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s.S[kk][c2 + j] = r4[i][j];
+        }
+      }
+    }
+    load_chunk(tid, c, true);
     __syncthreads();
-    chunk_forward(true);
+    chunk_forward(tid, true);
 
     // K dS' -> u2 (U is no longer needed), Q S -> qs
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.u2[m][n] = x; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
                     seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.dS[kk][n]; }));
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.qs[m][n] = x; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.qs[m][n] = x; },
                     seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
     __syncthreads();
     // du = scale P^T dO + D o K dS';  dQK = M o (scale dO u^T)
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.du[m][n] = scale * x + s.D[m] * s.u2[m][n]; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.du[m][n] = scale * x + s.D[m] * s.u2[m][n]; },
                     seg<C>([&](int m, int kk) { return s.m[kk][m] * s.qk[kk][m]; },
                            [&](int kk, int n) { return s.dO[kk][n]; }));
-    mm<C, C, 2, 2>([&](int m, int n, float x) { s.y[m][n] = scale * s.m[m][n] * x; },
+    mmx<C, C>(tid, [&](int m, int n, float x) { s.y[m][n] = scale * s.m[m][n] * x; },
                    seg<BV>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.u[n][kk]; }));
-    if (tid < C) {
-      float dd = 0.f, dg = 0.f;
-#pragma unroll
-      for (int c2 = 0; c2 < BV; ++c2) {
-        dd = __builtin_fmaf(s.u[tid][c2], s.u2[tid][c2], dd);
-        dg = __builtin_fmaf(s.dO[tid][c2], s.qs[tid][c2], dg);
+    {
+      const float dd = row_sum<BV>(tid, [&](int r, int i) { return s.u[r][i] * s.u2[r][i]; });
+      const float dg = row_sum<BV>(tid, [&](int r, int i) { return s.dO[r][i] * s.qs[r][i]; });
+      if (tid % RL == 0) {
+        s.dD[tid / RL] = dd;
+        s.dgam[tid / RL] = scale * dg;
       }
-      s.dD[tid] = dd;
-      s.dgam[tid] = scale * dg;
     }
     {
       // dgam_C = <dS', S>
@@ -337,38 +464,39 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
       s.dgC = r;
     }
     // dW = -du S^T
-    mm<C, K, TKM, TKN>([&](int m, int n, float x) { s.dw[m][n] = -x; },
+    mmx<C, K>(tid, [&](int m, int n, float x) { s.dw[m][n] = -x; },
                        seg<BV>([&](int m, int kk) { return s.du[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
     __syncthreads();
     // dT = du (beta V)^T + dW (beta gam K)^T;  dW~ = T^T dW -> x;  dU~ = T^T du -> u2
-    mm<C, C, 2, 2>([&](int m, int n, float x) { s.dt[m][n] = x; },
+    mmx<C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = x; },
                    seg<BV>([&](int m, int kk) { return s.du[m][kk]; },
                            [&](int kk, int n) { return s.bt[n] * s.v[n][kk]; }),
                    seg<K>([&](int m, int kk) { return s.dw[m][kk]; },
                           [&](int kk, int n) { return s.bt[n] * s.gam[n] * s.k[n][kk]; }));
-    mm<C, K, TKM, TKN>([&](int m, int n, float x) { s.x[m][n] = x; },
+    mmx<C, K>(tid, [&](int m, int n, float x) { s.x[m][n] = x; },
                        seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dw[kk][n]; }));
-    mm<C, BV, 2, 1>([&](int m, int n, float x) { s.u2[m][n] = x; },
+    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
                     seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
     __syncthreads();
     // Z = T^T dT;  dv = beta dU~;  dbeta, dgam through W~ and U~
-    mm<C, C, 2, 2>([&](int m, int n, float x) { s.z[m][n] = x; },
+    mmx<C, C>(tid, [&](int m, int n, float x) { s.z[m][n] = x; },
                    seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dt[kk][n]; }));
     for (int e = tid; e < C * BV; e += NT) {
       const int t = e / BV, c2 = e % BV;
       if (t0 + t < Tn) stx<TIn>(p.dv, dvb + (int64_t)(t0 + t) * p.sdv[1] + c2, s.bt[t] * s.u2[t][c2]);
     }
-    if (tid < C) {
-      float kw = 0.f, vu = 0.f;
-      for (int kk = 0; kk < K; ++kk) kw = __builtin_fmaf(s.k[tid][kk], s.x[tid][kk], kw);
-#pragma unroll
-      for (int c2 = 0; c2 < BV; ++c2) vu = __builtin_fmaf(s.v[tid][c2], s.u2[tid][c2], vu);
-      s.dbt[tid] = vu + s.gam[tid] * kw;
-      s.dgam[tid] += s.bt[tid] * kw;
+    {
+      const float kw = row_sum<K>(tid, [&](int r, int i) { return s.k[r][i] * s.x[r][i]; });
+      const float vu = row_sum<BV>(tid, [&](int r, int i) { return s.v[r][i] * s.u2[r][i]; });
+      if (tid % RL == 0) {
+        const int r = tid / RL;
+        s.dbt[r] = vu + s.gam[r] * kw;
+        s.dgam[r] += s.bt[r] * kw;
+      }
     }
     __syncthreads();
     // dA = -tril_-1(Z T^T) -> dt
-    mm<C, C, 2, 2>([&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
+    mmx<C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
                    seg<C>([&](int m, int kk) { return s.z[m][kk]; }, [&](int kk, int n) { return s.t[n][kk]; }));
     __syncthreads();
     // dKK = dA o beta_t M -> z;  dbeta += sum_j dA M KK
@@ -376,44 +504,44 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
       const int t = e / C, j = e % C;
       s.z[t][j] = j < t ? s.dt[t][j] * s.bt[t] * s.m[t][j] : 0.f;
     }
-    if (tid < C) {
-      float acc = 0.f;
-      for (int j = 0; j < C; ++j) acc = __builtin_fmaf(s.dt[tid][j] * s.m[tid][j], s.kk[tid][j], acc);
-      s.dbt[tid] += acc;
-      // db_t through gam, D, M (dQK o QK) and A (dA o A)
-      float d = s.dgam[tid] * s.gam[tid] - s.dD[tid] * s.D[tid];
-      for (int j = 0; j < C; ++j) {
-        d += s.y[tid][j] * s.qk[tid][j] - s.y[j][tid] * s.qk[j][tid];
-        d += s.dt[tid][j] * s.a[tid][j] - s.dt[j][tid] * s.a[j][tid];
+    {
+      const float am = row_sum<C>(tid, [&](int r, int j) { return s.dt[r][j] * s.m[r][j] * s.kk[r][j]; });
+      // db_t through M (dQK o QK) and A (dA o A): row sums minus column sums
+      const float mt = row_sum<C>(tid, [&](int r, int j) {
+        return s.y[r][j] * s.qk[r][j] - s.y[j][r] * s.qk[j][r] + s.dt[r][j] * s.a[r][j] -
+               s.dt[j][r] * s.a[j][r];
+      });
+      const float dd = row_sum<C>(tid, [&](int r, int j) { return s.dD[j] * s.D[j]; });
+      if (tid % RL == 0) {
+        const int r = tid / RL;
+        s.dbt[r] += am;
+        // ... and through gam, D and (last row) gam_C and every D_j
+        float d = mt + s.dgam[r] * s.gam[r] - s.dD[r] * s.D[r];
+        if (r == C - 1) d += dd + s.dgC * s.gC;
+        s.db[r] = d;
       }
-      if (tid == C - 1) {
-        float e2 = s.dgC * s.gC;
-        for (int j = 0; j < C; ++j) e2 = __builtin_fmaf(s.dD[j], s.D[j], e2);
-        d += e2;
-      }
-      s.db[tid] = d;
     }
     __syncthreads();
     if (tid < C && t0 + tid < Tn) {
       float acc = 0.f;
       for (int j = tid; j < C; ++j) acc += s.db[j];
-      const int64_t r = ((int64_t)vs * p.R + prow0 + t0 + tid) * p.H + hi;
-      p.pg[r] = acc;
-      p.pb[r] = s.dbt[tid];
+      const int64_t r = (int64_t)(t0 + tid) * p.H;
+      pg_h[r] = acc;
+      pb_h[r] = s.dbt[tid];
     }
     // dq (partial) = dQK K + scale gam dO S^T
-    mm<C, K, TKM, TKN>(
-        [&](int m, int n, float x) {
-          if (t0 + m < Tn) p.pq[(((int64_t)vs * p.R + prow0 + t0 + m) * p.H + hi) * K + n] = x;
+    mmx<C, K>(
+        tid, [&](int m, int n, float x) {
+          if (t0 + m < Tn) pq_h[(int64_t)(t0 + m) * hk + n] = x;
         },
         seg<C>([&](int m, int kk) { return s.y[m][kk]; }, [&](int kk, int n) { return s.k[kk][n]; }),
         seg<BV>([&](int m, int kk) { return scale * s.gam[m] * s.dO[m][kk]; },
                 [&](int kk, int n) { return s.S[n][kk]; }));
     // dk (partial) = dQK^T Q + D u dS'^T + (dKK + dKK^T) K + beta gam dW~
-    mm<C, K, TKM, TKN>(
-        [&](int m, int n, float x) {
+    mmx<C, K>(
+        tid, [&](int m, int n, float x) {
           if (t0 + m < Tn)
-            p.pk[(((int64_t)vs * p.R + prow0 + t0 + m) * p.H + hi) * K + n] =
+            pk_h[(int64_t)(t0 + m) * hk + n] =
                 x + s.bt[m] * s.gam[m] * s.x[m][n];
         },
         seg<C>([&](int m, int kk) { return s.y[kk][m]; }, [&](int kk, int n) { return s.q[kk][n]; }),
@@ -421,7 +549,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
         seg<C>([&](int m, int kk) { return s.z[m][kk] + s.z[kk][m]; }, [&](int kk, int n) { return s.k[kk][n]; }));
     __syncthreads();
     // dS = scale Q^T diag(gam) dO + gam_C dS' - W^T du -> x as [K][BD]
-    mm<K, BV, SVM, SVN>([&](int m, int n, float x) { xs[m * BD + n] = x + s.gC * s.dS[m][n]; },
+    mmx<K, BV>(tid, [&](int m, int n, float x) { xs[m * BD + n] = x + s.gC * s.dS[m][n]; },
                         seg<C>([&](int m, int kk) { return scale * s.gam[kk] * s.q[kk][m]; },
                                [&](int kk, int n) { return s.dO[kk][n]; }),
                         seg<C>([&](int m, int kk) { return -s.w[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
@@ -430,7 +558,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
   }
   __syncthreads();
   if (p.dh0 != nullptr) {
-    for (int e = tid; e < K * BV; e += NT) {
+    for (int e = tid0; e < K * BV; e += NT) {
       const int kk = e / BV, c2 = e % BV;
       p.dh0[bi * p.sdh0[0] + hi * p.sdh0[1] + kk * p.sdh0[2] + (v0 + c2) * p.sdh0[3]] = s.dS[kk][c2];
     }
