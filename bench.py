@@ -11,9 +11,10 @@ A "step" is one ``gdn_fwd`` call over the whole batch (one kernel launch).
 Extra fields report the C=64 variant, a cold-cache timing (caches flushed
 with a 512 MiB write between launches, each launch timed with its own
 events) and the fused input preparation (``gdn_prep``: L2-norm of q and k,
-sigmoid beta, logsigmoid g) on the same shapes.  ``--config`` selects
-another BASELINE config for exploration and ``--workload prep`` times only
-the input preparation; the driver's line is the default.
+sigmoid beta, logsigmoid g) and the backward (``gdn_bwd``) on the same
+shapes.  ``--config`` selects another BASELINE config for exploration;
+``--workload prep`` / ``--workload bwd`` time only the input preparation /
+the backward; the driver's line is the default.
 """
 
 from __future__ import annotations
@@ -122,6 +123,23 @@ def time_prep(pkg, B, T, H, K, dtype, steps, warmup):
             "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 5)}
 
 
+def bwd_bytes(B, T, H, K, V, in_bytes):
+    """Algorithmic bytes of one backward: q, k, v, dO read and dq, dk, dv
+    written in the input dtype, g, beta read and dg, dbeta written in fp32."""
+    return B * T * H * (in_bytes * (4 * K + 3 * V) + 16)
+
+
+def time_bwd(pkg, q, k, v, g, beta, h0, steps, warmup):
+    do = torch.randn(v.shape, generator=torch.Generator().manual_seed(1)).to(v.dtype).to(v.device)
+    ms = time_steps(lambda: pkg.gdn_bwd(q, k, v, g, beta, h0, do, None, need_dh0=h0 is not None),
+                    steps, warmup)
+    B, T, H, K = q.shape
+    nb = bwd_bytes(B, T, H, K, v.shape[-1], q.element_size())
+    gbs = nb / (ms / 1e3) / 1e9
+    return {"ms_per_step": round(ms, 5), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+            "bytes_per_launch": nb, "achieved_gbs": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 6)}
+
+
 def time_steps(fn, steps, warmup):
     """Warm up, then time exactly ``steps`` back-to-back calls between two
     events on the current stream (the stream the kernel is launched on)."""
@@ -212,8 +230,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--block-v", type=int, default=None)
-    ap.add_argument("--workload", default="fwd", choices=["fwd", "prep"],
-                    help="fwd: the GDN forward (default); prep: only the fused input preparation")
+    ap.add_argument("--workload", default="fwd", choices=["fwd", "prep", "bwd"],
+                    help="fwd: the GDN forward (default); prep: only the fused input "
+                         "preparation; bwd: only the backward (gdn_bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -257,6 +276,18 @@ def main():
                          "unit": "GB/s", "frac": r["frac"], "traffic": None}}), flush=True)
         return
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
+    if args.workload == "bwd":
+        r = time_bwd(pkg, q, k, v, g, beta, h0, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "GDN bwd tokens/sec (dq, dk, dv, dg, dbeta from dO)",
+            "value": r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": DTYPE_NAME[dtype],
+            "data": "synthetic (BASELINE.json recipe, seed 0)",
+            "config": {"workload": f"gdn_bwd {args.config}", "B": B, "T": T, "H": H, "K": K, "V": V},
+            "roofline": {"bound": "hbm", "achieved": r["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": r["frac"], "traffic": None}}), flush=True)
+        return
 
     def step(chunk=C):
         return pkg.gdn_fwd(q, k, v, g, beta, h0, scale=1.0, chunk_size=chunk, block_v=args.block_v)
@@ -314,6 +345,7 @@ def main():
         torch.cuda.synchronize()
         line["peak_hbm_delta_bytes"] = torch.cuda.max_memory_allocated() - base
         line["prep"] = time_prep(pkg, B, T, H, K, dtype, max(5, args.steps // 2), 5)
+        line["bwd"] = time_bwd(pkg, q, k, v, g, beta, h0, 5, 1)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(B, T, H, K, V, dtype, C)
