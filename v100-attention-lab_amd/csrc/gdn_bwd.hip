@@ -96,13 +96,6 @@ struct alignas(16) BSmem {
 };
 static_assert(C * (128 + 1) >= 128 * (BV + 1), "x holds a K x BD tile");
 
-template <typename TIn>
-__device__ __forceinline__ float ldx(const void* base, int64_t off) {
-  if constexpr (std::is_same<TIn, float>::value) return static_cast<const float*>(base)[off];
-  else if constexpr (std::is_same<TIn, f16>::value) return (float)static_cast<const f16*>(base)[off];
-  else return bf16_bits_to_float(static_cast<const uint16_t*>(base)[off]);
-}
-
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16 bytes of TIn -> 16 / sizeof(TIn) floats.
