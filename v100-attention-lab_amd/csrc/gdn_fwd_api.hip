@@ -99,7 +99,7 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
 
-  KArgs a;
+  KArgs a = {};
   a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
   a.o = P.o; a.fs = P.final_state;
   for (int d = 0; d < 3; ++d) {
