@@ -171,8 +171,9 @@ int gdn_prep_launch(const GdnPrepParams* params, void* stream);
  * is checked against reverse-mode differentiation of that recurrence.
  *   - Same tensors, strides and varlen convention as GdnFwdParams; the
  *     chunk length is 32.  K in {32, 64, 128}; V a multiple of 16.
- *   - dq, dk, dv take q's dtype layout rules (16-byte rows not required);
- *     dg, dbeta any strides; dh0 [B,H,K,V] fp32 (nullable: not written).
+ *   - q, k, v: 16-byte aligned rows as for the forward.  dq, dk, dv (q's
+ *     dtype), dg, dbeta (g's / beta's dtypes): any strides.  dh0 [B,H,K,V]
+ *     fp32 (nullable: not written).
  *   - d_final_state nullable (zero).  h0 nullable (zero).
  *   - workspace: device memory of at least gdn_bwd_workspace_size(...)
  *     bytes, 256-byte aligned, owned by the caller; its contents need no

@@ -320,6 +320,7 @@ def _bwd_params(L, **kw):
     (dict(K=256), 1003), (dict(V=24), 1002), (dict(B=0), 1002), (dict(do_dtype=4), 1005),
     (dict(d_o=None), 1001), (dict(dg=None), 1001), (dict(workspace=None), 1006),
     (dict(workspace=0x100010), 1006), (dict(workspace_bytes=1024), 1006),
+    (dict(q=0x1008), 1004),
 ])
 def test_bwd_rejects_bad_arguments(lib, kw, code):
     from importlib import import_module

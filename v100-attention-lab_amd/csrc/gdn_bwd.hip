@@ -659,6 +659,17 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
                   P.beta == nullptr || P.d_o == nullptr || P.dq == nullptr || P.dk == nullptr ||
                   P.dv == nullptr || P.dg == nullptr || P.dbeta == nullptr))
     return GDN_ERR_NULL_POINTER;
+  // q, k, v rows are read as 16-byte vectors, as in the forward
+  if (P.T > 0) {
+    const int eb = elem_bytes(P.qkv_dtype);
+    const void* ptrs[3] = {P.q, P.k, P.v};
+    const int64_t* strides[3] = {P.q_stride, P.k_stride, P.v_stride};
+    for (int i = 0; i < 3; ++i) {
+      if (reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) return GDN_ERR_MISALIGNED;
+      for (int d = 0; d < 3; ++d)
+        if ((strides[i][d] * eb) % 16 != 0) return GDN_ERR_MISALIGNED;
+    }
+  }
   const int64_t units = (int64_t)P.B * P.H * (P.V / bwd::BV);
   if (units > 0x7fffffffLL || (int64_t)P.B * P.T * P.H * P.K >= (1LL << 40)) return GDN_ERR_BAD_SHAPE;
   // B is the number of sequences when cu_seqlens is given (one packed batch)
