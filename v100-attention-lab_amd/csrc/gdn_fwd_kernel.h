@@ -474,7 +474,72 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
     __syncthreads();
 
     // ---------------- P3: T = (I + A)^{-1} by forward substitution ----------
-    if (wave == 0) {
+    if constexpr (C == 64) {
+      // Blocked: T = [[T11, 0], [T21, T22]] with T11 = (I + A11)^{-1} and
+      // T22 = (I + A22)^{-1} solved at the same time by waves 0 and 1 (lane c
+      // owns column c of its block), then T21 = -T22 (A21 T11).  Every block
+      // lands in place in s.a (fp32); the unused upper block holds A21 T11.
+      constexpr int H2 = 32;
+      if (wave < 2 && lane < H2) {
+        const int o = H2 * wave;
+        float tc[H2];
+#pragma unroll
+        for (int i = 0; i < H2; ++i) {
+          float acc = (lane == i) ? 1.f : 0.f;
+#pragma unroll
+          for (int j4 = 0; j4 < i; j4 += 4) {
+            const f32x4 a4 = *reinterpret_cast<const f32x4*>(&s.a[(o + i) * C + o + j4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (j4 + e < i) acc = fmaf(-a4[e], tc[j4 + e], acc);
+          }
+          tc[i] = acc;
+        }
+        // the block's A entries are no longer read: overwrite them with T
+#pragma unroll
+        for (int i = 0; i < H2; ++i) s.a[(o + i) * C + o + lane] = tc[i];
+      }
+      __syncthreads();
+      // 32 x 32 x 32 products in fp32 on the matrix cores
+      // (v_mfma_f32_16x16x4_f32): wave w makes the 16 x 16 tile (w / 2, w % 2).
+      // Lane (n, gq) supplies row n of the left operand and column n of the
+      // right one at contraction index 4 k4 + gq, and receives rows 4 gq + i.
+      static_assert(kWaves == 4, "one 16 x 16 tile per wave");
+      const int tr = 16 * (wave >> 1), tcl = 16 * (wave & 1);
+      // X = A21 T11 -> upper block (rows 0..31, columns 32..63)
+      {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k4 = 0; k4 < H2 / 4; ++k4) {
+          const int kk = 4 * k4 + gq;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.a[(H2 + tr + n) * C + kk], s.a[kk * C + tcl + n],
+                                                     acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.a[(tr + 4 * gq + i) * C + H2 + tcl + n] = acc[i];
+      }
+      __syncthreads();
+      // T21 = -T22 X -> lower-left block (A21 is no longer needed)
+      {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k4 = 0; k4 < H2 / 4; ++k4) {
+          const int kk = 4 * k4 + gq;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.a[(H2 + tr + n) * C + H2 + kk],
+                                                     s.a[kk * C + H2 + tcl + n], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.a[(H2 + tr + 4 * gq + i) * C + tcl + n] = -acc[i];
+      }
+      __syncthreads();
+      for (int e = tid; e < C * C; e += kThreads) {
+        const int i = e / C, c = e % C;
+        const float t = c <= i ? s.a[i * C + c] : 0.f;
+        const float ru = s.beta[c];
+        s.tw[i * SC + c] = (TOp)(t * (-ru * s.eb[c]));
+        s.tu[i * SC + c] = (TOp)(t * ru);
+      }
+    } else if (wave == 0) {
       // Lane c owns column c of T: T[i][c] = [i == c] - sum_{j<i} A[i][j] T[j][c].
       float tc[C];
 #pragma unroll
