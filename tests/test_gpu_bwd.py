@@ -162,3 +162,28 @@ def test_bwd_full_size_one_head(pkg, cuda):
     mine = (sel(got[0].cpu()), sel(got[1].cpu()), sel(got[2].cpu()), sel(got[4].cpu()),
             sel(got[3].cpu()), None)
     _compare(mine, want, torch.float16, "cfg2 head (1,5)")
+
+
+def test_autograd_fla_varlen_bf16(pkg, cuda):
+    """loss.backward() through FLA's varlen call (bf16, initial_state and
+    final-state gradient): every sequence's gradients match the oracle's."""
+    lens = [45, 70, 13]
+    H, K, V = 2, 64, 32
+    T = sum(lens)
+    q, k, v, g, beta, _, do, _ = _inputs(1, T, H, K, V, torch.bfloat16, seed=21)
+    gen = torch.Generator().manual_seed(22)
+    h0 = 0.1 * torch.randn(len(lens), H, K, V, generator=gen)
+    dfin = torch.randn(len(lens), H, K, V, generator=gen)
+    cu = torch.tensor([0, 45, 115, 128], dtype=torch.int64)
+    leaves = [t.to(cuda).requires_grad_(True) for t in (q, k, v, g, beta, h0)]
+    print("[bwd] FLA varlen bf16 autograd", flush=True)
+    o, fs = pkg.chunk_gated_delta_rule(*leaves[:5], scale=0.8, initial_state=leaves[5],
+                                       output_final_state=True, cu_seqlens=cu.to(cuda))
+    ((o.float() * do.to(cuda).float()).sum() + (fs * dfin.to(cuda)).sum()).backward()
+    for i, (a, b) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+        sl = lambda t: t[:, a:b]
+        want = ref.recurrent_grads(sl(q), sl(k), sl(v), sl(beta), sl(g), h0[i:i + 1], sl(do),
+                                   dfin[i:i + 1], scale=0.8)
+        got = (sl(leaves[0].grad.cpu()), sl(leaves[1].grad.cpu()), sl(leaves[2].grad.cpu()),
+               sl(leaves[4].grad.cpu()), sl(leaves[3].grad.cpu()), leaves[5].grad[i:i + 1].cpu())
+        _compare(got, want, torch.bfloat16, f"varlen seq {i}")
