@@ -337,6 +337,39 @@ constexpr int pipe_waves() {
   return 9 + BV / 16;
 }
 
+enum PipeRole { R_SCAN, R_OUT, R_L, R_E, R_S, R_LOAD, R_IDLE };
+
+constexpr int rc(int role, int idx = 0) { return role << 2 | idx; }
+constexpr uint64_t pack_roles(const int (&c)[9]) {
+  uint64_t x = 0;
+  for (int i = 0; i < 9; ++i) x |= uint64_t(c[i]) << (6 * i);
+  return x;
+}
+
+// Roles of waves NSW .. NSW + 8 (role << 2 | index, six bits each).  E0 and
+// E1 work in alternate iterations, SCAN, OUT, L and S0-S2 every iteration,
+// the loaders briefly.  Both orders put E0 / E1 on one SIMD, pair the
+// every-iteration roles two per SIMD, and let the loaders fill third slots;
+// which roles pair up matters (OUT or L beside a SCAN wave, or OUT beside L,
+// is slow), so each BV has the pairing that timed fastest with o in the
+// input dtype:
+//   BV = 16  SIMD0 SCAN S1 LD0 | SIMD1 S0 OUT LD1 | SIMD2 E0 E1 | SIMD3 L S2
+//            (cfg2: 130 us; the seven other orders timed 132-145 us)
+//   BV = 32  SIMD0 SCAN0 E0 E1 | SIMD1 SCAN1 S0 LD0 | SIMD2 OUT S1 LD1 |
+//            SIMD3 L S2  (cfg4: 225.5 us; the BV = 16 pairing costs 275 us)
+template <int BV>
+struct RoleOrder;
+template <>
+struct RoleOrder<16> {
+  static constexpr uint64_t packed = pack_roles({rc(R_S, 0), rc(R_E, 0), rc(R_L), rc(R_S, 1), rc(R_OUT),
+                                                 rc(R_E, 1), rc(R_S, 2), rc(R_LOAD, 0), rc(R_LOAD, 1)});
+};
+template <>
+struct RoleOrder<32> {
+  static constexpr uint64_t packed = pack_roles({rc(R_OUT), rc(R_L), rc(R_E, 0), rc(R_S, 0), rc(R_S, 1),
+                                                 rc(R_S, 2), rc(R_E, 1), rc(R_LOAD, 0), rc(R_LOAD, 1)});
+};
+
 template <typename TIn, int K, int BV>
 __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(const KArgs p) {
   using M = Mma<f16>;
@@ -398,26 +431,17 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   // Fragment (row r, 16-byte piece c) of a staged tile.
   auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int c) { return tile[r][swz<K>(r, c)]; };
 
-  // Roles in wave order; waves map to SIMDs round-robin (wave % 4).  E0 and
-  // E1 work in alternate iterations, so the order puts them on one SIMD and
-  // spreads the every-iteration roles (SCAN, OUT, L, S0-S2) two per SIMD
-  // elsewhere, loaders filling the third slots: measured against the
-  // previous order, 135.6 -> 133.7 us at BV = 16 and 220.4 -> 214.3 us at
-  // BV = 32 (cfg2 / cfg4).
-  enum { R_SCAN, R_OUT, R_L, R_E, R_S, R_LOAD, R_IDLE };
+  // Roles in wave order; waves map to SIMDs round-robin (wave % 4), the NSW
+  // scan waves first.  The order of the other nine decides which roles
+  // share a SIMD's issue slots, and the best one depends on BV (RoleOrder).
   int role = R_IDLE, ridx = 0;
-  {
-    const int w = wave - NSW;
-    if (wave < NSW) { role = R_SCAN; ridx = wave; }
-    else if (w == 0) { role = R_S; ridx = 0; }
-    else if (w == 1) { role = R_E; ridx = 0; }
-    else if (w == 2) role = R_L;
-    else if (w == 3) { role = R_S; ridx = 1; }
-    else if (w == 4) role = R_OUT;
-    else if (w == 5) { role = R_E; ridx = 1; }
-    else if (w == 6) { role = R_S; ridx = 2; }
-    else if (w == 7) { role = R_LOAD; ridx = 0; }
-    else if (w == 8) { role = R_LOAD; ridx = 1; }
+  if (wave < NSW) {
+    role = R_SCAN;
+    ridx = wave;
+  } else if (wave < NSW + 9) {
+    const int c = int(RoleOrder<BV>::packed >> (6 * (wave - NSW))) & 63;
+    role = c >> 2;
+    ridx = c & 3;
   }
 
   // Each role runs its own copy of the iteration loop, so registers that one
