@@ -19,16 +19,28 @@
 //   db: through gam, gam_C, D, M and A; dg = reverse cumsum of db
 //   dS  = scale Q^T diag(gam) dO + gam_C dS' - W^T du   (dS' of the chunk before)
 // (checked against reverse-mode differentiation of the step recurrence
-// gdn_ref.py:3-9).
+// gdn_ref.py:3-9).  Two row sums are taken from C x K products instead of
+// C x V ones: u_t.(K dS')_t = k_t.(u dS'^T)_t and dO_t.(Q S)_t =
+// q_t.(dO S^T)_t.
 //
-// One workgroup per (b, h, 16-column V-slice), 512 threads, everything in
-// fp32 in LDS.  Pass 1 walks the chunks forward from h0 and stores the state
-// at each chunk start in the workspace; pass 2 walks them backward carrying
-// dS.  The K-side terms (dq, dk, dbeta, dg) are sums over V, so each slice
-// writes its partial sums to the workspace and a second kernel adds the
-// slices (fixed order: deterministic).  Products run on fp32 MFMA with
-// operands read from LDS through accessors (the forward's fp16 pipeline is
-// not reused here).
+// Only S (forward) and dS (backward) carry from chunk to chunk, and each
+// needs a few products per chunk; everything else is independent per chunk.
+// So the backward is three launches, all fp32 on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32):
+//   1. prep_kernel, one workgroup per (chunk, head): gates, K K^T, P, T and
+//      W, written once to a per-chunk record (the state-independent half of
+//      the chunk's forward, shared by every V-slice below);
+//   2. recur_kernel, one workgroup per (sequence, head, 16-column V slice)
+//      and direction, both directions in one launch: the forward walk stores
+//      each chunk's start state S and u; the backward walk stores each
+//      chunk's dS' and du and finally dh0;
+//   3. grad_kernel, one workgroup per (chunk, head) over all of V: every
+//      gradient of the chunk from the stored S, dS', u, du and the record,
+//      written directly in the output dtypes (V is walked in 16-column steps
+//      with the C x K products held in MFMA accumulators).
+// Packed sequences (cu_seqlens): sequence i owns chunk slots floor(t0 / C) +
+// i onwards, one per chunk; the ranges are disjoint, so every launch handles
+// packed sequences like a batch.
 
 #include "gdn_fwd_kernel.h"
 
@@ -36,10 +48,10 @@ namespace gdn {
 namespace bwd {
 
 constexpr int C = 32;
-constexpr int BV = 16;
-constexpr int NT = 512;  // 8 waves: 2 per SIMD (256 VGPRs each)
-constexpr int RL = NT / C;  // lanes per row in row reductions
-static_assert(RL >= 1 && RL <= 64 && (RL & (RL - 1)) == 0, "row lanes");
+constexpr int BV = 16;    // state columns per workgroup of the recurrences
+constexpr int VS = 16;    // V columns per step of the gradient kernel's V walk
+constexpr int NTP = 256;  // threads: prep_kernel and recur_kernel (4 waves)
+constexpr int NTG = 512;  // threads: grad_kernel (8 waves)
 
 struct BArgs {
   const void* q;
@@ -50,51 +62,35 @@ struct BArgs {
   const float* h0;
   const void* d_o;
   const float* dfs;
+  void* dq;
+  void* dk;
   void* dv;
+  void* dg;
+  void* dbeta;
   float* dh0;
-  float* ckpt;
-  float* pq;
-  float* pk;
-  float* pg;
-  float* pb;
-  int64_t sq[3], sk[3], sv[3], sg[3], sb[3], sdo[3], sdv[3];
+  float* rec;  // per (slot, head): the prep kernel's record
+  float* ckS;  // per (slot, head): S at the chunk start, [K][V]
+  float* ckD;  // per (slot, head): dS', the gradient of the state after the chunk, [K][V]
+  float* uu;   // per (slot, head): u, [C][V]
+  float* du;   // per (slot, head): du, [C][V]
+  int64_t sq[3], sk[3], sv[3], sg[3], sb[3], sdo[3], sdq[3], sdk[3], sdv[3], sdg[3], sdb[3];
   int64_t sh0[4], sdfs[4], sdh0[4];
-  int64_t R;  // rows of the partial buffers: B T, or T for packed sequences
-  int B, T, H, V, nv;
+  int B, T, H, V, nv, nchmax, units;
   float scale;
   int g_dtype, beta_dtype, do_dtype;
   const int64_t* cu;
   int xcd_remap;
 };
 
-struct RArgs {
-  const float* pq;
-  const float* pk;
-  const float* pg;
-  const float* pb;
-  void* dq;
-  void* dk;
-  void* dg;
-  void* dbeta;
-  int64_t sdq[3], sdk[3], sdg[3], sdb[3];
-  int64_t R;
-  int T, H, K, nv;
-  int qkv_dtype, g_dtype, beta_dtype;
-};
-
+// Per-(slot, head) record, in floats: T, P = M o Q K^T and K K^T as [C][C],
+// W as [C][K], then b, gam, D as [C] each and gam_C (first of a [C] row).
 template <int K>
-struct alignas(16) BSmem {
-  static constexpr int KD = K + 1, BD = BV + 1, CD = C + 1;
-  float q[C][KD], k[C][KD], w[C][KD], dw[C][KD];
-  float x[C][KD];  // dW~, then the new dS as [K][BD]
-  float v[C][BD], dO[C][BD], u[C][BD], du[C][BD], u2[C][BD], qs[C][BD];
-  float S[K][BD], dS[K][BD];
-  float kk[C][CD], qk[C][CD], m[C][CD], a[C][CD], t[C][CD], dt[C][CD], y[C][CD], z[C][CD];
-  float gl[C], bt[C], b[C], gam[C], D[C], dgam[C], dD[C], dbt[C], db[C];
-  float red[NT / 64];
-  float gC, dgC;
+struct Rec {
+  static constexpr int T = 0, PM = C * C, KK = 2 * C * C, W = 3 * C * C;
+  static constexpr int G = W + C * K;
+  static constexpr int SIZE = G + 4 * C;
 };
-static_assert(C * (128 + 1) >= 128 * (BV + 1), "x holds a K x BD tile");
+inline int64_t rec_size(int K) { return 3 * C * C + (int64_t)C * K + 4 * C; }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -124,6 +120,38 @@ __device__ __forceinline__ void stx(void* base, int64_t off, float x) {
   else static_cast<uint16_t*>(base)[off] = float_to_bf16_bits(x);
 }
 
+// ROWS x COLS block of a row-major TIn array (row stride `rs` elements,
+// 16-byte aligned rows) -> LDS as fp32, in two steps so that all global loads
+// of a phase are issued before the first LDS store.  Rows >= nvalid read as
+// zero.
+template <typename TIn, int ROWS, int COLS, int NT>
+struct RowLoad {
+  static constexpr int VEC = 16 / (int)sizeof(TIn), RV = COLS / VEC, N = (ROWS * RV + NT - 1) / NT;
+  static_assert(COLS % VEC == 0, "row width");
+  u32x4 r[N];
+  __device__ __forceinline__ void load(int tid, const TIn* base, int64_t rs, int nvalid) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      r[i] = (e < ROWS * RV && t < nvalid) ? *reinterpret_cast<const u32x4*>(base + t * rs + col) : z;
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void store(int tid, float (*dst)[LD]) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (e < ROWS * RV) {
+        float x[VEC];
+        unpack16<TIn>(r[i], x);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) dst[t][col + j] = x[j];
+      }
+    }
+  }
+};
+
 // One term sum_{kk < KD} a(m, kk) b(kk, n) of a product.
 template <int KD, typename FA, typename FB>
 struct Seg {
@@ -135,12 +163,10 @@ __device__ __forceinline__ Seg<KD, FA, FB> seg(FA a, FB b) {
   return Seg<KD, FA, FB>{a, b};
 }
 
-// out(m, n, sum over the segments) for an M x N result on the matrix cores
-// (v_mfma_f32_16x16x4_f32, full fp32): 16 x 16 output tiles dealt round-robin
-// to the waves, up to G of them in
-// flight per wave so that their operand loads and MFMA chains overlap.
+// acc[g] += one segment over the 16 x 16 tiles at (m0[g], n0[g]), g < ng, on
+// v_mfma_f32_16x16x4_f32 (full fp32), the G tiles in flight together.
 // Lane l supplies a(m0 + l % 16, k0 + l / 16) and b(k0 + l / 16, n0 + l % 16)
-// and receives rows m0 + 4 (l / 16) + i, column n0 + l % 16 of a tile.
+// and holds rows m0 + 4 (l / 16) + i, column n0 + l % 16 of a tile.
 template <int G, int KD, typename FA, typename FB>
 __device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], const int (&n0)[G],
                                          int ng, int r, int kq, const Seg<KD, FA, FB>& s) {
@@ -158,7 +184,9 @@ __device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], co
   }
 }
 
-template <int M, int N, typename FO, typename... Segs>
+// out(m, n, sum over the segments) for an M x N result: 16 x 16 tiles dealt
+// round-robin to the NT / 64 waves, up to 4 of them in flight per wave.
+template <int NT, int M, int N, typename FO, typename... Segs>
 __device__ __forceinline__ void mmx(int tid, FO&& out, const Segs&... segs) {
   static_assert(M % 16 == 0 && N % 16 == 0, "16 x 16 tiles");
   constexpr int TNt = N / 16, NTILE = (M / 16) * TNt, NW = NT / 64;
@@ -187,10 +215,13 @@ __device__ __forceinline__ void mmx(int tid, FO&& out, const Segs&... segs) {
   }
 }
 
-// sum_{i < LEN} f(r, i) for row r = tid / RL, computed by the RL lanes of
-// the row (a power of two inside one wave) and returned to all of them.
-template <int LEN, typename F>
+// sum_{i < LEN} f(r, i) for row r = tid / (NT / C), computed by the NT / C
+// lanes of the row (a power of two inside one wave) and returned to all of
+// them.
+template <int NT, int LEN, typename F>
 __device__ __forceinline__ float row_sum(int tid, F&& f) {
+  constexpr int RL = NT / C;
+  static_assert(RL >= 1 && RL <= 64 && (RL & (RL - 1)) == 0, "row lanes");
   const int r = tid / RL, part = tid % RL;
   float acc = 0.f;
   for (int i = part; i < LEN; i += RL) acc += f(r, i);
@@ -199,441 +230,701 @@ __device__ __forceinline__ float row_sum(int tid, F&& f) {
   return acc;
 }
 
+// Sum over the 16 lanes of a lane's group (the lanes that differ in bits 0-3).
+__device__ __forceinline__ float sum16(float x) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// Chunk slot -> (sequence rows, chunk).  False for a slot that holds no
+// chunk (the gaps between packed sequences).
+__device__ __forceinline__ bool slot_chunk(const BArgs& p, int64_t slot, RowSpan& rs, int& c) {
+  if (p.cu == nullptr) {
+    const int seq = (int)(slot / p.nchmax);
+    c = (int)(slot % p.nchmax);
+    rs = row_span(nullptr, p.T, seq);
+    return seq < p.B && (int64_t)c * C < rs.T;
+  }
+  // the last sequence whose first slot floor(t0 / C) + i is <= slot
+  int lo = 0, hi = p.B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (row_span(p.cu, p.T, mid).t0 / C + mid <= slot) lo = mid;
+    else hi = mid - 1;
+  }
+  rs = row_span(p.cu, p.T, lo);
+  const int64_t cc = slot - (rs.t0 / C + lo);
+  c = (int)cc;
+  return cc >= 0 && cc * C < rs.T;
+}
+
+// ---------------------------------------------------------------------------
+// 1. prep: the state-independent half of a chunk's forward
+// ---------------------------------------------------------------------------
+
+template <int K>
+struct alignas(16) PSmem {
+  float q[C][K + 1], k[C][K + 1];
+  float kk[C][C + 1], qk[C][C + 1], a[C][C + 1], t[C][C + 1];
+  float gl[C], bt[C], b[C], gam[C], D[C];
+  float gC;
+};
+
 template <typename TIn, int K>
-__global__ __launch_bounds__(NT) void bwd_kernel(const BArgs p) {
-  using Sm = BSmem<K>;
-  constexpr int BD = Sm::BD;
-  static_assert(K == 32 || K == 64 || K == 128, "K");
+__global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
+  using R = Rec<K>;
+  __shared__ PSmem<K> s;
+  const int tid = threadIdx.x;
+  const int64_t slot = blockIdx.x / p.H;
+  const int hi = blockIdx.x % p.H;
+  RowSpan rs;
+  int c;
+  if (!slot_chunk(p, slot, rs, c)) return;
+  const int t0 = c * C, nval = min(C, rs.T - t0);
+  float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
 
-  __shared__ Sm s;
-  // The thread index is re-read as an opaque value at the top of every
-  // chunk iteration, so that per-thread LDS addresses are recomputed there
-  // instead of being hoisted out of the chunk loops and held in registers.
-  const int tid0 = threadIdx.x;
-  const int lane = tid0 & 63, wave = tid0 >> 6;
-
-  int unit = blockIdx.x;
-  if (p.xcd_remap) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-  const int vs = unit % p.nv;
-  const int bh = unit / p.nv;
-  const int bi = bh / p.H;
-  const int hi = bh % p.H;
-  const int v0 = vs * BV;
-  const RowSpan rs = row_span(p.cu, p.T, bi);
-  const int Tn = rs.T;
-  const int nch = (Tn + C - 1) / C;
-  const float scale = p.scale;
-
-  const int64_t qb = head_base(rs, hi, p.sq), kb = head_base(rs, hi, p.sk);
-  const int64_t vb = head_base(rs, hi, p.sv) + v0, dob = head_base(rs, hi, p.sdo) + v0;
-  const int64_t gb = head_base(rs, hi, p.sg), bb = head_base(rs, hi, p.sb);
-  const int64_t dvb = head_base(rs, hi, p.sdv) + v0;
-  // rows of the partial buffers ([nv][R][H](K)): b T + t; row t of this
-  // chunk sequence starts at pq_h + t H K (pg_h + t H for the gates)
-  const int64_t prow0 = rs.b * p.T + rs.t0;
-  const int64_t hk = (int64_t)p.H * K;
-  float* const pq_h = p.pq + ((int64_t)vs * p.R + prow0) * hk + (int64_t)hi * K;
-  float* const pk_h = p.pk + ((int64_t)vs * p.R + prow0) * hk + (int64_t)hi * K;
-  float* const pg_h = p.pg + ((int64_t)vs * p.R + prow0) * p.H + hi;
-  float* const pb_h = p.pb + ((int64_t)vs * p.R + prow0) * p.H + hi;
-  // chunk-start states: slot (chunk) x H x nv x [K][BV]; packed sequence i
-  // starts at slot floor(t0 / C) + i, which keeps sequences disjoint.
-  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * ((p.T + C - 1) / C);
-  const int64_t ck_stride = (int64_t)p.H * p.nv * K * BV;
-  float* const ck0 = p.ckpt + ((slot0 * p.H + hi) * p.nv + vs) * (int64_t)(K * BV);
-
-  // Chunk rows -> LDS as fp32.  q, k, v move as 16-byte vectors (their rows
-  // are 16-byte aligned: the host checks it); every global load of the
-  // chunk is issued before the first LDS store.
-  constexpr int VEC = 16 / (int)sizeof(TIn);
-  constexpr int RVK = K / VEC, NVK = (C * RVK + NT - 1) / NT;
-  constexpr int RVV = BV / VEC;
-  constexpr int NDO = (C * BV + NT - 1) / NT;
-  static_assert(C * RVV <= NT, "v vectors");
-  const TIn* const qg = static_cast<const TIn*>(p.q) + qb;
-  const TIn* const kg = static_cast<const TIn*>(p.k) + kb;
-  const TIn* const vg = static_cast<const TIn*>(p.v) + vb;
-  auto load_chunk = [&](int tid, int c, bool full) __attribute__((always_inline)) {
-    const int t0 = c * C;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    u32x4 rk[NVK], rq[NVK], rv = z;
-    float rdo[NDO], rg = 0.f, rb = 0.f;
-#pragma unroll
-    for (int i = 0; i < NVK; ++i) {
-      const int e = tid + i * NT, t = e / RVK, col = (e % RVK) * VEC;
-      const bool ok = e < C * RVK && t0 + t < Tn;
-      rk[i] = ok ? *reinterpret_cast<const u32x4*>(kg + (int64_t)(t0 + t) * p.sk[1] + col) : z;
-      rq[i] = (ok && full) ? *reinterpret_cast<const u32x4*>(qg + (int64_t)(t0 + t) * p.sq[1] + col) : z;
+  {
+    RowLoad<TIn, C, K, NTP> lq, lk;
+    lq.load(tid, static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq) + t0 * p.sq[1], p.sq[1], nval);
+    lk.load(tid, static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + t0 * p.sk[1], p.sk[1], nval);
+    float gv = 0.f, bv = 0.f;
+    if (tid < nval) {
+      gv = load_scalar(p.g, head_base(rs, hi, p.sg) + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
+      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
     }
-    if (tid < C * RVV) {
-      const int t = tid / RVV, col = (tid % RVV) * VEC;
-      if (t0 + t < Tn) rv = *reinterpret_cast<const u32x4*>(vg + (int64_t)(t0 + t) * p.sv[1] + col);
-    }
-#pragma unroll
-    for (int i = 0; i < NDO; ++i) {
-      const int e = tid + i * NT, t = e / BV, c2 = e % BV;
-      rdo[i] = (full && e < C * BV && t0 + t < Tn)
-                   ? load_scalar(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype)
-                   : 0.f;
-    }
-    if (tid < C && t0 + tid < Tn) {
-      rg = load_scalar(p.g, gb + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
-      rb = load_scalar(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
-    }
-#pragma unroll
-    for (int i = 0; i < NVK; ++i) {
-      const int e = tid + i * NT, t = e / RVK, col = (e % RVK) * VEC;
-      if (e < C * RVK) {
-        float x[VEC];
-        unpack16<TIn>(rk[i], x);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) s.k[t][col + j] = x[j];
-        if (full) {
-          unpack16<TIn>(rq[i], x);
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) s.q[t][col + j] = x[j];
-        }
-      }
-    }
-    if (tid < C * RVV) {
-      const int t = tid / RVV, col = (tid % RVV) * VEC;
-      float x[VEC];
-      unpack16<TIn>(rv, x);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) s.v[t][col + j] = x[j];
-    }
-    if (full) {
-#pragma unroll
-      for (int i = 0; i < NDO; ++i) {
-        const int e = tid + i * NT;
-        if (e < C * BV) s.dO[e / BV][e % BV] = rdo[i];
-      }
-    }
+    lq.store(tid, s.q);
+    lk.store(tid, s.k);
     if (tid < C) {
-      s.gl[tid] = rg;
-      s.bt[tid] = rb;
+      s.gl[tid] = gv;
+      s.bt[tid] = bv;
     }
-  };
+  }
+  __syncthreads();
+  if (tid < C) {
+    float bt = 0.f, bc = 0.f;
+    for (int j = 0; j < C; ++j) {
+      bc += s.gl[j];
+      if (j == tid) bt = bc;
+    }
+    s.b[tid] = bt;
+    s.gam[tid] = expf(bt);
+    s.D[tid] = expf(bc - bt);
+    if (tid == C - 1) s.gC = expf(bc);
+  }
+  mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.kk[m][n] = x; },
+                 seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                 seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  __syncthreads();
+  for (int e = tid; e < C * C; e += NTP) {
+    const int t = e / C, j = e % C;
+    const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
+    s.a[t][j] = j < t ? s.bt[t] * mv * s.kk[t][j] : 0.f;
+    rec[R::PM + e] = mv * s.qk[t][j];
+    rec[R::KK + e] = s.kk[t][j];
+  }
+  if (tid < C) {
+    rec[R::G + tid] = s.b[tid];
+    rec[R::G + C + tid] = s.gam[tid];
+    rec[R::G + 2 * C + tid] = s.D[tid];
+    rec[R::G + 3 * C + tid] = tid == 0 ? s.gC : 0.f;
+  }
+  __syncthreads();
+  if (tid < C) {
+    // column tid of T = (I + A)^-1 by forward substitution, in registers
+    const int cc = tid;
+    float col[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      float x = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) x = __builtin_fmaf(-s.a[i][j], col[j], x);
+      col[i] = x;
+    }
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      s.t[i][cc] = col[i];
+      rec[R::T + i * C + cc] = col[i];
+    }
+  }
+  __syncthreads();
+  mmx<NTP, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
+                 seg<C>([&](int m, int kk) { return s.t[m][kk]; },
+                        [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
+}
 
-  // Gates, M, K K^T (and Q K^T), A, T = (I + A)^-1, W, U, u.  Leaves
-  // U in u2.  Starts and ends on a barrier.
-  auto chunk_forward = [&](int tid, bool full) __attribute__((always_inline)) {
-    if (tid < C) {
-      float bt = 0.f, bc = 0.f;
-      for (int j = 0; j < C; ++j) {
-        bc += s.gl[j];
-        if (j == tid) bt = bc;
-      }
-      s.b[tid] = bt;
-      s.gam[tid] = expf(bt);
-      s.D[tid] = expf(bc - bt);
-      if (tid == C - 1) s.gC = expf(bc);
-    }
-    mmx<C, C>(tid, [&](int m, int n, float x) { s.kk[m][n] = x; },
-                   seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-    if (full)
-      mmx<C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
-                     seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-    __syncthreads();
-    for (int e = tid; e < C * C; e += NT) {
-      const int t = e / C, j = e % C;
-      const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
-      s.m[t][j] = mv;
-      s.a[t][j] = j < t ? s.bt[t] * mv * s.kk[t][j] : 0.f;
-    }
-    __syncthreads();
-    if (tid < C) {
-      // column tid of T by forward substitution, the column in registers
-      const int c = tid;
-      float col[C];
-#pragma unroll
-      for (int i = 0; i < C; ++i) {
-        float x = (i == c) ? 1.f : 0.f;
-#pragma unroll
-        for (int j = 0; j < i; ++j) x = __builtin_fmaf(-s.a[i][j], col[j], x);
-        col[i] = x;
-      }
-#pragma unroll
-      for (int i = 0; i < C; ++i) s.t[i][c] = col[i];
-    }
-    __syncthreads();
-    mmx<C, K>(tid, [&](int m, int n, float x) { s.w[m][n] = x; },
-                       seg<C>([&](int m, int kk) { return s.t[m][kk]; },
-                              [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
-                    seg<C>([&](int m, int kk) { return s.t[m][kk]; },
-                           [&](int kk, int n) { return s.bt[kk] * s.v[kk][n]; }));
-    __syncthreads();
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u[m][n] = s.u2[m][n] - x; },
-                    seg<K>([&](int m, int kk) { return s.w[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
-    __syncthreads();
-  };
+// ---------------------------------------------------------------------------
+// 2. the two recurrences (one launch: blocks [0, units) walk forward, the
+//    rest backward)
+// ---------------------------------------------------------------------------
 
-  // ---------------- pass 1: chunk-start states ----------------
-  for (int e = tid0; e < K * BV; e += NT) {
+template <int K>
+struct alignas(16) FSmem {
+  float S[K][BV + 1];
+  float t[C][C + 1];
+  float w[C][K + 1], k[C][K + 1];
+  float v[C][BV + 1], u[C][BV + 1];
+  float bt[C], D[C];
+  float gC;
+};
+
+template <int K>
+struct alignas(16) RSmem {
+  float dS[K][BV + 1];
+  float pm[C][C + 1];
+  float q[C][K + 1], k[C][K + 1], w[C][K + 1];
+  float dO[C][BV + 1], du[C][BV + 1];
+  float gam[C], D[C];
+  float gC;
+};
+
+template <int K>
+union FRSmem {
+  FSmem<K> f;
+  RSmem<K> r;
+};
+
+// Forward walk: S at each chunk start -> ckS, u -> uu.
+template <typename TIn, int K>
+__device__ __forceinline__ void walk_forward(const BArgs& p, FSmem<K>& s, const RowSpan& rs, int bi, int hi,
+                                             int v0, int64_t slot0) {
+  using R = Rec<K>;
+  const int tid = threadIdx.x;
+  const int nch = (rs.T + C - 1) / C;
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  const int64_t bb = head_base(rs, hi, p.sb);
+  for (int e = tid; e < K * BV; e += NTP) {
     const int kk = e / BV, c2 = e % BV;
     s.S[kk][c2] = p.h0 ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]] : 0.f;
   }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
-    int tid = tid0;
-    asm volatile("" : "+v"(tid));
-    float* ck = ck0 + c * ck_stride;
-    for (int e = 4 * tid; e < K * BV; e += 4 * NT) {
-      const int kk = e / BV, c2 = e % BV;
-      *reinterpret_cast<f32x4*>(ck + e) = f32x4{s.S[kk][c2], s.S[kk][c2 + 1], s.S[kk][c2 + 2], s.S[kk][c2 + 3]};
+    const int t0 = c * C, nval = min(C, rs.T - t0);
+    const int64_t ri = (slot0 + c) * p.H + hi;
+    const float* const rec = p.rec + ri * R::SIZE;
+    float* const cks = p.ckS + ri * (int64_t)K * p.V + v0;
+    float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
+    RowLoad<float, C, C, NTP> lt;
+    RowLoad<float, C, K, NTP> lw;
+    RowLoad<TIn, C, K, NTP> lk;
+    RowLoad<TIn, C, BV, NTP> lv;
+    lt.load(tid, rec + R::T, C, C);
+    lw.load(tid, rec + R::W, K, C);
+    lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    lv.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
+    float bv = 0.f, dv = 0.f, gc = 0.f;
+    if (tid < C) {
+      bv = tid < nval ? load_scalar(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0.f;
+      dv = rec[R::G + 2 * C + tid];
     }
-    load_chunk(tid, c, false);
+    if (tid == 0) gc = rec[R::G + 3 * C];
+    for (int e = tid; e < K * BV / 4; e += NTP) {
+      const int kk = e / (BV / 4), c4 = (e % (BV / 4)) * 4;
+      *reinterpret_cast<f32x4*>(cks + (int64_t)kk * p.V + c4) =
+          f32x4{s.S[kk][c4], s.S[kk][c4 + 1], s.S[kk][c4 + 2], s.S[kk][c4 + 3]};
+    }
+    lt.store(tid, s.t);
+    lw.store(tid, s.w);
+    lk.store(tid, s.k);
+    lv.store(tid, s.v);
+    if (tid < C) {
+      s.bt[tid] = bv;
+      s.D[tid] = dv;
+    }
+    if (tid == 0) s.gC = gc;
     __syncthreads();
-    chunk_forward(tid, false);
-    mmx<K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
-                        seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
-                               [&](int kk, int n) { return s.u[kk][n]; }));
+    // u = T diag(beta) V - W S
+    mmx<NTP, C, BV>(
+        tid,
+        [&](int m, int n, float x) {
+          s.u[m][n] = x;
+          uo[(int64_t)m * p.V + n] = x;
+        },
+        seg<C>([&](int m, int kk) { return s.t[m][kk]; }, [&](int kk, int n) { return s.bt[kk] * s.v[kk][n]; }),
+        seg<K>([&](int m, int kk) { return -s.w[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
+    __syncthreads();
+    // S <- gam_C S + K^T diag(D) u
+    mmx<NTP, K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
+                    seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
+                           [&](int kk, int n) { return s.u[kk][n]; }));
     __syncthreads();
   }
+}
 
-  // ---------------- pass 2: gradients, last chunk first ----------------
-  for (int e = tid0; e < K * BV; e += NT) {
+// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.
+template <typename TIn, int K>
+__device__ __forceinline__ void walk_backward(const BArgs& p, RSmem<K>& s, const RowSpan& rs, int bi, int hi,
+                                              int v0, int64_t slot0) {
+  using R = Rec<K>;
+  const int tid = threadIdx.x;
+  const int nch = (rs.T + C - 1) / C;
+  const float scale = p.scale;
+  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const int64_t dob = head_base(rs, hi, p.sdo) + v0;
+  constexpr int NDO = C * BV / NTP;
+  static_assert(C * BV % NTP == 0, "dO elements per thread");
+  for (int e = tid; e < K * BV; e += NTP) {
     const int kk = e / BV, c2 = e % BV;
     s.dS[kk][c2] =
         p.dfs ? p.dfs[bi * p.sdfs[0] + hi * p.sdfs[1] + kk * p.sdfs[2] + (v0 + c2) * p.sdfs[3]] : 0.f;
   }
-  float* const xs = &s.x[0][0];
-  for (int c = nch - 1; c >= 0; --c) {
-    int tid = tid0;
-    asm volatile("" : "+v"(tid));
-    const int t0 = c * C;
-    const float* ck = ck0 + c * ck_stride;
-    {
-      constexpr int NCK = (K * BV / 4 + NT - 1) / NT;
-      f32x4 r4[NCK];
-#pragma unroll
-      for (int i = 0; i < NCK; ++i)
-        if (4 * (tid + i * NT) < K * BV) r4[i] = *reinterpret_cast<const f32x4*>(ck + 4 * (tid + i * NT));
-#pragma unroll
-      for (int i = 0; i < NCK; ++i) {
-        const int e = 4 * (tid + i * NT), kk = e / BV, c2 = e % BV;
-        if (e < K * BV) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) s.S[kk][c2 + j] = r4[i][j];
-        }
-      }
-    }
-    load_chunk(tid, c, true);
-    __syncthreads();
-    chunk_forward(tid, true);
-
-    // K dS' -> u2 (U is no longer needed), Q S -> qs
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
-                    seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.dS[kk][n]; }));
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.qs[m][n] = x; },
-                    seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
-    __syncthreads();
-    // du = scale P^T dO + D o K dS';  dQK = M o (scale dO u^T)
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.du[m][n] = scale * x + s.D[m] * s.u2[m][n]; },
-                    seg<C>([&](int m, int kk) { return s.m[kk][m] * s.qk[kk][m]; },
-                           [&](int kk, int n) { return s.dO[kk][n]; }));
-    mmx<C, C>(tid, [&](int m, int n, float x) { s.y[m][n] = scale * s.m[m][n] * x; },
-                   seg<BV>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.u[n][kk]; }));
-    {
-      const float dd = row_sum<BV>(tid, [&](int r, int i) { return s.u[r][i] * s.u2[r][i]; });
-      const float dg = row_sum<BV>(tid, [&](int r, int i) { return s.dO[r][i] * s.qs[r][i]; });
-      if (tid % RL == 0) {
-        s.dD[tid / RL] = dd;
-        s.dgam[tid / RL] = scale * dg;
-      }
-    }
-    {
-      // dgam_C = <dS', S>
-      float part = 0.f;
-      for (int e = tid; e < K * BV; e += NT) part = __builtin_fmaf(s.dS[e / BV][e % BV], s.S[e / BV][e % BV], part);
-      for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
-      if (lane == 0) s.red[wave] = part;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float r = 0.f;
-      for (int w = 0; w < NT / 64; ++w) r += s.red[w];
-      s.dgC = r;
-    }
-    // dW = -du S^T
-    mmx<C, K>(tid, [&](int m, int n, float x) { s.dw[m][n] = -x; },
-                       seg<BV>([&](int m, int kk) { return s.du[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
-    __syncthreads();
-    // dT = du (beta V)^T + dW (beta gam K)^T;  dW~ = T^T dW -> x;  dU~ = T^T du -> u2
-    mmx<C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = x; },
-                   seg<BV>([&](int m, int kk) { return s.du[m][kk]; },
-                           [&](int kk, int n) { return s.bt[n] * s.v[n][kk]; }),
-                   seg<K>([&](int m, int kk) { return s.dw[m][kk]; },
-                          [&](int kk, int n) { return s.bt[n] * s.gam[n] * s.k[n][kk]; }));
-    mmx<C, K>(tid, [&](int m, int n, float x) { s.x[m][n] = x; },
-                       seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dw[kk][n]; }));
-    mmx<C, BV>(tid, [&](int m, int n, float x) { s.u2[m][n] = x; },
-                    seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
-    __syncthreads();
-    // Z = T^T dT;  dv = beta dU~;  dbeta, dgam through W~ and U~
-    mmx<C, C>(tid, [&](int m, int n, float x) { s.z[m][n] = x; },
-                   seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dt[kk][n]; }));
-    for (int e = tid; e < C * BV; e += NT) {
-      const int t = e / BV, c2 = e % BV;
-      if (t0 + t < Tn) stx<TIn>(p.dv, dvb + (int64_t)(t0 + t) * p.sdv[1] + c2, s.bt[t] * s.u2[t][c2]);
-    }
-    {
-      const float kw = row_sum<K>(tid, [&](int r, int i) { return s.k[r][i] * s.x[r][i]; });
-      const float vu = row_sum<BV>(tid, [&](int r, int i) { return s.v[r][i] * s.u2[r][i]; });
-      if (tid % RL == 0) {
-        const int r = tid / RL;
-        s.dbt[r] = vu + s.gam[r] * kw;
-        s.dgam[r] += s.bt[r] * kw;
-      }
-    }
-    __syncthreads();
-    // dA = -tril_-1(Z T^T) -> dt
-    mmx<C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
-                   seg<C>([&](int m, int kk) { return s.z[m][kk]; }, [&](int kk, int n) { return s.t[n][kk]; }));
-    __syncthreads();
-    // dKK = dA o beta_t M -> z;  dbeta += sum_j dA M KK
-    for (int e = tid; e < C * C; e += NT) {
-      const int t = e / C, j = e % C;
-      s.z[t][j] = j < t ? s.dt[t][j] * s.bt[t] * s.m[t][j] : 0.f;
-    }
-    {
-      const float am = row_sum<C>(tid, [&](int r, int j) { return s.dt[r][j] * s.m[r][j] * s.kk[r][j]; });
-      // db_t through M (dQK o QK) and A (dA o A): row sums minus column sums
-      const float mt = row_sum<C>(tid, [&](int r, int j) {
-        return s.y[r][j] * s.qk[r][j] - s.y[j][r] * s.qk[j][r] + s.dt[r][j] * s.a[r][j] -
-               s.dt[j][r] * s.a[j][r];
-      });
-      const float dd = row_sum<C>(tid, [&](int r, int j) { return s.dD[j] * s.D[j]; });
-      if (tid % RL == 0) {
-        const int r = tid / RL;
-        s.dbt[r] += am;
-        // ... and through gam, D and (last row) gam_C and every D_j
-        float d = mt + s.dgam[r] * s.gam[r] - s.dD[r] * s.D[r];
-        if (r == C - 1) d += dd + s.dgC * s.gC;
-        s.db[r] = d;
-      }
-    }
-    __syncthreads();
-    if (tid < C && t0 + tid < Tn) {
-      float acc = 0.f;
-      for (int j = tid; j < C; ++j) acc += s.db[j];
-      const int64_t r = (int64_t)(t0 + tid) * p.H;
-      pg_h[r] = acc;
-      pb_h[r] = s.dbt[tid];
-    }
-    // dq (partial) = dQK K + scale gam dO S^T
-    mmx<C, K>(
-        tid, [&](int m, int n, float x) {
-          if (t0 + m < Tn) pq_h[(int64_t)(t0 + m) * hk + n] = x;
-        },
-        seg<C>([&](int m, int kk) { return s.y[m][kk]; }, [&](int kk, int n) { return s.k[kk][n]; }),
-        seg<BV>([&](int m, int kk) { return scale * s.gam[m] * s.dO[m][kk]; },
-                [&](int kk, int n) { return s.S[n][kk]; }));
-    // dk (partial) = dQK^T Q + D u dS'^T + (dKK + dKK^T) K + beta gam dW~
-    mmx<C, K>(
-        tid, [&](int m, int n, float x) {
-          if (t0 + m < Tn)
-            pk_h[(int64_t)(t0 + m) * hk + n] =
-                x + s.bt[m] * s.gam[m] * s.x[m][n];
-        },
-        seg<C>([&](int m, int kk) { return s.y[kk][m]; }, [&](int kk, int n) { return s.q[kk][n]; }),
-        seg<BV>([&](int m, int kk) { return s.D[m] * s.u[m][kk]; }, [&](int kk, int n) { return s.dS[n][kk]; }),
-        seg<C>([&](int m, int kk) { return s.z[m][kk] + s.z[kk][m]; }, [&](int kk, int n) { return s.k[kk][n]; }));
-    __syncthreads();
-    // dS = scale Q^T diag(gam) dO + gam_C dS' - W^T du -> x as [K][BD]
-    mmx<K, BV>(tid, [&](int m, int n, float x) { xs[m * BD + n] = x + s.gC * s.dS[m][n]; },
-                        seg<C>([&](int m, int kk) { return scale * s.gam[kk] * s.q[kk][m]; },
-                               [&](int kk, int n) { return s.dO[kk][n]; }),
-                        seg<C>([&](int m, int kk) { return -s.w[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
-    __syncthreads();
-    for (int e = tid; e < K * BV; e += NT) s.dS[e / BV][e % BV] = xs[(e / BV) * BD + e % BV];
-  }
   __syncthreads();
+  for (int c = nch - 1; c >= 0; --c) {
+    const int t0 = c * C, nval = min(C, rs.T - t0);
+    const int64_t ri = (slot0 + c) * p.H + hi;
+    const float* const rec = p.rec + ri * R::SIZE;
+    float* const ckd = p.ckD + ri * (int64_t)K * p.V + v0;
+    float* const duo = p.du + ri * (int64_t)C * p.V + v0;
+    RowLoad<float, C, C, NTP> lp;
+    RowLoad<float, C, K, NTP> lw;
+    RowLoad<TIn, C, K, NTP> lq, lk;
+    lp.load(tid, rec + R::PM, C, C);
+    lw.load(tid, rec + R::W, K, C);
+    lq.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
+    lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    float rdo[NDO];
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int e = tid + i * NTP, t = e / BV, c2 = e % BV;
+      rdo[i] = t < nval ? load_scalar(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype) : 0.f;
+    }
+    float gm = 0.f, dv = 0.f, gc = 0.f;
+    if (tid < C) {
+      gm = rec[R::G + C + tid];
+      dv = rec[R::G + 2 * C + tid];
+    }
+    if (tid == 0) gc = rec[R::G + 3 * C];
+    for (int e = tid; e < K * BV / 4; e += NTP) {
+      const int kk = e / (BV / 4), c4 = (e % (BV / 4)) * 4;
+      *reinterpret_cast<f32x4*>(ckd + (int64_t)kk * p.V + c4) =
+          f32x4{s.dS[kk][c4], s.dS[kk][c4 + 1], s.dS[kk][c4 + 2], s.dS[kk][c4 + 3]};
+    }
+    lp.store(tid, s.pm);
+    lw.store(tid, s.w);
+    lq.store(tid, s.q);
+    lk.store(tid, s.k);
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int e = tid + i * NTP;
+      s.dO[e / BV][e % BV] = rdo[i];
+    }
+    if (tid < C) {
+      s.gam[tid] = gm;
+      s.D[tid] = dv;
+    }
+    if (tid == 0) s.gC = gc;
+    __syncthreads();
+    // du = scale P^T dO + diag(D) K dS'
+    mmx<NTP, C, BV>(
+        tid,
+        [&](int m, int n, float x) {
+          s.du[m][n] = x;
+          duo[(int64_t)m * p.V + n] = x;
+        },
+        seg<C>([&](int m, int kk) { return scale * s.pm[kk][m]; }, [&](int kk, int n) { return s.dO[kk][n]; }),
+        seg<K>([&](int m, int kk) { return s.D[m] * s.k[m][kk]; }, [&](int kk, int n) { return s.dS[kk][n]; }));
+    __syncthreads();
+    // dS <- scale Q^T diag(gam) dO + gam_C dS' - W^T du
+    mmx<NTP, K, BV>(tid, [&](int m, int n, float x) { s.dS[m][n] = x + s.gC * s.dS[m][n]; },
+                    seg<C>([&](int m, int kk) { return scale * s.gam[kk] * s.q[kk][m]; },
+                           [&](int kk, int n) { return s.dO[kk][n]; }),
+                    seg<C>([&](int m, int kk) { return -s.w[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
+    __syncthreads();
+  }
   if (p.dh0 != nullptr) {
-    for (int e = tid0; e < K * BV; e += NT) {
+    for (int e = tid; e < K * BV; e += NTP) {
       const int kk = e / BV, c2 = e % BV;
       p.dh0[bi * p.sdh0[0] + hi * p.sdh0[1] + kk * p.sdh0[2] + (v0 + c2) * p.sdh0[3]] = s.dS[kk][c2];
     }
   }
 }
 
-// dq, dk, dg, dbeta = the sums of the slices' partials, in row order.
-template <typename TIn>
-__global__ __launch_bounds__(256) void reduce_kernel(const RArgs p) {
-  const int64_t nrow = p.R * p.H;
-  const int64_t n_qk = nrow * p.K;
-  const int64_t slab_qk = n_qk, slab_g = nrow;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_qk + nrow; e += stride) {
-    if (e < n_qk) {
-      const int64_t kk = e % p.K, rh = e / p.K;
-      const int64_t h = rh % p.H, r = rh / p.H;
-      const int64_t b = r / p.T, t = r % p.T;
-      float sq = 0.f, sk = 0.f;
-      for (int vs = 0; vs < p.nv; ++vs) {
-        sq += p.pq[vs * slab_qk + e];
-        sk += p.pk[vs * slab_qk + e];
+template <typename TIn, int K>
+__global__ __launch_bounds__(NTP) void recur_kernel(const BArgs p) {
+  __shared__ FRSmem<K> sm;
+  int blk = blockIdx.x;
+  const bool backward = blk >= p.units;
+  if (backward) blk -= p.units;
+  // consecutive units (the V-slices of one head) on one XCD: they read the
+  // same records
+  int unit = blk;
+  if (p.xcd_remap) unit = (blk & 7) * (p.units >> 3) + (blk >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const RowSpan rs = row_span(p.cu, p.T, bi);
+  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
+  if (backward) walk_backward<TIn, K>(p, sm.r, rs, bi, hi, vs * BV, slot0);
+  else walk_forward<TIn, K>(p, sm.f, rs, bi, hi, vs * BV, slot0);
+}
+
+// ---------------------------------------------------------------------------
+// 3. every gradient of a chunk
+// ---------------------------------------------------------------------------
+
+template <int K>
+struct alignas(16) GSmem {
+  static constexpr int KD = K + 1, CD = C + 1, SD = VS + 1;
+  float q[C][KD], k[C][KD];
+  float dw[C][KD];   // dW = -du S^T
+  float dwt[C][KD];  // dW~ = T^T dW
+  float t[C][CD], pm[C][CD], kk[C][CD], m[C][CD];
+  float y[C][CD];    // dQK = M o (scale dO u^T)
+  float yp[C][CD];   // dQK o Q K^T = scale (dO u^T) o P
+  float dt[C][CD];   // dT, then dA
+  float z[C][CD];    // T^T dT, then dKK
+  float v[C][SD], dO[C][SD], u[C][SD], du[C][SD];
+  float S[K][SD], dS[K][SD];
+  float b[C], gam[C], D[C], bt[C];
+  float rq[K / 16][C], rk[K / 16][C];  // row partials, one row per 16-column tile
+  float vu[C], kw[C], dgam[C], dD[C], db[C], dbt[C];
+  float red[NTG / 64];
+  float gC, dgC;
+};
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
+  using R = Rec<K>;
+  constexpr int RL = NTG / C;
+  __shared__ GSmem<K> s;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t slot = blockIdx.x / p.H;
+  const int hi = blockIdx.x % p.H;
+  RowSpan rs;
+  int c;
+  if (!slot_chunk(p, slot, rs, c)) return;
+  const int t0 = c * C, nval = min(C, rs.T - t0);
+  const float scale = p.scale;
+  const int64_t ri = slot * p.H + hi;
+  const float* const rec = p.rec + ri * R::SIZE;
+  const float* const cks = p.ckS + ri * (int64_t)K * p.V;
+  const float* const ckd = p.ckD + ri * (int64_t)K * p.V;
+  const float* const uu = p.uu + ri * (int64_t)C * p.V;
+  const float* const dug = p.du + ri * (int64_t)C * p.V;
+  const int64_t qb = head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1];
+  const int64_t kb = head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1];
+  const int64_t vb = head_base(rs, hi, p.sv) + (int64_t)t0 * p.sv[1];
+  const int64_t dob = head_base(rs, hi, p.sdo) + (int64_t)t0 * p.sdo[1];
+  const int64_t dvb = head_base(rs, hi, p.sdv) + (int64_t)t0 * p.sdv[1];
+  const int64_t dqb = head_base(rs, hi, p.sdq) + (int64_t)t0 * p.sdq[1];
+  const int64_t dkb = head_base(rs, hi, p.sdk) + (int64_t)t0 * p.sdk[1];
+
+  // ---- q, k, beta and the record
+  {
+    RowLoad<TIn, C, K, NTG> lq, lk;
+    RowLoad<float, C, C, NTG> lt, lp, lkk;
+    lq.load(tid, static_cast<const TIn*>(p.q) + qb, p.sq[1], nval);
+    lk.load(tid, static_cast<const TIn*>(p.k) + kb, p.sk[1], nval);
+    lt.load(tid, rec + R::T, C, C);
+    lp.load(tid, rec + R::PM, C, C);
+    lkk.load(tid, rec + R::KK, C, C);
+    const float gate = tid < 4 * C ? rec[R::G + tid] : 0.f;
+    float bv = 0.f;
+    if (tid < nval)
+      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
+    lq.store(tid, s.q);
+    lk.store(tid, s.k);
+    lt.store(tid, s.t);
+    lp.store(tid, s.pm);
+    lkk.store(tid, s.kk);
+    if (tid < C) {
+      s.b[tid] = gate;
+      s.bt[tid] = bv;
+    } else if (tid < 2 * C) {
+      s.gam[tid - C] = gate;
+    } else if (tid < 3 * C) {
+      s.D[tid - 2 * C] = gate;
+    } else if (tid == 3 * C) {
+      s.gC = gate;
+    }
+  }
+
+  // ---- walk V in VS-column steps.  The C x K products (dW, dO S^T,
+  // u dS'^T) accumulate in registers: wave w owns tiles w + 8 i of the
+  // (C/16) x (K/16) tiles.
+  constexpr int NCT = K / 16, NTA = (C / 16) * NCT, NPW = (NTA + 7) / 8;
+  int am0[NPW], an0[NPW], ana = 0;
+#pragma unroll
+  for (int i = 0; i < NPW; ++i) {
+    const int j = wave + 8 * i;
+    am0[i] = j < NTA ? (j / NCT) * 16 : 0;
+    an0[i] = j < NTA ? (j % NCT) * 16 : 0;
+    if (j < NTA) ana = i + 1;
+  }
+  f32x4 accW[NPW], accQ[NPW], accK[NPW];
+#pragma unroll
+  for (int i = 0; i < NPW; ++i) {
+    accW[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accQ[i] = accW[i];
+    accK[i] = accW[i];
+  }
+  // one C x C tile per wave: dO u^T (waves 0-3) or du (beta V)^T (waves 4-7)
+  const int cm0[1] = {((wave & 3) >> 1) * 16}, cn0[1] = {(wave & 1) * 16};
+  f32x4 accC[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+  // dU~ = T^T du of the step: waves 4 and 5, rows 16 (wave - 4) .. + 15
+  const bool du_wave = wave == 4 || wave == 5;
+  const int um0[1] = {16 * (wave & 1)}, un0[1] = {0};
+  float vu_acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float dgc_acc = 0.f;
+
+  const int nvs = p.V / VS;
+  RowLoad<TIn, C, VS, NTG> lv;
+  RowLoad<float, C, VS, NTG> lu, ldu;
+  RowLoad<float, K, VS, NTG> lS, ldS;
+  static_assert(C * VS == NTG, "one dO element per thread");
+  float rdo = 0.f;
+  auto load_step = [&](int vsi) __attribute__((always_inline)) {
+    const int v0 = vsi * VS;
+    lv.load(tid, static_cast<const TIn*>(p.v) + vb + v0, p.sv[1], nval);
+    lu.load(tid, uu + v0, p.V, C);
+    ldu.load(tid, dug + v0, p.V, C);
+    lS.load(tid, cks + v0, p.V, K);
+    ldS.load(tid, ckd + v0, p.V, K);
+    const int t = tid / VS, c2 = tid % VS;
+    rdo = t < nval ? load_scalar(p.d_o, dob + (int64_t)t * p.sdo[1] + v0 + c2, p.do_dtype) : 0.f;
+  };
+  auto store_step = [&]() __attribute__((always_inline)) {
+    lv.store(tid, s.v);
+    lu.store(tid, s.u);
+    ldu.store(tid, s.du);
+    lS.store(tid, s.S);
+    ldS.store(tid, s.dS);
+    s.dO[tid / VS][tid % VS] = rdo;
+  };
+  load_step(0);
+  store_step();
+  __syncthreads();
+  for (int e = tid; e < C * C; e += NTG) {
+    const int t = e / C, j = e % C;
+    s.m[t][j] = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
+  }
+  for (int vsi = 0; vsi < nvs; ++vsi) {
+    const int v0 = vsi * VS;
+    if (vsi + 1 < nvs) load_step(vsi + 1);
+    seg_mfma<NPW>(accW, am0, an0, ana, r, kq,
+                  seg<VS>([&](int m, int kk) { return s.du[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
+    seg_mfma<NPW>(accQ, am0, an0, ana, r, kq,
+                  seg<VS>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
+    seg_mfma<NPW>(accK, am0, an0, ana, r, kq,
+                  seg<VS>([&](int m, int kk) { return s.u[m][kk]; }, [&](int kk, int n) { return s.dS[n][kk]; }));
+    if (wave < 4)
+      seg_mfma<1>(accC, cm0, cn0, 1, r, kq,
+                  seg<VS>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.u[n][kk]; }));
+    else
+      seg_mfma<1>(accC, cm0, cn0, 1, r, kq,
+                  seg<VS>([&](int m, int kk) { return s.du[m][kk]; },
+                          [&](int kk, int n) { return s.bt[n] * s.v[n][kk]; }));
+    if (du_wave) {
+      f32x4 a[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+      seg_mfma<1>(a, um0, un0, 1, r, kq,
+                  seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = um0[0] + 4 * kq + i;
+        if (row < nval) stx<TIn>(p.dv, dvb + (int64_t)row * p.sdv[1] + v0 + r, s.bt[row] * a[0][i]);
+        vu_acc[i] = __builtin_fmaf(s.v[row][r], a[0][i], vu_acc[i]);
       }
-      stx<TIn>(p.dq, b * p.sdq[0] + t * p.sdq[1] + h * p.sdq[2] + kk, sq);
-      stx<TIn>(p.dk, b * p.sdk[0] + t * p.sdk[1] + h * p.sdk[2] + kk, sk);
+    }
+    for (int e = tid; e < K * VS; e += NTG) dgc_acc = __builtin_fmaf(s.S[e / VS][e % VS], s.dS[e / VS][e % VS], dgc_acc);
+    __syncthreads();
+    if (vsi + 1 < nvs) {
+      store_step();
+      __syncthreads();
+    }
+  }
+
+  // ---- accumulators -> LDS, row partials
+#pragma unroll
+  for (int i = 0; i < NPW; ++i) {
+    if (i < ana) {
+      float pq[4], pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = am0[i] + 4 * kq + e, col = an0[i] + r;
+        s.dw[row][col] = -accW[i][e];
+        pq[e] = sum16(s.q[row][col] * accQ[i][e]);
+        pk[e] = sum16(s.k[row][col] * accK[i][e]);
+      }
+      if (r == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s.rq[an0[i] / 16][am0[i] + 4 * kq + e] = pq[e];
+          s.rk[an0[i] / 16][am0[i] + 4 * kq + e] = pk[e];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = cm0[0] + 4 * kq + e, col = cn0[0] + r;
+    if (wave < 4) {
+      s.y[row][col] = scale * s.m[row][col] * accC[0][e];
+      s.yp[row][col] = scale * accC[0][e] * s.pm[row][col];
     } else {
-      const int64_t rh = e - n_qk;
-      const int64_t h = rh % p.H, r = rh / p.H;
-      const int64_t b = r / p.T, t = r % p.T;
-      float sg = 0.f, sb = 0.f;
-      for (int vs = 0; vs < p.nv; ++vs) {
-        sg += p.pg[vs * slab_g + rh];
-        sb += p.pb[vs * slab_g + rh];
+      s.dt[row][col] = accC[0][e];
+    }
+  }
+  if (du_wave) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = sum16(vu_acc[e]);
+      if (r == 0) s.vu[um0[0] + 4 * kq + e] = x;
+    }
+  }
+  {
+    float x = dgc_acc;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    if (lane == 0) s.red[wave] = x;
+  }
+  __syncthreads();
+  // dT = du (beta V)^T + dW (beta gam K)^T;  dW~ = T^T dW
+  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] += x; },
+                 seg<K>([&](int m, int kk) { return s.dw[m][kk]; },
+                        [&](int kk, int n) { return s.bt[n] * s.gam[n] * s.k[n][kk]; }));
+  mmx<NTG, C, K>(tid, [&](int m, int n, float x) { s.dwt[m][n] = x; },
+                 seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dw[kk][n]; }));
+  if (tid < C) {
+    float a = 0.f, b = 0.f;
+    for (int j = 0; j < NCT; ++j) {
+      a += s.rq[j][tid];
+      b += s.rk[j][tid];
+    }
+    s.dgam[tid] = scale * a;  // scale dO_t.(Q S)_t
+    s.dD[tid] = b;            // u_t.(K dS')_t
+  }
+  if (tid == 0) {
+    float x = 0.f;
+    for (int w = 0; w < NTG / 64; ++w) x += s.red[w];
+    s.dgC = x;  // <dS', S>
+  }
+  __syncthreads();
+  // Z = T^T dT;  k_t.dW~_t
+  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.z[m][n] = x; },
+                 seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dt[kk][n]; }));
+  {
+    const float kw = row_sum<NTG, K>(tid, [&](int rr, int i) { return s.k[rr][i] * s.dwt[rr][i]; });
+    if (tid % RL == 0) s.kw[tid / RL] = kw;
+  }
+  __syncthreads();
+  // dA = -tril_-1(Z T^T) -> dt
+  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
+                 seg<C>([&](int m, int kk) { return s.z[m][kk]; }, [&](int kk, int n) { return s.t[n][kk]; }));
+  __syncthreads();
+  // dKK = dA o beta_t M -> z;  dbeta and db
+  for (int e = tid; e < C * C; e += NTG) {
+    const int t = e / C, j = e % C;
+    s.z[t][j] = j < t ? s.dt[t][j] * s.bt[t] * s.m[t][j] : 0.f;
+  }
+  {
+    auto amat = [&](int t, int j) { return j < t ? s.bt[t] * s.m[t][j] * s.kk[t][j] : 0.f; };
+    const float am = row_sum<NTG, C>(tid, [&](int rr, int j) { return s.dt[rr][j] * s.m[rr][j] * s.kk[rr][j]; });
+    // db_t through M (dQK o QK) and A (dA o A): row sums minus column sums
+    const float mt = row_sum<NTG, C>(tid, [&](int rr, int j) {
+      return s.yp[rr][j] - s.yp[j][rr] + s.dt[rr][j] * amat(rr, j) - s.dt[j][rr] * amat(j, rr);
+    });
+    const float dd = row_sum<NTG, C>(tid, [&](int rr, int j) { return s.dD[j] * s.D[j]; });
+    if (tid % RL == 0) {
+      const int rr = tid / RL;
+      s.dbt[rr] = s.vu[rr] + s.gam[rr] * s.kw[rr] + am;
+      const float dgam = s.dgam[rr] + s.bt[rr] * s.kw[rr];
+      // ... and through gam, D and (last row) gam_C and every D_j
+      float d = mt + dgam * s.gam[rr] - s.dD[rr] * s.D[rr];
+      if (rr == C - 1) d += dd + s.dgC * s.gC;
+      s.db[rr] = d;
+    }
+  }
+  __syncthreads();
+  if (tid < nval) {
+    float acc = 0.f;
+    for (int j = tid; j < C; ++j) acc += s.db[j];
+    store_scalar(p.dg, head_base(rs, hi, p.sdg) + (int64_t)(t0 + tid) * p.sdg[1], p.g_dtype, acc);
+    store_scalar(p.dbeta, head_base(rs, hi, p.sdb) + (int64_t)(t0 + tid) * p.sdb[1], p.beta_dtype, s.dbt[tid]);
+  }
+  // dq = dQK K + scale diag(gam) dO S^T;
+  // dk = dQK^T Q + diag(D) u dS'^T + diag(beta gam) dW~ + (dKK + dKK^T) K
+  {
+    f32x4 aq[NPW], ak[NPW];
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+      aq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ak[i] = aq[i];
+    }
+    seg_mfma<NPW>(aq, am0, an0, ana, r, kq,
+                  seg<C>([&](int m, int kk) { return s.y[m][kk]; }, [&](int kk, int n) { return s.k[kk][n]; }));
+    seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
+                  seg<C>([&](int m, int kk) { return s.y[kk][m]; }, [&](int kk, int n) { return s.q[kk][n]; }));
+    seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
+                  seg<C>([&](int m, int kk) { return s.z[m][kk] + s.z[kk][m]; },
+                         [&](int kk, int n) { return s.k[kk][n]; }));
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+      if (i < ana) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = am0[i] + 4 * kq + e, col = an0[i] + r;
+          if (row < nval) {
+            const float dq = aq[i][e] + scale * s.gam[row] * accQ[i][e];
+            const float dk = ak[i][e] + s.D[row] * accK[i][e] + s.bt[row] * s.gam[row] * s.dwt[row][col];
+            stx<TIn>(p.dq, dqb + (int64_t)row * p.sdq[1] + col, dq);
+            stx<TIn>(p.dk, dkb + (int64_t)row * p.sdk[1] + col, dk);
+          }
+        }
       }
-      store_scalar(p.dg, b * p.sdg[0] + t * p.sdg[1] + h * p.sdg[2], p.g_dtype, sg);
-      store_scalar(p.dbeta, b * p.sdb[0] + t * p.sdb[1] + h * p.sdb[2], p.beta_dtype, sb);
     }
   }
 }
 
-// Workspace layout (floats, each part 256-byte aligned).
+// Workspace layout (each part 256-byte aligned).
 struct Layout {
-  int64_t ckpt, pq, pk, pg, pb, total;  // offsets in bytes
-  int64_t R, nslot;
+  int64_t rec, ckS, ckD, uu, du, total;  // offsets in bytes
+  int64_t nslot;
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
   Layout L;
-  const int64_t nv = V / BV, nch = (T + C - 1) / C;
-  L.R = n_seq > 0 ? (int64_t)T : (int64_t)B * T;
+  const int64_t nch = (T + C - 1) / C;
   L.nslot = n_seq > 0 ? nch + n_seq : (int64_t)B * nch;
+  const int64_t nr = L.nslot * H;
   int64_t off = 0;
-  L.ckpt = off;
-  off = align256(off + L.nslot * H * nv * K * BV * 4);
-  L.pq = off;
-  off = align256(off + nv * L.R * H * K * 4);
-  L.pk = off;
-  off = align256(off + nv * L.R * H * K * 4);
-  L.pg = off;
-  off = align256(off + nv * L.R * H * 4);
-  L.pb = off;
-  off = align256(off + nv * L.R * H * 4);
+  L.rec = off;
+  off = align256(off + nr * rec_size(K) * 4);
+  L.ckS = off;
+  off = align256(off + nr * K * V * 4);
+  L.ckD = off;
+  off = align256(off + nr * K * V * 4);
+  L.uu = off;
+  off = align256(off + nr * C * V * 4);
+  L.du = off;
+  off = align256(off + nr * C * V * 4);
   L.total = off;
   return L;
 }
 
+template <typename TIn, int K>
+int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
+  if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
+  hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
+  if (nrec > 0) hipLaunchKernelGGL((grad_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
+  return (int)hipGetLastError();
+}
+
 template <typename TIn>
-int launch_t(const BArgs& a, const RArgs& r, int K, int grid, hipStream_t s) {
+int launch_t(const BArgs& a, int K, int64_t nrec, hipStream_t s) {
   switch (K) {
-    case 32: hipLaunchKernelGGL((bwd_kernel<TIn, 32>), dim3(grid), dim3(NT), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((bwd_kernel<TIn, 64>), dim3(grid), dim3(NT), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((bwd_kernel<TIn, 128>), dim3(grid), dim3(NT), 0, s, a); break;
+    case 32: return launch_k<TIn, 32>(a, nrec, s);
+    case 64: return launch_k<TIn, 64>(a, nrec, s);
+    case 128: return launch_k<TIn, 128>(a, nrec, s);
     default: return GDN_ERR_UNSUPPORTED;
   }
-  int err = (int)hipGetLastError();
-  if (err != 0) return err;
-  const int64_t work = r.R * r.H * (r.K + 1);
-  const int rgrid = (int)std::min<int64_t>((work + 255) / 256, 4096);
-  if (rgrid > 0) hipLaunchKernelGGL((reduce_kernel<TIn>), dim3(rgrid), dim3(256), 0, s, r);
-  return (int)hipGetLastError();
 }
 
 }  // namespace bwd
@@ -671,9 +962,11 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
     }
   }
   const int64_t units = (int64_t)P.B * P.H * (P.V / bwd::BV);
-  if (units > 0x7fffffffLL || (int64_t)P.B * P.T * P.H * P.K >= (1LL << 40)) return GDN_ERR_BAD_SHAPE;
   // B is the number of sequences when cu_seqlens is given (one packed batch)
   const bwd::Layout L = bwd::layout(P.B, P.T, P.H, P.K, P.V, P.cu_seqlens ? P.B : 0);
+  const int64_t nrec = L.nslot * P.H;
+  if (2 * units > 0x7fffffffLL || nrec > 0x7fffffffLL || (int64_t)P.B * P.T * P.H * P.K >= (1LL << 40))
+    return GDN_ERR_BAD_SHAPE;
   if (P.workspace == nullptr || reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 ||
       P.workspace_bytes < L.total)
     return GDN_ERR_WORKSPACE;
@@ -682,43 +975,35 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   char* ws = static_cast<char*>(P.workspace);
   bwd::BArgs a = {};
   a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
-  a.d_o = P.d_o; a.dfs = P.d_final_state; a.dv = P.dv; a.dh0 = P.dh0;
-  a.ckpt = reinterpret_cast<float*>(ws + L.ckpt);
-  a.pq = reinterpret_cast<float*>(ws + L.pq);
-  a.pk = reinterpret_cast<float*>(ws + L.pk);
-  a.pg = reinterpret_cast<float*>(ws + L.pg);
-  a.pb = reinterpret_cast<float*>(ws + L.pb);
+  a.d_o = P.d_o; a.dfs = P.d_final_state;
+  a.dq = P.dq; a.dk = P.dk; a.dv = P.dv; a.dg = P.dg; a.dbeta = P.dbeta; a.dh0 = P.dh0;
+  a.rec = reinterpret_cast<float*>(ws + L.rec);
+  a.ckS = reinterpret_cast<float*>(ws + L.ckS);
+  a.ckD = reinterpret_cast<float*>(ws + L.ckD);
+  a.uu = reinterpret_cast<float*>(ws + L.uu);
+  a.du = reinterpret_cast<float*>(ws + L.du);
   for (int d = 0; d < 3; ++d) {
     a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
     a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.sdo[d] = P.do_stride[d];
-    a.sdv[d] = P.dv_stride[d];
+    a.sdq[d] = P.dq_stride[d]; a.sdk[d] = P.dk_stride[d]; a.sdv[d] = P.dv_stride[d];
+    a.sdg[d] = P.dg_stride[d]; a.sdb[d] = P.dbeta_stride[d];
   }
   for (int d = 0; d < 4; ++d) {
     a.sh0[d] = P.h0_stride[d]; a.sdfs[d] = P.dfs_stride[d]; a.sdh0[d] = P.dh0_stride[d];
   }
-  a.R = L.R;
   a.B = P.B; a.T = P.T; a.H = P.H; a.V = P.V; a.nv = P.V / bwd::BV;
+  a.nchmax = (P.T + bwd::C - 1) / bwd::C;
+  a.units = (int)units;
   a.scale = P.scale;
   a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.do_dtype = P.do_dtype;
   a.cu = P.cu_seqlens;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
 
-  bwd::RArgs r = {};
-  r.pq = a.pq; r.pk = a.pk; r.pg = a.pg; r.pb = a.pb;
-  r.dq = P.dq; r.dk = P.dk; r.dg = P.dg; r.dbeta = P.dbeta;
-  for (int d = 0; d < 3; ++d) {
-    r.sdq[d] = P.dq_stride[d]; r.sdk[d] = P.dk_stride[d]; r.sdg[d] = P.dg_stride[d];
-    r.sdb[d] = P.dbeta_stride[d];
-  }
-  r.R = P.T > 0 ? L.R : 0;
-  r.T = P.T > 0 ? P.T : 1; r.H = P.H; r.K = P.K; r.nv = a.nv;
-  r.qkv_dtype = P.qkv_dtype; r.g_dtype = P.g_dtype; r.beta_dtype = P.beta_dtype;
-
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int grid = (int)units;
+  const int64_t nrec_launch = P.T > 0 ? nrec : 0;
   switch (P.qkv_dtype) {
-    case GDN_DTYPE_F16: return bwd::launch_t<f16>(a, r, P.K, grid, s);
-    case GDN_DTYPE_BF16: return bwd::launch_t<bf16_t>(a, r, P.K, grid, s);
-    default: return bwd::launch_t<float>(a, r, P.K, grid, s);
+    case GDN_DTYPE_F16: return bwd::launch_t<f16>(a, P.K, nrec_launch, s);
+    case GDN_DTYPE_BF16: return bwd::launch_t<bf16_t>(a, P.K, nrec_launch, s);
+    default: return bwd::launch_t<float>(a, P.K, nrec_launch, s);
   }
 }
