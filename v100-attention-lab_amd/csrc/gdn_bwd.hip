@@ -36,8 +36,9 @@
 //      chunk's dS' and du and finally dh0;
 //   3. grad_kernel, one workgroup per (chunk, head) over all of V: every
 //      gradient of the chunk from the stored S, dS', u, du and the record,
-//      written directly in the output dtypes (V is walked in 16-column steps
-//      with the C x K products held in MFMA accumulators).
+//      written directly in the output dtypes (V is walked in 32-column steps,
+//      16 when V is an odd multiple of 16, with the C x K products held in
+//      MFMA accumulators).
 // Packed sequences (cu_seqlens): sequence i owns chunk slots floor(t0 / C) +
 // i onwards, one per chunk; the ranges are disjoint, so every launch handles
 // packed sequences like a batch.
@@ -49,7 +50,6 @@ namespace bwd {
 
 constexpr int C = 32;
 constexpr int BV = 16;    // state columns per workgroup of the recurrences
-constexpr int VS = 16;    // V columns per step of the gradient kernel's V walk
 constexpr int NTP = 256;  // threads: prep_kernel and recur_kernel (4 waves)
 constexpr int NTG = 512;  // threads: grad_kernel (8 waves)
 
@@ -120,6 +120,20 @@ __device__ __forceinline__ void stx(void* base, int64_t off, float x) {
   else static_cast<uint16_t*>(base)[off] = float_to_bf16_bits(x);
 }
 
+// One element's raw bits (fp32 bits, or the 16-bit value zero-extended);
+// bits_to_float converts where the value is used.  A load whose result is
+// converted right away makes the wave wait for it and for every load issued
+// before it, which would drain loads meant to run ahead.
+__device__ __forceinline__ uint32_t load_bits(const void* base, int64_t off, int dtype) {
+  return dtype == GDN_DTYPE_F32 ? static_cast<const uint32_t*>(base)[off]
+                                : (uint32_t) static_cast<const uint16_t*>(base)[off];
+}
+__device__ __forceinline__ float bits_to_float(uint32_t x, int dtype) {
+  if (dtype == GDN_DTYPE_F32) return __uint_as_float(x);
+  if (dtype == GDN_DTYPE_F16) return (float)__builtin_bit_cast(f16, (uint16_t)x);
+  return __uint_as_float(x << 16);
+}
+
 // ROWS x COLS block of a row-major TIn array (row stride `rs` elements,
 // 16-byte aligned rows) -> LDS as fp32, in two steps so that all global loads
 // of a phase are issued before the first LDS store.  Rows >= nvalid read as
@@ -143,10 +157,14 @@ struct RowLoad {
     for (int i = 0; i < N; ++i) {
       const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
       if (e < ROWS * RV) {
-        float x[VEC];
-        unpack16<TIn>(r[i], x);
+        if constexpr (std::is_same<TIn, float>::value && LD % 4 == 0) {
+          *reinterpret_cast<u32x4*>(&dst[t][col]) = r[i];
+        } else {
+          float x[VEC];
+          unpack16<TIn>(r[i], x);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) dst[t][col + j] = x[j];
+          for (int j = 0; j < VEC; ++j) dst[t][col + j] = x[j];
+        }
       }
     }
   }
@@ -171,7 +189,9 @@ template <int G, int KD, typename FA, typename FB>
 __device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], const int (&n0)[G],
                                          int ng, int r, int kq, const Seg<KD, FA, FB>& s) {
   static_assert(KD % 4 == 0, "contraction length");
-#pragma unroll 2
+  // short contractions fully unrolled: all their operand reads in flight
+  constexpr int UNR = KD <= 32 ? KD / 4 : 2;
+#pragma unroll UNR
   for (int k0 = 0; k0 < KD; k0 += 4) {
     float av[G], bv[G];
 #pragma unroll
@@ -230,11 +250,42 @@ __device__ __forceinline__ float row_sum(int tid, F&& f) {
   return acc;
 }
 
-// Sum over the 16 lanes of a lane's group (the lanes that differ in bits 0-3).
+// Sum over the 16 lanes of a lane's row (lanes 16 j .. 16 j + 15), returned
+// to all of them: rotate-and-add within the row on DPP (row_ror 8, 4, 2, 1).
+template <int CTRL>
+__device__ __forceinline__ float dpp_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float sum16(float x) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+  x += dpp_ror<0x128>(x);
+  x += dpp_ror<0x124>(x);
+  x += dpp_ror<0x122>(x);
+  x += dpp_ror<0x121>(x);
   return x;
+}
+
+// Inclusive prefix sum over lanes 0..31 (and separately 32..63): DPP
+// row_shr 1, 2, 4, 8 within each row of 16 lanes (lanes shifted in from
+// outside the row read 0), then row_bcast:15 adds the totals of rows 0 / 2
+// to rows 1 / 3.  All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_shr0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float scan32(float x) {
+  x += dpp_shr0<0x111>(x);
+  x += dpp_shr0<0x112>(x);
+  x += dpp_shr0<0x114>(x);
+  x += dpp_shr0<0x118>(x);
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+  return x;
+}
+
+// 16 bytes of LDS as four floats.
+template <int LD>
+__device__ __forceinline__ f32x4 ld4(const float (*x)[LD], int row, int col) {
+  static_assert(LD % 4 == 0, "16-byte rows");
+  return *reinterpret_cast<const f32x4*>(&x[row][col]);
 }
 
 // Chunk slot -> (sequence rows, chunk).  False for a slot that holds no
@@ -357,7 +408,15 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
 // ---------------------------------------------------------------------------
 // 2. the two recurrences (one launch: blocks [0, units) walk forward, the
 //    rest backward)
+//
+// Per chunk each walk needs one product through the carried state and one
+// that updates it.  The first (u or du: two 16 x 16 tiles, contraction
+// C + K) is split over the four waves by contraction range and the partial
+// tiles summed once, so that every wave works in both products.  The chunk's record and input rows for the next
+// chunk are loaded into registers while the current chunk computes.
 // ---------------------------------------------------------------------------
+
+constexpr int NWP = NTP / 64;  // waves of a recurrence workgroup
 
 template <int K>
 struct alignas(16) FSmem {
@@ -365,6 +424,7 @@ struct alignas(16) FSmem {
   float t[C][C + 1];
   float w[C][K + 1], k[C][K + 1];
   float v[C][BV + 1], u[C][BV + 1];
+  float part[NWP][C][BV + 1];  // partial u tiles, one per wave
   float bt[C], D[C];
   float gC;
 };
@@ -375,6 +435,7 @@ struct alignas(16) RSmem {
   float pm[C][C + 1];
   float q[C][K + 1], k[C][K + 1], w[C][K + 1];
   float dO[C][BV + 1], du[C][BV + 1];
+  float part[NWP][C][BV + 1];  // partial du tiles, one per wave
   float gam[C], D[C];
   float gC;
 };
@@ -385,12 +446,85 @@ union FRSmem {
   RSmem<K> r;
 };
 
+// acc[g] += sum over kc in [kc0, kc0 + LEN) of a(m, kc) b(kc, n) for the two
+// C x 16 tiles (rows 0-15, 16-31), where kc < C1 takes (a1, b1) at kc and
+// kc >= C1 takes (a2, b2) at kc - C1.  kc0 is wave-uniform, so the two
+// loops have uniform bounds and no per-lane branches.
+template <int LEN, int C1, typename FA1, typename FB1, typename FA2, typename FB2>
+__device__ __forceinline__ void split_tiles(f32x4 (&acc)[2], int kc0, int r, int kq, FA1&& a1, FB1&& b1,
+                                            FA2&& a2, FB2&& b2) {
+  static_assert(LEN % 4 == 0 && C1 % 4 == 0, "contraction steps");
+  const int e1 = min(kc0 + LEN, C1);
+  for (int k0 = kc0; k0 < e1; k0 += 4) {
+    const float b0 = b1(k0 + kq, r);
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1(r, k0 + kq), b0, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1(16 + r, k0 + kq), b0, acc[1], 0, 0, 0);
+  }
+  for (int k0 = max(kc0, C1) - C1; k0 < kc0 + LEN - C1; k0 += 4) {
+    const float b0 = b2(k0 + kq, r);
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a2(r, k0 + kq), b0, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a2(16 + r, k0 + kq), b0, acc[1], 0, 0, 0);
+  }
+}
+
+// K x BV state block (LDS) -> rows of a [K][V] fp32 array, 16 bytes per
+// store.  A fixed count of stores per thread (no loop over a thread-dependent
+// range), so that waits for loads issued before them need not wait for them.
+template <int K>
+__device__ __forceinline__ void store_state(int tid, const float (*st)[BV + 1], float* dst, int64_t ld) {
+  constexpr int NV = K * BV / 4, PER = (NV + NTP - 1) / NTP;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid + i * NTP;
+    if (NV % NTP == 0 || e < NV) {
+      const int kk = e / (BV / 4), c4 = (e % (BV / 4)) * 4;
+      *reinterpret_cast<f32x4*>(dst + kk * ld + c4) = f32x4{st[kk][c4], st[kk][c4 + 1], st[kk][c4 + 2], st[kk][c4 + 3]};
+    }
+  }
+}
+
+// Next chunk's state-independent inputs of the forward walk, in registers.
+template <typename TIn, int K>
+struct FNext {
+  RowLoad<float, C, C, NTP> lt;
+  RowLoad<float, C, K, NTP> lw;
+  RowLoad<TIn, C, K, NTP> lk;
+  RowLoad<TIn, C, BV, NTP> lv;
+  uint32_t bv;
+  float dv, gc;
+  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* kg, const TIn* vg,
+                                       int64_t bb, int t0, int nval) {
+    using R = Rec<K>;
+    const float* const rec = p.rec + ri * R::SIZE;
+    lt.load(tid, rec + R::T, C, C);
+    lw.load(tid, rec + R::W, K, C);
+    lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    lv.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
+    bv = (tid < nval) ? load_bits(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0u;
+    dv = tid < C ? rec[R::G + 2 * C + tid] : 0.f;
+    gc = tid == 0 ? rec[R::G + 3 * C] : 0.f;
+  }
+  __device__ __forceinline__ void store(FSmem<K>& s, int tid, int beta_dtype) const {
+    lt.store(tid, s.t);
+    lw.store(tid, s.w);
+    lk.store(tid, s.k);
+    lv.store(tid, s.v);
+    if (tid < C) {
+      s.bt[tid] = bits_to_float(bv, beta_dtype);
+      s.D[tid] = dv;
+    }
+    if (tid == 0) s.gC = gc;
+  }
+};
+
 // Forward walk: S at each chunk start -> ckS, u -> uu.
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_forward(const BArgs& p, FSmem<K>& s, const RowSpan& rs, int bi, int hi,
                                              int v0, int64_t slot0) {
-  using R = Rec<K>;
-  const int tid = threadIdx.x;
+  constexpr int LEN = (C + K) / NWP;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
   const int nch = (rs.T + C - 1) / C;
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
   const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
@@ -399,109 +533,83 @@ __device__ __forceinline__ void walk_forward(const BArgs& p, FSmem<K>& s, const 
     const int kk = e / BV, c2 = e % BV;
     s.S[kk][c2] = p.h0 ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]] : 0.f;
   }
+  FNext<TIn, K> nx;
+  if (nch > 0) {
+    nx.load(p, tid, slot0 * p.H + hi, kg, vg, bb, 0, min(C, rs.T));
+    nx.store(s, tid, p.beta_dtype);
+  }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
-    const int t0 = c * C, nval = min(C, rs.T - t0);
     const int64_t ri = (slot0 + c) * p.H + hi;
-    const float* const rec = p.rec + ri * R::SIZE;
+    if (c + 1 < nch) nx.load(p, tid, ri + p.H, kg, vg, bb, (c + 1) * C, min(C, rs.T - (c + 1) * C));
     float* const cks = p.ckS + ri * (int64_t)K * p.V + v0;
     float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
-    RowLoad<float, C, C, NTP> lt;
-    RowLoad<float, C, K, NTP> lw;
-    RowLoad<TIn, C, K, NTP> lk;
-    RowLoad<TIn, C, BV, NTP> lv;
-    lt.load(tid, rec + R::T, C, C);
-    lw.load(tid, rec + R::W, K, C);
-    lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
-    lv.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
-    float bv = 0.f, dv = 0.f, gc = 0.f;
-    if (tid < C) {
-      bv = tid < nval ? load_scalar(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0.f;
-      dv = rec[R::G + 2 * C + tid];
+    store_state<K>(tid, s.S, cks, p.V);
+    // partial u = [T, -W] [diag(beta) V; S] over this wave's contraction range
+    {
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      split_tiles<LEN, C>(
+          acc, wave * LEN, r, kq, [&](int m, int kk) { return s.t[m][kk]; },
+          [&](int kk, int n) { return s.bt[kk] * s.v[kk][n]; }, [&](int m, int kk) { return -s.w[m][kk]; },
+          [&](int kk, int n) { return s.S[kk][n]; });
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s.part[wave][4 * kq + i][r] = acc[0][i];
+        s.part[wave][16 + 4 * kq + i][r] = acc[1][i];
+      }
     }
-    if (tid == 0) gc = rec[R::G + 3 * C];
-    for (int e = tid; e < K * BV / 4; e += NTP) {
-      const int kk = e / (BV / 4), c4 = (e % (BV / 4)) * 4;
-      *reinterpret_cast<f32x4*>(cks + (int64_t)kk * p.V + c4) =
-          f32x4{s.S[kk][c4], s.S[kk][c4 + 1], s.S[kk][c4 + 2], s.S[kk][c4 + 3]};
-    }
-    lt.store(tid, s.t);
-    lw.store(tid, s.w);
-    lk.store(tid, s.k);
-    lv.store(tid, s.v);
-    if (tid < C) {
-      s.bt[tid] = bv;
-      s.D[tid] = dv;
-    }
-    if (tid == 0) s.gC = gc;
     __syncthreads();
-    // u = T diag(beta) V - W S
-    mmx<NTP, C, BV>(
-        tid,
-        [&](int m, int n, float x) {
-          s.u[m][n] = x;
-          uo[(int64_t)m * p.V + n] = x;
-        },
-        seg<C>([&](int m, int kk) { return s.t[m][kk]; }, [&](int kk, int n) { return s.bt[kk] * s.v[kk][n]; }),
-        seg<K>([&](int m, int kk) { return -s.w[m][kk]; }, [&](int kk, int n) { return s.S[kk][n]; }));
+    // u = the sum of the partial tiles, once
+#pragma unroll
+    for (int i = 0; i < C * BV / NTP; ++i) {
+      const int e = tid + i * NTP, m = e / BV, n = e % BV;
+      float x = s.part[0][m][n];
+#pragma unroll
+      for (int w = 1; w < NWP; ++w) x += s.part[w][m][n];
+      s.u[m][n] = x;
+      uo[(int64_t)m * p.V + n] = x;
+    }
     __syncthreads();
     // S <- gam_C S + K^T diag(D) u
     mmx<NTP, K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
                     seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
                            [&](int kk, int n) { return s.u[kk][n]; }));
     __syncthreads();
+    if (c + 1 < nch) {
+      nx.store(s, tid, p.beta_dtype);
+      __syncthreads();
+    }
   }
 }
 
-// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.
+// Next chunk's state-independent inputs of the backward walk, in registers.
 template <typename TIn, int K>
-__device__ __forceinline__ void walk_backward(const BArgs& p, RSmem<K>& s, const RowSpan& rs, int bi, int hi,
-                                              int v0, int64_t slot0) {
-  using R = Rec<K>;
-  const int tid = threadIdx.x;
-  const int nch = (rs.T + C - 1) / C;
-  const float scale = p.scale;
-  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
-  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
-  const int64_t dob = head_base(rs, hi, p.sdo) + v0;
-  constexpr int NDO = C * BV / NTP;
+struct RNext {
+  static constexpr int NDO = C * BV / NTP;
   static_assert(C * BV % NTP == 0, "dO elements per thread");
-  for (int e = tid; e < K * BV; e += NTP) {
-    const int kk = e / BV, c2 = e % BV;
-    s.dS[kk][c2] =
-        p.dfs ? p.dfs[bi * p.sdfs[0] + hi * p.sdfs[1] + kk * p.sdfs[2] + (v0 + c2) * p.sdfs[3]] : 0.f;
-  }
-  __syncthreads();
-  for (int c = nch - 1; c >= 0; --c) {
-    const int t0 = c * C, nval = min(C, rs.T - t0);
-    const int64_t ri = (slot0 + c) * p.H + hi;
+  RowLoad<float, C, C, NTP> lp;
+  RowLoad<float, C, K, NTP> lw;
+  RowLoad<TIn, C, K, NTP> lq, lk;
+  uint32_t rdo[NDO];
+  float gm, dv, gc;
+  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
+                                       int64_t dob, int t0, int nval) {
+    using R = Rec<K>;
     const float* const rec = p.rec + ri * R::SIZE;
-    float* const ckd = p.ckD + ri * (int64_t)K * p.V + v0;
-    float* const duo = p.du + ri * (int64_t)C * p.V + v0;
-    RowLoad<float, C, C, NTP> lp;
-    RowLoad<float, C, K, NTP> lw;
-    RowLoad<TIn, C, K, NTP> lq, lk;
     lp.load(tid, rec + R::PM, C, C);
     lw.load(tid, rec + R::W, K, C);
     lq.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
     lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
-    float rdo[NDO];
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int e = tid + i * NTP, t = e / BV, c2 = e % BV;
-      rdo[i] = t < nval ? load_scalar(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype) : 0.f;
+      rdo[i] = t < nval ? load_bits(p.d_o, dob + (int64_t)(t0 + t) * p.sdo[1] + c2, p.do_dtype) : 0u;
     }
-    float gm = 0.f, dv = 0.f, gc = 0.f;
-    if (tid < C) {
-      gm = rec[R::G + C + tid];
-      dv = rec[R::G + 2 * C + tid];
-    }
-    if (tid == 0) gc = rec[R::G + 3 * C];
-    for (int e = tid; e < K * BV / 4; e += NTP) {
-      const int kk = e / (BV / 4), c4 = (e % (BV / 4)) * 4;
-      *reinterpret_cast<f32x4*>(ckd + (int64_t)kk * p.V + c4) =
-          f32x4{s.dS[kk][c4], s.dS[kk][c4 + 1], s.dS[kk][c4 + 2], s.dS[kk][c4 + 3]};
-    }
+    gm = tid < C ? rec[R::G + C + tid] : 0.f;
+    dv = tid < C ? rec[R::G + 2 * C + tid] : 0.f;
+    gc = tid == 0 ? rec[R::G + 3 * C] : 0.f;
+  }
+  __device__ __forceinline__ void store(RSmem<K>& s, int tid, int do_dtype) const {
     lp.store(tid, s.pm);
     lw.store(tid, s.w);
     lq.store(tid, s.q);
@@ -509,23 +617,71 @@ __device__ __forceinline__ void walk_backward(const BArgs& p, RSmem<K>& s, const
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int e = tid + i * NTP;
-      s.dO[e / BV][e % BV] = rdo[i];
+      s.dO[e / BV][e % BV] = bits_to_float(rdo[i], do_dtype);
     }
     if (tid < C) {
       s.gam[tid] = gm;
       s.D[tid] = dv;
     }
     if (tid == 0) s.gC = gc;
+  }
+};
+
+// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.
+template <typename TIn, int K>
+__device__ __forceinline__ void walk_backward(const BArgs& p, RSmem<K>& s, const RowSpan& rs, int bi, int hi,
+                                              int v0, int64_t slot0) {
+  constexpr int LEN = (C + K) / NWP;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int nch = (rs.T + C - 1) / C;
+  const float scale = p.scale;
+  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const int64_t dob = head_base(rs, hi, p.sdo) + v0;
+  for (int e = tid; e < K * BV; e += NTP) {
+    const int kk = e / BV, c2 = e % BV;
+    s.dS[kk][c2] =
+        p.dfs ? p.dfs[bi * p.sdfs[0] + hi * p.sdfs[1] + kk * p.sdfs[2] + (v0 + c2) * p.sdfs[3]] : 0.f;
+  }
+  RNext<TIn, K> nx;
+  if (nch > 0) {
+    const int t0 = (nch - 1) * C;
+    nx.load(p, tid, (slot0 + nch - 1) * p.H + hi, qg, kg, dob, t0, rs.T - t0);
+    nx.store(s, tid, p.do_dtype);
+  }
+  __syncthreads();
+  for (int c = nch - 1; c >= 0; --c) {
+    const int64_t ri = (slot0 + c) * p.H + hi;
+    if (c > 0) nx.load(p, tid, ri - p.H, qg, kg, dob, (c - 1) * C, C);
+    float* const ckd = p.ckD + ri * (int64_t)K * p.V + v0;
+    float* const duo = p.du + ri * (int64_t)C * p.V + v0;
+    store_state<K>(tid, s.dS, ckd, p.V);
+    // partial du = [scale P^T, diag(D) K] [dO; dS'] over this wave's range
+    {
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      split_tiles<LEN, C>(
+          acc, wave * LEN, r, kq, [&](int m, int kk) { return scale * s.pm[kk][m]; },
+          [&](int kk, int n) { return s.dO[kk][n]; }, [&](int m, int kk) { return s.D[m] * s.k[m][kk]; },
+          [&](int kk, int n) { return s.dS[kk][n]; });
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s.part[wave][4 * kq + i][r] = acc[0][i];
+        s.part[wave][16 + 4 * kq + i][r] = acc[1][i];
+      }
+    }
     __syncthreads();
-    // du = scale P^T dO + diag(D) K dS'
-    mmx<NTP, C, BV>(
-        tid,
-        [&](int m, int n, float x) {
-          s.du[m][n] = x;
-          duo[(int64_t)m * p.V + n] = x;
-        },
-        seg<C>([&](int m, int kk) { return scale * s.pm[kk][m]; }, [&](int kk, int n) { return s.dO[kk][n]; }),
-        seg<K>([&](int m, int kk) { return s.D[m] * s.k[m][kk]; }, [&](int kk, int n) { return s.dS[kk][n]; }));
+    // du = the sum of the partial tiles, once
+#pragma unroll
+    for (int i = 0; i < C * BV / NTP; ++i) {
+      const int e = tid + i * NTP, m = e / BV, n = e % BV;
+      float x = s.part[0][m][n];
+#pragma unroll
+      for (int w = 1; w < NWP; ++w) x += s.part[w][m][n];
+      s.du[m][n] = x;
+      duo[(int64_t)m * p.V + n] = x;
+    }
     __syncthreads();
     // dS <- scale Q^T diag(gam) dO + gam_C dS' - W^T du
     mmx<NTP, K, BV>(tid, [&](int m, int n, float x) { s.dS[m][n] = x + s.gC * s.dS[m][n]; },
@@ -533,6 +689,10 @@ __device__ __forceinline__ void walk_backward(const BArgs& p, RSmem<K>& s, const
                            [&](int kk, int n) { return s.dO[kk][n]; }),
                     seg<C>([&](int m, int kk) { return -s.w[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
     __syncthreads();
+    if (c > 0) {
+      nx.store(s, tid, p.do_dtype);
+      __syncthreads();
+    }
   }
   if (p.dh0 != nullptr) {
     for (int e = tid; e < K * BV; e += NTP) {
@@ -566,9 +726,12 @@ __global__ __launch_bounds__(NTP) void recur_kernel(const BArgs p) {
 // 3. every gradient of a chunk
 // ---------------------------------------------------------------------------
 
-template <int K>
+template <int K, int VS>
 struct alignas(16) GSmem {
-  static constexpr int KD = K + 1, CD = C + 1, SD = VS + 1;
+  // SD = VS + 4: rows of the V-step tiles are read 16 bytes per lane, lane
+  // (r, kq) at row r, columns 4 kq .. 4 kq + 3 of a 16-column group; a row
+  // stride of 4 (mod 32) words makes each 8-lane group's reads conflict-free.
+  static constexpr int KD = K + 1, CD = C + 1, SD = VS + 4;
   float q[C][KD], k[C][KD];
   float dw[C][KD];   // dW = -du S^T
   float dwt[C][KD];  // dW~ = T^T dW
@@ -581,16 +744,19 @@ struct alignas(16) GSmem {
   float S[K][SD], dS[K][SD];
   float b[C], gam[C], D[C], bt[C];
   float rq[K / 16][C], rk[K / 16][C];  // row partials, one row per 16-column tile
-  float vu[C], kw[C], dgam[C], dD[C], db[C], dbt[C];
+  float vu[VS / 16][C];  // v.dU~ row partials, one row per 16-column tile
+  float kw[C], dgam[C], dD[C], db[C], dbt[C];
   float red[NTG / 64];
   float gC, dgC;
 };
 
-template <typename TIn, int K>
+// VS: V columns per step of the V walk (32, or 16 when V is an odd
+// multiple of 16).
+template <typename TIn, int K, int VS>
 __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   using R = Rec<K>;
   constexpr int RL = NTG / C;
-  __shared__ GSmem<K> s;
+  __shared__ GSmem<K, VS> s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, kq = lane >> 4;
@@ -615,35 +781,18 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   const int64_t dqb = head_base(rs, hi, p.sdq) + (int64_t)t0 * p.sdq[1];
   const int64_t dkb = head_base(rs, hi, p.sdk) + (int64_t)t0 * p.sdk[1];
 
-  // ---- q, k, beta and the record
-  {
-    RowLoad<TIn, C, K, NTG> lq, lk;
-    RowLoad<float, C, C, NTG> lt, lp, lkk;
-    lq.load(tid, static_cast<const TIn*>(p.q) + qb, p.sq[1], nval);
-    lk.load(tid, static_cast<const TIn*>(p.k) + kb, p.sk[1], nval);
-    lt.load(tid, rec + R::T, C, C);
-    lp.load(tid, rec + R::PM, C, C);
-    lkk.load(tid, rec + R::KK, C, C);
-    const float gate = tid < 4 * C ? rec[R::G + tid] : 0.f;
-    float bv = 0.f;
-    if (tid < nval)
-      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
-    lq.store(tid, s.q);
-    lk.store(tid, s.k);
-    lt.store(tid, s.t);
-    lp.store(tid, s.pm);
-    lkk.store(tid, s.kk);
-    if (tid < C) {
-      s.b[tid] = gate;
-      s.bt[tid] = bv;
-    } else if (tid < 2 * C) {
-      s.gam[tid - C] = gate;
-    } else if (tid < 3 * C) {
-      s.D[tid - 2 * C] = gate;
-    } else if (tid == 3 * C) {
-      s.gC = gate;
-    }
-  }
+  // ---- q, k, beta and the record: loads issued here, stored to LDS with
+  // the first V step's rows (one wait for both)
+  RowLoad<TIn, C, K, NTG> lq, lk;
+  RowLoad<float, C, C, NTG> lt, lp, lkk;
+  lq.load(tid, static_cast<const TIn*>(p.q) + qb, p.sq[1], nval);
+  lk.load(tid, static_cast<const TIn*>(p.k) + kb, p.sk[1], nval);
+  lt.load(tid, rec + R::T, C, C);
+  lp.load(tid, rec + R::PM, C, C);
+  lkk.load(tid, rec + R::KK, C, C);
+  const float gate = tid < 4 * C ? rec[R::G + tid] : 0.f;
+  const uint32_t bvb =
+      tid < nval ? load_bits(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0u;
 
   // ---- walk V in VS-column steps.  The C x K products (dW, dO S^T,
   // u dS'^T) accumulate in registers: wave w owns tiles w + 8 i of the
@@ -667,9 +816,10 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   // one C x C tile per wave: dO u^T (waves 0-3) or du (beta V)^T (waves 4-7)
   const int cm0[1] = {((wave & 3) >> 1) * 16}, cn0[1] = {(wave & 1) * 16};
   f32x4 accC[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-  // dU~ = T^T du of the step: waves 4 and 5, rows 16 (wave - 4) .. + 15
-  const bool du_wave = wave == 4 || wave == 5;
-  const int um0[1] = {16 * (wave & 1)}, un0[1] = {0};
+  // dU~ = T^T du of the step: waves 4 .. 4 + NDU - 1, one 16 x 16 tile each
+  constexpr int NDU = (C / 16) * (VS / 16);
+  const bool du_wave = wave >= 4 && wave < 4 + NDU;
+  const int um0[1] = {((wave - 4) / (VS / 16)) * 16}, un0[1] = {((wave - 4) % (VS / 16)) * 16};
   float vu_acc[4] = {0.f, 0.f, 0.f, 0.f};
   float dgc_acc = 0.f;
 
@@ -677,8 +827,9 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   RowLoad<TIn, C, VS, NTG> lv;
   RowLoad<float, C, VS, NTG> lu, ldu;
   RowLoad<float, K, VS, NTG> lS, ldS;
-  static_assert(C * VS == NTG, "one dO element per thread");
-  float rdo = 0.f;
+  constexpr int NDO = C * VS / NTG;
+  static_assert(C * VS % NTG == 0, "dO elements per thread");
+  uint32_t rdo[NDO];
   auto load_step = [&](int vsi) __attribute__((always_inline)) {
     const int v0 = vsi * VS;
     lv.load(tid, static_cast<const TIn*>(p.v) + vb + v0, p.sv[1], nval);
@@ -686,8 +837,11 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     ldu.load(tid, dug + v0, p.V, C);
     lS.load(tid, cks + v0, p.V, K);
     ldS.load(tid, ckd + v0, p.V, K);
-    const int t = tid / VS, c2 = tid % VS;
-    rdo = t < nval ? load_scalar(p.d_o, dob + (int64_t)t * p.sdo[1] + v0 + c2, p.do_dtype) : 0.f;
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int e = tid + i * NTG, t = e / VS, c2 = e % VS;
+      rdo[i] = t < nval ? load_bits(p.d_o, dob + (int64_t)t * p.sdo[1] + v0 + c2, p.do_dtype) : 0u;
+    }
   };
   auto store_step = [&]() __attribute__((always_inline)) {
     lv.store(tid, s.v);
@@ -695,9 +849,28 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     ldu.store(tid, s.du);
     lS.store(tid, s.S);
     ldS.store(tid, s.dS);
-    s.dO[tid / VS][tid % VS] = rdo;
+#pragma unroll
+    for (int i = 0; i < NDO; ++i) {
+      const int e = tid + i * NTG;
+      s.dO[e / VS][e % VS] = bits_to_float(rdo[i], p.do_dtype);
+    }
   };
   load_step(0);
+  lq.store(tid, s.q);
+  lk.store(tid, s.k);
+  lt.store(tid, s.t);
+  lp.store(tid, s.pm);
+  lkk.store(tid, s.kk);
+  if (tid < C) {
+    s.b[tid] = gate;
+    s.bt[tid] = bits_to_float(bvb, p.beta_dtype);
+  } else if (tid < 2 * C) {
+    s.gam[tid - C] = gate;
+  } else if (tid < 3 * C) {
+    s.D[tid - 2 * C] = gate;
+  } else if (tid == 3 * C) {
+    s.gC = gate;
+  }
   store_step();
   __syncthreads();
   for (int e = tid; e < C * C; e += NTG) {
@@ -706,20 +879,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   }
   for (int vsi = 0; vsi < nvs; ++vsi) {
     const int v0 = vsi * VS;
-    if (vsi + 1 < nvs) load_step(vsi + 1);
-    seg_mfma<NPW>(accW, am0, an0, ana, r, kq,
-                  seg<VS>([&](int m, int kk) { return s.du[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
-    seg_mfma<NPW>(accQ, am0, an0, ana, r, kq,
-                  seg<VS>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.S[n][kk]; }));
-    seg_mfma<NPW>(accK, am0, an0, ana, r, kq,
-                  seg<VS>([&](int m, int kk) { return s.u[m][kk]; }, [&](int kk, int n) { return s.dS[n][kk]; }));
-    if (wave < 4)
-      seg_mfma<1>(accC, cm0, cn0, 1, r, kq,
-                  seg<VS>([&](int m, int kk) { return s.dO[m][kk]; }, [&](int kk, int n) { return s.u[n][kk]; }));
-    else
-      seg_mfma<1>(accC, cm0, cn0, 1, r, kq,
-                  seg<VS>([&](int m, int kk) { return s.du[m][kk]; },
-                          [&](int kk, int n) { return s.bt[n] * s.v[n][kk]; }));
+    // dU~ of the step and dv first: its stores go out before the next
+    // step's loads, so that waiting for those loads does not wait for them
     if (du_wave) {
       f32x4 a[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
       seg_mfma<1>(a, um0, un0, 1, r, kq,
@@ -727,9 +888,39 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = um0[0] + 4 * kq + i;
-        if (row < nval) stx<TIn>(p.dv, dvb + (int64_t)row * p.sdv[1] + v0 + r, s.bt[row] * a[0][i]);
-        vu_acc[i] = __builtin_fmaf(s.v[row][r], a[0][i], vu_acc[i]);
+        const int col = un0[0] + r;
+        if (row < nval) stx<TIn>(p.dv, dvb + (int64_t)row * p.sdv[1] + v0 + col, s.bt[row] * a[0][i]);
+        vu_acc[i] = __builtin_fmaf(s.v[row][col], a[0][i], vu_acc[i]);
       }
+    }
+    if (vsi + 1 < nvs) load_step(vsi + 1);
+    // Products contracted over the step's V columns, all of the form
+    // X[m][v] Y[n][v]: the contraction runs in 16-column groups in which
+    // lane (r, kq) covers columns 4 kq .. 4 kq + 3 over four MFMA steps, so
+    // each operand is one 16-byte read per four steps.
+#pragma unroll
+    for (int c0 = 0; c0 < VS; c0 += 16) {
+      const int cc = c0 + 4 * kq;
+#pragma unroll
+      for (int g = 0; g < NPW; ++g) {
+        if (g < ana) {
+          const f32x4 sb = ld4(s.S, an0[g] + r, cc), db = ld4(s.dS, an0[g] + r, cc);
+          const f32x4 xa = ld4(s.du, am0[g] + r, cc), xo = ld4(s.dO, am0[g] + r, cc);
+          const f32x4 xu = ld4(s.u, am0[g] + r, cc);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            accW[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], sb[j], accW[g], 0, 0, 0);
+            accQ[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo[j], sb[j], accQ[g], 0, 0, 0);
+            accK[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xu[j], db[j], accK[g], 0, 0, 0);
+          }
+        }
+      }
+      // dO u^T (waves 0-3) or du (diag(beta) V)^T (waves 4-7)
+      const f32x4 xc = wave < 4 ? ld4(s.dO, cm0[0] + r, cc) : ld4(s.du, cm0[0] + r, cc);
+      f32x4 yc = wave < 4 ? ld4(s.u, cn0[0] + r, cc) : ld4(s.v, cn0[0] + r, cc);
+      if (wave >= 4) yc *= s.bt[cn0[0] + r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) accC[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[j], yc[j], accC[0], 0, 0, 0);
     }
     for (int e = tid; e < K * VS; e += NTG) dgc_acc = __builtin_fmaf(s.S[e / VS][e % VS], s.dS[e / VS][e % VS], dgc_acc);
     __syncthreads();
@@ -774,7 +965,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float x = sum16(vu_acc[e]);
-      if (r == 0) s.vu[um0[0] + 4 * kq + e] = x;
+      if (r == 0) s.vu[un0[0] / 16][um0[0] + 4 * kq + e] = x;
     }
   }
   {
@@ -832,7 +1023,10 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     const float dd = row_sum<NTG, C>(tid, [&](int rr, int j) { return s.dD[j] * s.D[j]; });
     if (tid % RL == 0) {
       const int rr = tid / RL;
-      s.dbt[rr] = s.vu[rr] + s.gam[rr] * s.kw[rr] + am;
+      float vu = 0.f;
+#pragma unroll
+      for (int j = 0; j < VS / 16; ++j) vu += s.vu[j][rr];
+      s.dbt[rr] = vu + s.gam[rr] * s.kw[rr] + am;
       const float dgam = s.dgam[rr] + s.bt[rr] * s.kw[rr];
       // ... and through gam, D and (last row) gam_C and every D_j
       float d = mt + dgam * s.gam[rr] - s.dD[rr] * s.D[rr];
@@ -841,12 +1035,14 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     }
   }
   __syncthreads();
-  if (tid < nval) {
-    float acc = 0.f;
-    for (int j = tid; j < C; ++j) acc += s.db[j];
-    store_scalar(p.dg, head_base(rs, hi, p.sdg) + (int64_t)(t0 + tid) * p.sdg[1], p.g_dtype, acc);
-    store_scalar(p.dbeta, head_base(rs, hi, p.sdb) + (int64_t)(t0 + tid) * p.sdb[1], p.beta_dtype, s.dbt[tid]);
+  if (wave == 0) {
+    // dg_t = sum_{j >= t} db_j: lane l scans db[C - 1 - l]
+    const float x = scan32(lane < C ? s.db[C - 1 - lane] : 0.f);
+    const int t = C - 1 - lane;
+    if (lane < C && t < nval) store_scalar(p.dg, head_base(rs, hi, p.sdg) + (int64_t)(t0 + t) * p.sdg[1], p.g_dtype, x);
   }
+  if (tid < nval)
+    store_scalar(p.dbeta, head_base(rs, hi, p.sdb) + (int64_t)(t0 + tid) * p.sdb[1], p.beta_dtype, s.dbt[tid]);
   // dq = dQK K + scale diag(gam) dO S^T;
   // dk = dQK^T Q + diag(D) u dS'^T + diag(beta gam) dW~ + (dKK + dKK^T) K
   {
@@ -913,7 +1109,12 @@ template <typename TIn, int K>
 int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
   if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
   hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
-  if (nrec > 0) hipLaunchKernelGGL((grad_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
+  if (nrec > 0) {
+    if (a.V % 32 == 0)
+      hipLaunchKernelGGL((grad_kernel<TIn, K, 32>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
+    else
+      hipLaunchKernelGGL((grad_kernel<TIn, K, 16>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
+  }
   return (int)hipGetLastError();
 }
 
