@@ -178,7 +178,8 @@ int gdn_prep_launch(const GdnPrepParams* params, void* stream);
  *   - workspace: device memory of at least gdn_bwd_workspace_size(...)
  *     bytes, 256-byte aligned, owned by the caller; its contents need no
  *     initialisation and are undefined afterwards.
- *   - Enqueues two kernels on `stream`; no allocation, no synchronisation. */
+ *   - Enqueues three kernels on `stream` (per-chunk record, the two state
+ *     recurrences, per-chunk gradients); no allocation, no synchronisation. */
 typedef struct GdnBwdParams {
   const void* q;
   const void* k;

@@ -513,9 +513,9 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     Returns ``(dq, dk, dv, dg, dbeta, dh0)`` in the inputs' dtypes (``dh0``
     fp32, None unless ``need_dh0``).  K in {32, 64, 128}, V a multiple of 16;
     same strides, dtypes and ``cu_seqlens`` convention as the forward.  One
-    call enqueues the backward kernel and the slice reduction on the current
-    stream; the workspace (chunk-start states and per-slice partial sums) is
-    allocated here and released when the call returns.
+    call enqueues the backward's three kernels on the current stream; the
+    workspace (per-chunk records, chunk-start states and their gradients,
+    u and du) is allocated here and released when the call returns.
     """
     n_seq = None
     if cu_seqlens is not None:
