@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GDN_MI355X_ABI_VERSION 3
+#define GDN_MI355X_ABI_VERSION 4
 
 /* Element types of the tensors crossing the boundary. */
 enum GdnDtype {
@@ -107,12 +107,26 @@ typedef struct GdnFwdParams {
   int32_t flags;            /* GdnFlags; 0 = default */
   /* nullable: B + 1 int64 row offsets of packed sequences (device memory) */
   const int64_t* cu_seqlens;
+  /* device memory of at least gdn_fwd_workspace_size(params) bytes,
+   * 256-byte aligned, owned by the caller; nullable when that size is 0 */
+  void* workspace;
+  int64_t workspace_bytes;
 } GdnFwdParams;
 
-/* Enqueue one fused chunked GDN forward on `stream` (a hipStream_t; NULL =
- * the legacy default stream).  Returns a GdnStatus / hipError_t value.
- * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140). */
+/* Enqueue one chunked GDN forward on `stream` (a hipStream_t; NULL = the
+ * legacy default stream).  Returns a GdnStatus / hipError_t value.
+ * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140).
+ * C = 32 (and K = 256 or GDN_FLAG_PHASED_KERNEL) runs one fused kernel with
+ * no workspace.  C = 64 with K in {32, 64, 128} runs two launches (a
+ * per-chunk record, then the scan over chunks; block_v is 16 there) and
+ * needs params->workspace; the state stays on chip in both. */
 int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
+
+/* Bytes of workspace gdn_fwd_launch needs for these params (0 for the fused
+ * kernels; B = the number of sequences when cu_seqlens is set); -1 if the
+ * shape is invalid.  No counterpart in the reference, whose Triton launch
+ * needs none. */
+int64_t gdn_fwd_workspace_size(const GdnFwdParams* params);
 
 /* The block_v the launcher picks when params->block_v == 0 (for logging and
  * tests); -1 if the shape is unsupported.  No counterpart in the reference,

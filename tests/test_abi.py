@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_fwd_abi_version() == 3
+    assert lib.gdn_fwd_abi_version() == 4
 
 
 @pytest.mark.parametrize("struct", ["GdnFwdParams", "GdnPrepParams", "GdnBwdParams"])
@@ -93,6 +93,35 @@ def _params(L, **kw):
     for k_, v_ in kw.items():
         setattr(P, k_, v_)
     return P
+
+
+def test_fwd_workspace_size(lib, pkg):
+    """Fused kernels need no workspace; 64-row chunks with K <= 128 take one
+    fp32 record per (chunk slot, head): T and P (C x C), W (C x K), three
+    gate rows."""
+    L = pkg._lib
+    size = lambda **kw: lib.gdn_fwd_workspace_size(ctypes.byref(_params(L, **kw)))
+    assert size() == 0                                   # C = 32: pipelined, none
+    assert size(chunk_size=64, K=256) == 0               # phased kernel, none
+    assert size(chunk_size=64, flags=1) == 0             # phased forced, none
+    C, K, H = 64, 128, 16
+    rec = 4 * (2 * C * C + C * K + 3 * C)
+    want = 2 * (4096 // C) * H * rec
+    assert want <= size(chunk_size=64) < want + 256
+    # packed sequences: slots ceil(T / C) + N = 2 + 3
+    got = size(chunk_size=64, B=3, T=100, cu_seqlens=0x2000)
+    assert 5 * H * rec <= got < 5 * H * rec + 256
+    assert size(chunk_size=64, B=0) == -1
+    assert lib.gdn_fwd_workspace_size(None) == -1
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(chunk_size=64), 1006), (dict(chunk_size=64, workspace=0x1010, workspace_bytes=1 << 40), 1006),
+    (dict(chunk_size=64, workspace=0x1000, workspace_bytes=1024), 1006),
+])
+def test_fwd_c64_rejects_bad_workspace(lib, pkg, kw, code):
+    P = _params(pkg._lib, **kw)
+    assert lib.gdn_fwd_launch(ctypes.byref(P), None) == code
 
 
 @pytest.mark.parametrize("kw,code", [

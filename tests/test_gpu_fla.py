@@ -36,24 +36,26 @@ def _packed_inputs(lens, H, K, V, dtype, seed):
     return q, k, v, g, beta, h0, cu
 
 
-@pytest.mark.parametrize("kernel", ["auto", "phased"])
+@pytest.mark.parametrize("kernel,C", [("auto", 32), ("phased", 32), ("auto", 64)])
 @pytest.mark.parametrize("dtype,K,V,bv", [(torch.float16, 64, 64, 16), (torch.bfloat16, 128, 32, 32),
                                           (torch.float16, 32, 48, 16)])
-def test_varlen_equals_separate_runs(pkg, cuda, kernel, dtype, K, V, bv):
-    lens = [37, 0, 1, 32, 100, 64, 5]
+def test_varlen_equals_separate_runs(pkg, cuda, kernel, C, dtype, K, V, bv):
+    """C=64 'auto' is the two-launch path (record + scan)."""
+    lens = [37, 0, 1, 32, 100, 64, 5, 129]
     H = 2
     q, k, v, g, beta, h0, cu = _packed_inputs(lens, H, K, V, dtype, seed=21)
     d = lambda t: t.to(cuda)
-    print(f"[varlen] {dtype} K={K} V={V} bv={bv} kernel={kernel} lens={lens}", flush=True)
+    print(f"[varlen] {dtype} K={K} V={V} bv={bv} kernel={kernel} C={C} lens={lens}", flush=True)
     o, fs = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), scale=0.5, block_v=bv,
-                        kernel=kernel, cu_seqlens=d(cu))
+                        kernel=kernel, cu_seqlens=d(cu), chunk_size=C)
     torch.cuda.synchronize()
     o, fs = o.cpu(), fs.cpu()
     assert o.shape == (1, sum(lens), H, V) and fs.shape == (len(lens), H, K, V)
     for i, (a, b) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
         sl = lambda t: t[:, a:b].contiguous()
         oi, fi = pkg.gdn_fwd(d(sl(q)), d(sl(k)), d(sl(v)), d(sl(g)), d(sl(beta)),
-                             d(h0[i:i + 1].contiguous()), scale=0.5, block_v=bv, kernel=kernel)
+                             d(h0[i:i + 1].contiguous()), scale=0.5, block_v=bv, kernel=kernel,
+                             chunk_size=C)
         torch.cuda.synchronize()
         assert torch.equal(o[:, a:b], oi.cpu()), f"sequence {i}: o differs from a separate run"
         assert torch.equal(fs[i:i + 1], fi.cpu()), f"sequence {i}: state differs"

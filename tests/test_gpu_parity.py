@@ -199,3 +199,45 @@ def test_t_zero_returns_h0(pkg, cuda):
                  torch.zeros(1, 0, 2), torch.zeros(1, 0, 2), h0)
     assert o.shape == (1, 0, 2, 32)
     assert torch.equal(fs, h0)
+
+
+# --------------------------------------------------------------------------
+# 64-row chunks: the two-launch path (per-chunk record, then the scan)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("K,V,T", [(32, 48, 200), (64, 64, 129), (128, 48, 64), (128, 128, 333)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_c64_two_launch(pkg, cuda, dtype, K, V, T):
+    """C=64 with K <= 128 runs the record + scan launches (workspace from
+    gdn_fwd_workspace_size).  fp32: <= 1e-5 against the fp32 chunked UT path
+    with C=64 (inputs padded to whole chunks); fp16 / bf16: <= 1e-3 against
+    the step recurrence.  h0 non-zero, T with a partial last chunk."""
+    q, k, v, beta, g = ref.make_inputs_reference(2, T, 3, K, V, seed=21, gate_scale=0.2, dtype=dtype)
+    h0 = 0.1 * torch.randn(2, 3, K, V, generator=torch.Generator().manual_seed(4))
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, chunk_size=64, scale=0.7,
+                 output_dtype=torch.float32)
+    if dtype == torch.float32:
+        qp, kp, vp, bp, gp = ref.pad_to_multiple(q, k, v, beta, g, 64)
+        o_ref, h_ref = ref.chunked_ut(qp, kp, vp, bp, gp, C=64, initial_state=ref.to_vk(h0))
+        o_ref, h_ref, tol = 0.7 * o_ref[:, :T], ref.to_kv(h_ref), TOL_F32
+    else:
+        o_ref, h_ref = _recurrent(q, k, v, g, beta, h0, scale=0.7)
+        tol = TOL_LOWP
+    eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
+    _report(f"c64 {dtype} K={K} V={V} T={T}", eo, eh)
+    assert eo <= tol and eh <= tol
+
+
+def test_c64_degenerate_and_agrees_with_phased(pkg, cuda):
+    """g = 0, beta = 1 (plain DeltaNet, the hardest substitution) at C=64;
+    the two-launch path and the phased kernel agree to rounding."""
+    q, k, v, g, beta, h0 = ref.make_inputs_baseline(2, 512, 4, 128, 128, seed=3, dtype=torch.bfloat16,
+                                                    with_h0=True, degenerate=True)
+    o, fs = _run(pkg, cuda, q, k, v, g, beta, h0, chunk_size=64, output_dtype=torch.float32)
+    o2, fs2 = _run(pkg, cuda, q, k, v, g, beta, h0, chunk_size=64, output_dtype=torch.float32,
+                   kernel="phased")
+    o_ref, h_ref = _recurrent(q, k, v, g, beta, h0)
+    eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
+    _report("c64 degenerate bf16", eo, eh)
+    assert eo <= TOL_LOWP and eh <= TOL_LOWP
+    assert ref.rel_err(o2, o) <= TOL_LOWP and ref.rel_err(fs2, fs) <= TOL_LOWP

@@ -9,7 +9,7 @@ import threading
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libgdn_mi355x.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enum GdnDtype
 DTYPE_F32 = 0
@@ -31,6 +31,7 @@ FLAG_PHASED_KERNEL = 1
 # Every symbol the header declares; tests check the library exports them.
 EXPORTED_SYMBOLS = (
     "gdn_fwd_launch",
+    "gdn_fwd_workspace_size",
     "gdn_fwd_auto_block_v",
     "gdn_fwd_status_string",
     "gdn_fwd_abi_version",
@@ -77,6 +78,8 @@ class GdnFwdParams(ctypes.Structure):
         ("o_dtype", ctypes.c_int32),
         ("flags", ctypes.c_int32),
         ("cu_seqlens", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -150,6 +153,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         lib = ctypes.CDLL(path)
         lib.gdn_fwd_launch.argtypes = [ctypes.POINTER(GdnFwdParams), ctypes.c_void_p]
         lib.gdn_fwd_launch.restype = ctypes.c_int
+        lib.gdn_fwd_workspace_size.argtypes = [ctypes.POINTER(GdnFwdParams)]
+        lib.gdn_fwd_workspace_size.restype = ctypes.c_int64
         lib.gdn_fwd_auto_block_v.argtypes = [ctypes.c_int] * 6
         lib.gdn_fwd_auto_block_v.restype = ctypes.c_int
         lib.gdn_fwd_status_string.argtypes = [ctypes.c_int]

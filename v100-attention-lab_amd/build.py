@@ -19,7 +19,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 # One translation unit per q/k/v dtype, the host API, the input
 # preparation and the backward, compiled in parallel.
 SOURCES = ["gdn_fwd_api.hip", "gdn_fwd_f16.hip", "gdn_fwd_bf16.hip", "gdn_fwd_f32.hip",
-           "gdn_prep.hip", "gdn_bwd.hip"]
+           "gdn_fwd_c64.hip", "gdn_prep.hip", "gdn_bwd.hip"]
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")

@@ -64,9 +64,23 @@ const char* gdn_fwd_status_string(int status) {
       return "gdn_fwd: q/k/v rows must be 16-byte aligned with a contiguous last dimension";
     case GDN_ERR_BAD_DTYPE: return "gdn_fwd: unknown dtype code";
     case GDN_ERR_WORKSPACE:
-      return "gdn_fwd: workspace missing, misaligned or smaller than gdn_bwd_workspace_size()";
+      return "gdn: workspace missing, misaligned or smaller than gdn_fwd_workspace_size() / "
+             "gdn_bwd_workspace_size()";
     default: return hipGetErrorString((hipError_t)status);
   }
+}
+
+// The two-launch path for 64-row chunks, unless the phased kernel is asked for.
+static bool uses_c64(const GdnFwdParams& P) {
+  return !(P.flags & GDN_FLAG_PHASED_KERNEL) && c64_supported(P.K, P.chunk_size, P.V);
+}
+
+int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
+  if (prm == nullptr) return -1;
+  const GdnFwdParams& P = *prm;
+  if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0) return -1;
+  if (!uses_c64(P)) return 0;
+  return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0);
 }
 
 int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
@@ -81,9 +95,10 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   if (P.T > 0 && (P.q == nullptr || P.k == nullptr || P.v == nullptr || P.g == nullptr ||
                   P.beta == nullptr || P.o == nullptr))
     return GDN_ERR_NULL_POINTER;
-  int bv = P.block_v;
+  const bool c64 = uses_c64(P);
+  int bv = c64 ? 16 : P.block_v;
   if (bv == 0) bv = auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
-  if (bv <= 0 || P.V % bv != 0 || !supported(P.qkv_dtype, P.K, P.chunk_size, bv))
+  if (!c64 && (bv <= 0 || P.V % bv != 0 || !supported(P.qkv_dtype, P.K, P.chunk_size, bv)))
     return GDN_ERR_UNSUPPORTED;
   // 16-byte rows for the vector loads of q, k, v.
   const int eb = elem_bytes(P.qkv_dtype);
@@ -98,6 +113,13 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   }
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
+  if (c64) {
+    const int64_t need = c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0);
+    if (P.T > 0 && (P.workspace == nullptr || reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 ||
+                    P.workspace_bytes < need))
+      return GDN_ERR_WORKSPACE;
+    return c64_launch(P, static_cast<hipStream_t>(stream));
+  }
 
   KArgs a = {};
   a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;

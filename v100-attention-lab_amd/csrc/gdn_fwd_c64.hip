@@ -1,0 +1,377 @@
+// The forward for 64-row chunks, as two launches (fp16, bf16 and fp32
+// inputs; K in {32, 64, 128}; fp32 arithmetic on v_mfma_f32_16x16x4_f32).
+//
+// Per chunk (C = 64 rows, b = in-chunk cumsum of g, gam = e^b, D_j =
+// e^{bC - b_j}, M[t][j] = e^{b_t - b_j} for j <= t), as in gdn_ref.py:48-99:
+//   A = tril_-1(beta_t M K K^T),  T = (I + A)^-1,  W = T diag(beta gam) K,
+//   u = T diag(beta) V - W S,
+//   o = scale (P u + diag(gam) Q S),  P = M o (Q K^T),
+//   S' = gam_C S + K^T diag(D) u.
+// Only u, o and S' involve the carried state S.  With 64-row chunks the
+// state-independent half (the K K^T and Q K^T products, the 64 x 64
+// substitution, W) is the larger one, and it runs first, for every chunk at
+// once:
+//   1. prep_kernel, one workgroup per (chunk, head): gates, T (two 32 x 32
+//      diagonal solves, one lane per column, then the off-diagonal block
+//      T21 = -T22 A21 T11 on the matrix cores), W and P, written to a
+//      per-chunk record in the caller's workspace;
+//   2. scan_kernel, one workgroup per (sequence, head, 16-column V slice):
+//      walks the chunks with S resident in LDS (O(B H K V) state: no chunk
+//      state is written), loading the next chunk's record and rows while the
+//      current one computes.  Wave w owns rows 16 w .. 16 w + 15 of u and o
+//      (u and Q S in one pass over the contraction) and rows 32 w .. of the
+//      state update.
+// Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
+// onwards, as in the backward.
+
+#include "gdn_tiles_f32.h"
+
+namespace gdn {
+namespace c64 {
+
+using namespace tiles;
+
+constexpr int C = 64;
+constexpr int BV = 16;
+constexpr int NT = 256;  // threads of both kernels (4 waves)
+
+struct FArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;
+  void* o;
+  float* fs;
+  float* rec;
+  int64_t sq[3], sk[3], sv[3], sg[3], sb[3], so[3];
+  int64_t sh0[4], sfs[4];
+  int B, T, H, V, nv, nchmax, units;
+  float scale;
+  int g_dtype, beta_dtype, o_dtype;
+  const int64_t* cu;
+  int xcd_remap;
+};
+
+// Per-(slot, head) record, in floats: T and P as [C][C], W as [C][K], then
+// gam and D as [C] each and gam_C (first of a [C] row).
+template <int K>
+struct Rec {
+  static constexpr int T = 0, PM = C * C, W = 2 * C * C;
+  static constexpr int G = W + C * K;
+  static constexpr int SIZE = G + 3 * C;
+};
+inline int64_t rec_size(int K) { return 2 * C * C + (int64_t)C * K + 3 * C; }
+
+// ---------------------------------------------------------------------------
+// 1. prep
+// ---------------------------------------------------------------------------
+
+template <int K>
+struct alignas(16) PSmem {
+  float q[C][K + 1], k[C][K + 1];
+  float a[C][C + 1];   // K K^T, then A
+  float qk[C][C + 1];  // Q K^T, then A21 T11
+  float t[C][C + 1];
+  float gl[C], bt[C], b[C], gam[C], D[C];
+  float gC;
+};
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
+  using R = Rec<K>;
+  __shared__ PSmem<K> s;
+  const int tid = threadIdx.x;
+  const int64_t slot = blockIdx.x / p.H;
+  const int hi = blockIdx.x % p.H;
+  RowSpan rs;
+  int c;
+  if (!slot_chunk<C>(p, slot, rs, c)) return;
+  const int t0 = c * C, nval = min(C, rs.T - t0);
+  float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
+
+  {
+    RowLoad<TIn, C, K, NT> lq, lk;
+    lq.load(tid, static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq) + t0 * p.sq[1], p.sq[1], nval);
+    lk.load(tid, static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + t0 * p.sk[1], p.sk[1], nval);
+    float gv = 0.f, bv = 0.f;
+    if (tid < nval) {
+      gv = load_scalar(p.g, head_base(rs, hi, p.sg) + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
+      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
+    }
+    lq.store(tid, s.q);
+    lk.store(tid, s.k);
+    if (tid < C) {
+      s.gl[tid] = gv;
+      s.bt[tid] = bv;
+    }
+  }
+  __syncthreads();
+  if (tid < C) {
+    // sequential cumsum in each lane (the association order of a plain
+    // running sum)
+    float bt = 0.f, bc = 0.f;
+    for (int j = 0; j < C; ++j) {
+      bc += s.gl[j];
+      if (j == tid) bt = bc;
+    }
+    s.b[tid] = bt;
+    s.gam[tid] = expf(bt);
+    s.D[tid] = expf(bc - bt);
+    if (tid == C - 1) s.gC = expf(bc);
+  }
+  mmx<NT, C, C>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
+                seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  mmx<NT, C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  __syncthreads();
+  for (int e = tid; e < C * C; e += NT) {
+    const int t = e / C, j = e % C;
+    const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
+    rec[R::PM + e] = mv * s.qk[t][j];
+    s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
+  }
+  if (tid < C) {
+    rec[R::G + tid] = s.gam[tid];
+    rec[R::G + C + tid] = s.D[tid];
+    rec[R::G + 2 * C + tid] = tid == 0 ? s.gC : 0.f;
+  }
+  __syncthreads();
+  // T11 = (I + A11)^-1 (lanes 0-31 of wave 0) and T22 = (I + A22)^-1 (lanes
+  // 0-31 of wave 1): one column per lane, the column in registers
+  if ((tid & 63) < 32 && tid < 128) {
+    const int o = tid < 64 ? 0 : 32, cc = tid & 31;
+    float col[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      float x = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) x = __builtin_fmaf(-s.a[o + i][o + j], col[j], x);
+      col[i] = x;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      s.t[o + i][o + cc] = col[i];
+      s.t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21 overwritten below)
+    }
+  }
+  __syncthreads();
+  // X = A21 T11 -> qk
+  mmx<NT, 32, 32>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                  seg<32>([&](int m, int kk) { return s.a[32 + m][kk]; }, [&](int kk, int n) { return s.t[kk][n]; }));
+  __syncthreads();
+  // T21 = -T22 X
+  mmx<NT, 32, 32>(tid, [&](int m, int n, float x) { s.t[32 + m][n] = -x; },
+                  seg<32>([&](int m, int kk) { return s.t[32 + m][32 + kk]; },
+                          [&](int kk, int n) { return s.qk[kk][n]; }));
+  __syncthreads();
+  for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
+  // W = T diag(beta gam) K
+  mmx<NT, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
+                seg<C>([&](int m, int kk) { return s.t[m][kk]; },
+                       [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
+}
+
+// ---------------------------------------------------------------------------
+// 2. scan
+// ---------------------------------------------------------------------------
+
+template <int K>
+struct alignas(16) SSmem {
+  float S[K][BV + 1];
+  float t[C][C + 1], pm[C][C + 1];
+  float w[C][K + 1], q[C][K + 1], k[C][K + 1];
+  float v[C][BV + 1], u[C][BV + 1];
+  float bt[C], gam[C], D[C];
+  float gC;
+};
+
+// Next chunk's record and rows, in registers.  Scalars are kept as raw bits
+// and converted when stored: a conversion right after the load would make
+// the wave wait for every load issued before it.
+template <typename TIn, int K>
+struct Next {
+  using R = Rec<K>;
+  RowLoad<float, C, C, NT> lt, lp;
+  RowLoad<float, C, K, NT> lw;
+  RowLoad<TIn, C, K, NT> lq, lk;
+  RowLoad<TIn, C, BV, NT> lv;
+  uint32_t bv;
+  float gm, dv, gc;
+  __device__ __forceinline__ void load(const FArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
+                                       const TIn* vg, int64_t bb, int t0, int nval) {
+    const float* const rec = p.rec + ri * R::SIZE;
+    lt.load(tid, rec + R::T, C, C);
+    lp.load(tid, rec + R::PM, C, C);
+    lw.load(tid, rec + R::W, K, C);
+    lq.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
+    lk.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    lv.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
+    bv = tid < nval ? load_bits(p.beta, bb + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0u;
+    gm = tid < C ? rec[R::G + tid] : 0.f;
+    dv = tid < C ? rec[R::G + C + tid] : 0.f;
+    gc = tid == 0 ? rec[R::G + 2 * C] : 0.f;
+  }
+  __device__ __forceinline__ void store(SSmem<K>& s, int tid, int beta_dtype) const {
+    lt.store(tid, s.t);
+    lp.store(tid, s.pm);
+    lw.store(tid, s.w);
+    lq.store(tid, s.q);
+    lk.store(tid, s.k);
+    lv.store(tid, s.v);
+    if (tid < C) {
+      s.bt[tid] = bits_to_float(bv, beta_dtype);
+      s.gam[tid] = gm;
+      s.D[tid] = dv;
+    }
+    if (tid == 0) s.gC = gc;
+  }
+};
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
+  __shared__ SSmem<K> s;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  int unit = blockIdx.x;
+  if (p.xcd_remap) unit = (blockIdx.x & 7) * (p.units >> 3) + (blockIdx.x >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const int v0 = vs * BV;
+  const RowSpan rs = row_span(p.cu, p.T, bi);
+  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
+  const int nch = (rs.T + C - 1) / C;
+  const float scale = p.scale;
+  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  const int64_t bb = head_base(rs, hi, p.sb);
+  const int64_t ob = head_base(rs, hi, p.so) + v0;
+
+  for (int e = tid; e < K * BV; e += NT) {
+    const int kk = e / BV, c2 = e % BV;
+    s.S[kk][c2] = p.h0 ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]] : 0.f;
+  }
+  Next<TIn, K> nx;
+  if (nch > 0) {
+    nx.load(p, tid, slot0 * p.H + hi, qg, kg, vg, bb, 0, min(C, rs.T));
+    nx.store(s, tid, p.beta_dtype);
+  }
+  __syncthreads();
+  const int um0 = 16 * wave;  // this wave's rows of u and o
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * C, nval = min(C, rs.T - t0);
+    if (c + 1 < nch)
+      nx.load(p, tid, (slot0 + c + 1) * p.H + hi, qg, kg, vg, bb, t0 + C, min(C, rs.T - t0 - C));
+    // u = T diag(beta) V - W S and Q S for rows um0 .. um0 + 15; the state
+    // operand is read once for both
+    f32x4 au = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k0 = 0; k0 < C; k0 += 4) {
+      au = __builtin_amdgcn_mfma_f32_16x16x4f32(s.t[um0 + r][k0 + kq], s.bt[k0 + kq] * s.v[k0 + kq][r], au, 0,
+                                                0, 0);
+    }
+#pragma unroll 4
+    for (int k0 = 0; k0 < K; k0 += 4) {
+      const float sb = s.S[k0 + kq][r];
+      au = __builtin_amdgcn_mfma_f32_16x16x4f32(-s.w[um0 + r][k0 + kq], sb, au, 0, 0, 0);
+      aq = __builtin_amdgcn_mfma_f32_16x16x4f32(s.q[um0 + r][k0 + kq], sb, aq, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.u[um0 + 4 * kq + i][r] = au[i];
+    __syncthreads();
+    // o = scale (P u + diag(gam) Q S) for rows um0 .. um0 + 15
+    {
+      f32x4 ao = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int k0 = 0; k0 < C; k0 += 4)
+        ao = __builtin_amdgcn_mfma_f32_16x16x4f32(s.pm[um0 + r][k0 + kq], s.u[k0 + kq][r], ao, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = um0 + 4 * kq + i;
+        if (row < nval)
+          store_scalar(p.o, ob + (int64_t)(t0 + row) * p.so[1] + r, p.o_dtype,
+                       scale * (ao[i] + s.gam[row] * aq[i]));
+      }
+    }
+    // S <- gam_C S + K^T diag(D) u
+    mmx<NT, K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
+                   seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
+                          [&](int kk, int n) { return s.u[kk][n]; }));
+    __syncthreads();
+    if (c + 1 < nch) {
+      nx.store(s, tid, p.beta_dtype);
+      __syncthreads();
+    }
+  }
+  for (int e = tid; e < K * BV; e += NT) {
+    const int kk = e / BV, c2 = e % BV;
+    p.fs[bi * p.sfs[0] + hi * p.sfs[1] + kk * p.sfs[2] + (v0 + c2) * p.sfs[3]] = s.S[kk][c2];
+  }
+}
+
+template <typename TIn, int K>
+int launch_k(const FArgs& a, int64_t nrec, hipStream_t s) {
+  if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((scan_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn>
+int launch_t(const FArgs& a, int K, int64_t nrec, hipStream_t s) {
+  switch (K) {
+    case 32: return launch_k<TIn, 32>(a, nrec, s);
+    case 64: return launch_k<TIn, 64>(a, nrec, s);
+    case 128: return launch_k<TIn, 128>(a, nrec, s);
+    default: return GDN_ERR_UNSUPPORTED;
+  }
+}
+
+inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+}  // namespace c64
+
+// Chunk slots x heads x record size, in bytes.
+int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq) {
+  const int64_t nch = (T + c64::C - 1) / c64::C;
+  const int64_t nslot = n_seq > 0 ? nch + n_seq : (int64_t)B * nch;
+  return c64::align256(nslot * H * c64::rec_size(K) * 4);
+}
+
+bool c64_supported(int K, int C, int V) { return C == c64::C && (K == 32 || K == 64 || K == 128) && V % 16 == 0; }
+
+// Enqueue the two launches (arguments checked by the caller).
+int c64_launch(const GdnFwdParams& P, hipStream_t stream) {
+  const int n_seq = P.cu_seqlens ? P.B : 0;
+  c64::FArgs a = {};
+  a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
+  a.o = P.o; a.fs = P.final_state;
+  a.rec = static_cast<float*>(P.workspace);
+  for (int d = 0; d < 3; ++d) {
+    a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
+    a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.so[d] = P.o_stride[d];
+  }
+  for (int d = 0; d < 4; ++d) { a.sh0[d] = P.h0_stride[d]; a.sfs[d] = P.fs_stride[d]; }
+  a.B = P.B; a.T = P.T; a.H = P.H; a.V = P.V; a.nv = P.V / c64::BV;
+  a.nchmax = (P.T + c64::C - 1) / c64::C;
+  const int64_t units = (int64_t)P.B * P.H * a.nv;
+  a.units = (int)units;
+  a.scale = P.scale;
+  a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.o_dtype = P.o_dtype;
+  a.cu = P.cu_seqlens;
+  a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+  const int64_t nslot = n_seq > 0 ? a.nchmax + n_seq : (int64_t)P.B * a.nchmax;
+  const int64_t nrec = P.T > 0 ? nslot * P.H : 0;
+  if (nrec > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
+  switch (P.qkv_dtype) {
+    case GDN_DTYPE_F16: return c64::launch_t<f16>(a, P.K, nrec, stream);
+    case GDN_DTYPE_BF16: return c64::launch_t<bf16_t>(a, P.K, nrec, stream);
+    default: return c64::launch_t<float>(a, P.K, nrec, stream);
+  }
+}
+
+}  // namespace gdn

@@ -771,5 +771,10 @@ inline bool pipe_supported(int dtype, int K, int C, int BV) {
 }
 int launch_pipe_f16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
 int launch_pipe_bf16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
+// 64-row chunks with K in {32, 64, 128} run as two launches (gdn_fwd_c64.hip)
+// over a caller-owned workspace of per-chunk records.
+bool c64_supported(int K, int C, int V);
+int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq);
+int c64_launch(const GdnFwdParams& P, hipStream_t stream);
 
 }  // namespace gdn

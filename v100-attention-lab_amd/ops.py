@@ -122,7 +122,7 @@ _PLANS_MAX = 256
 
 
 class _Plan:
-    __slots__ = ("shape_o", "shape_fs", "out_dtype", "fs_vk", "o_hf", "params")
+    __slots__ = ("shape_o", "shape_fs", "out_dtype", "fs_vk", "o_hf", "params", "ws_bytes")
 
 
 def _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
@@ -173,6 +173,14 @@ def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, k
     P.beta_dtype = _DTYPE_CODE[beta.dtype]
     P.o_dtype = _DTYPE_CODE[out_dtype]
     P.flags = _KERNELS[kernel]
+    # workspace bytes for these shapes (only whether cu_seqlens is set
+    # matters to the size, not where it points)
+    P.cu_seqlens = 1 if n_seq is not None else None
+    ws = _lib.load_library().gdn_fwd_workspace_size(ctypes.byref(P))
+    P.cu_seqlens = None
+    if ws < 0:
+        raise ValueError(f"unsupported forward shape B={B} T={T} H={H} K={K} V={V}")
+    plan.ws_bytes = int(ws)
     plan.params = bytes(P)
     return plan
 
@@ -228,6 +236,10 @@ def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
     P.h0 = h0.data_ptr() if h0 is not None else None
     P.o, P.final_state = o.data_ptr(), fs.data_ptr()
     P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
+    ws = None   # released when this call returns: later work on the stream is ordered after it
+    if plan.ws_bytes > 0:
+        ws = torch.empty(plan.ws_bytes, dtype=torch.uint8, device=dev)
+        P.workspace, P.workspace_bytes = ws.data_ptr(), plan.ws_bytes
     lib = _lib.load_library()
     if dev.index == torch.cuda.current_device():
         status = lib.gdn_fwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
