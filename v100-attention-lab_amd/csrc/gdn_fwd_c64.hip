@@ -18,9 +18,8 @@
 //   2. scan_kernel, one workgroup per (sequence, head, 16-column V slice):
 //      walks the chunks with S resident in LDS (O(B H K V) state: no chunk
 //      state is written), loading the next chunk's record and rows while the
-//      current one computes.  Wave w owns rows 16 w .. 16 w + 15 of u and o
-//      (u and Q S in one pass over the contraction) and rows 32 w .. of the
-//      state update.
+//      current one computes.  Waves 0-3 compute u (16 rows each), then the
+//      state update; waves 4-7 compute Q S for the same rows, then o.
 // Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
 // onwards, as in the backward.
 
@@ -33,7 +32,11 @@ using namespace tiles;
 
 constexpr int C = 64;
 constexpr int BV = 16;
-constexpr int NT = 256;  // threads of both kernels (4 waves)
+constexpr int NT = 512;   // threads of both kernels (8 waves)
+constexpr int UNR = 8;    // contraction steps unrolled in the products
+// LDS rows padded to a multiple of 4 floats: 16-byte stores when staging,
+// at most 2-way bank conflicts on the operand reads
+constexpr int PAD = 4;
 
 struct FArgs {
   const void* q;
@@ -70,10 +73,10 @@ inline int64_t rec_size(int K) { return 2 * C * C + (int64_t)C * K + 3 * C; }
 
 template <int K>
 struct alignas(16) PSmem {
-  float q[C][K + 1], k[C][K + 1];
-  float a[C][C + 1];   // K K^T, then A
-  float qk[C][C + 1];  // Q K^T, then A21 T11
-  float t[C][C + 1];
+  float q[C][K + PAD], k[C][K + PAD];
+  float a[C][C + PAD];   // K K^T, then A
+  float qk[C][C + PAD];  // Q K^T, then A21 T11
+  float t[C][C + PAD];
   float gl[C], bt[C], b[C], gam[C], D[C];
   float gC;
 };
@@ -121,10 +124,34 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
     s.D[tid] = expf(bc - bt);
     if (tid == C - 1) s.gC = expf(bc);
   }
-  mmx<NT, C, C>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
-                seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-  mmx<NT, C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
-                seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  if constexpr (std::is_same<TIn, float>::value) {
+    mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
+                       seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+    mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                       seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  } else {
+    // 16-bit inputs are exact in fp16 (bf16 values within the fp16 range,
+    // as in the fused kernels): K K^T and Q K^T on v_mfma_f32_16x16x32_f16,
+    // exact products with fp32 accumulation.  Lane (r, kq) supplies 8
+    // consecutive k of row r; 2 x 16 tiles over the 8 waves.
+    const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
+    auto frag8 = [&](const float* row) {
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(row), hi = *reinterpret_cast<const f32x4*>(row + 4);
+      return f16x8{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3], (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
+    };
+    for (int job = tid >> 6; job < 2 * (C / 16) * (C / 16); job += NT / 64) {
+      const int mat = job / ((C / 16) * (C / 16)), mt = (job / (C / 16)) % (C / 16), nt = job % (C / 16);
+      const float* arow = (mat ? &s.q[0][0] : &s.k[0][0]) + (16 * mt + r) * (K + PAD) + 8 * kq;
+      const float* brow = &s.k[0][0] + (16 * nt + r) * (K + PAD) + 8 * kq;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K / 32; ++kb)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(arow + 32 * kb), frag8(brow + 32 * kb), acc, 0, 0, 0);
+      float(*dst)[C + PAD] = mat ? s.qk : s.a;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[16 * mt + 4 * kq + i][16 * nt + r] = acc[i];
+    }
+  }
   __syncthreads();
   for (int e = tid; e < C * C; e += NT) {
     const int t = e / C, j = e % C;
@@ -158,17 +185,17 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
   }
   __syncthreads();
   // X = A21 T11 -> qk
-  mmx<NT, 32, 32>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
                   seg<32>([&](int m, int kk) { return s.a[32 + m][kk]; }, [&](int kk, int n) { return s.t[kk][n]; }));
   __syncthreads();
   // T21 = -T22 X
-  mmx<NT, 32, 32>(tid, [&](int m, int n, float x) { s.t[32 + m][n] = -x; },
+  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float x) { s.t[32 + m][n] = -x; },
                   seg<32>([&](int m, int kk) { return s.t[32 + m][32 + kk]; },
                           [&](int kk, int n) { return s.qk[kk][n]; }));
   __syncthreads();
   for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
   // W = T diag(beta gam) K
-  mmx<NT, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
+  mmx<NT, C, K, UNR>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
                 seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                        [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
 }
@@ -180,9 +207,9 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
 template <int K>
 struct alignas(16) SSmem {
   float S[K][BV + 1];
-  float t[C][C + 1], pm[C][C + 1];
-  float w[C][K + 1], q[C][K + 1], k[C][K + 1];
-  float v[C][BV + 1], u[C][BV + 1];
+  float t[C][C + PAD], pm[C][C + PAD];
+  float w[C][K + PAD], q[C][K + PAD], k[C][K + PAD];
+  float v[C][BV + PAD], u[C][BV + 1];
   float bt[C], gam[C], D[C];
   float gC;
 };
@@ -262,32 +289,60 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
     nx.store(s, tid, p.beta_dtype);
   }
   __syncthreads();
-  const int um0 = 16 * wave;  // this wave's rows of u and o
+  // waves 0-3: u rows 16 w .., then the state update; waves 4-7: Q S rows
+  // 16 (w - 4) .., then o of those rows
+  const int um0 = 16 * (wave & 3);
+  constexpr int NST = (K / 16 + 3) / 4;  // state tiles per wave: rows 16 (w + 4 j)
   for (int c = 0; c < nch; ++c) {
     const int t0 = c * C, nval = min(C, rs.T - t0);
     if (c + 1 < nch)
       nx.load(p, tid, (slot0 + c + 1) * p.H + hi, qg, kg, vg, bb, t0 + C, min(C, rs.T - t0 - C));
-    // u = T diag(beta) V - W S and Q S for rows um0 .. um0 + 15; the state
-    // operand is read once for both
-    f32x4 au = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int k0 = 0; k0 < C; k0 += 4) {
-      au = __builtin_amdgcn_mfma_f32_16x16x4f32(s.t[um0 + r][k0 + kq], s.bt[k0 + kq] * s.v[k0 + kq][r], au, 0,
-                                                0, 0);
-    }
-#pragma unroll 4
-    for (int k0 = 0; k0 < K; k0 += 4) {
-      const float sb = s.S[k0 + kq][r];
-      au = __builtin_amdgcn_mfma_f32_16x16x4f32(-s.w[um0 + r][k0 + kq], sb, au, 0, 0, 0);
-      aq = __builtin_amdgcn_mfma_f32_16x16x4f32(s.q[um0 + r][k0 + kq], sb, aq, 0, 0, 0);
-    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (wave < 4) {
+      // u = T diag(beta) V - W S
+#pragma unroll UNR
+      for (int k0 = 0; k0 < C; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.t[um0 + r][k0 + kq], s.bt[k0 + kq] * s.v[k0 + kq][r], acc,
+                                                   0, 0, 0);
+#pragma unroll UNR
+      for (int k0 = 0; k0 < K; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-s.w[um0 + r][k0 + kq], s.S[k0 + kq][r], acc, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s.u[um0 + 4 * kq + i][r] = au[i];
+      for (int i = 0; i < 4; ++i) s.u[um0 + 4 * kq + i][r] = acc[i];
+    } else {
+      // Q S, kept for o
+#pragma unroll UNR
+      for (int k0 = 0; k0 < K; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.q[um0 + r][k0 + kq], s.S[k0 + kq][r], acc, 0, 0, 0);
+    }
     __syncthreads();
-    // o = scale (P u + diag(gam) Q S) for rows um0 .. um0 + 15
-    {
+    if (wave < 4) {
+      // S <- gam_C S + K^T diag(D) u
+      f32x4 as[NST];
+#pragma unroll
+      for (int j = 0; j < NST; ++j) as[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll UNR
+      for (int k0 = 0; k0 < C; k0 += 4) {
+        const float ub = s.u[k0 + kq][r], d = s.D[k0 + kq];
+#pragma unroll
+        for (int j = 0; j < NST; ++j)
+          if (wave + 4 * j < K / 16)
+            as[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(s.k[k0 + kq][16 * (wave + 4 * j) + r] * d, ub, as[j],
+                                                         0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < NST; ++j)
+        if (wave + 4 * j < K / 16) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 16 * (wave + 4 * j) + 4 * kq + i;
+            s.S[m][r] = s.gC * s.S[m][r] + as[j][i];
+          }
+        }
+    } else {
+      // o = scale (P u + diag(gam) Q S)
       f32x4 ao = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
+#pragma unroll UNR
       for (int k0 = 0; k0 < C; k0 += 4)
         ao = __builtin_amdgcn_mfma_f32_16x16x4f32(s.pm[um0 + r][k0 + kq], s.u[k0 + kq][r], ao, 0, 0, 0);
 #pragma unroll
@@ -295,13 +350,9 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
         const int row = um0 + 4 * kq + i;
         if (row < nval)
           store_scalar(p.o, ob + (int64_t)(t0 + row) * p.so[1] + r, p.o_dtype,
-                       scale * (ao[i] + s.gam[row] * aq[i]));
+                       scale * (ao[i] + s.gam[row] * acc[i]));
       }
     }
-    // S <- gam_C S + K^T diag(D) u
-    mmx<NT, K, BV>(tid, [&](int m, int n, float x) { s.S[m][n] = s.gC * s.S[m][n] + x; },
-                   seg<C>([&](int m, int kk) { return s.k[kk][m] * s.D[kk]; },
-                          [&](int kk, int n) { return s.u[kk][n]; }));
     __syncthreads();
     if (c + 1 < nch) {
       nx.store(s, tid, p.beta_dtype);

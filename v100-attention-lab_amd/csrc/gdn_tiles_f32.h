@@ -77,6 +77,12 @@ struct RowLoad {
       if (e < ROWS * RV) {
         if constexpr (std::is_same<TIn, float>::value && LD % 4 == 0) {
           *reinterpret_cast<u32x4*>(&dst[t][col]) = r[i];
+        } else if constexpr (LD % 4 == 0) {
+          float x[VEC];
+          unpack16<TIn>(r[i], x);
+#pragma unroll
+          for (int j = 0; j < VEC; j += 4)
+            *reinterpret_cast<f32x4*>(&dst[t][col + j]) = f32x4{x[j], x[j + 1], x[j + 2], x[j + 3]};
         } else {
           float x[VEC];
           unpack16<TIn>(r[i], x);
@@ -103,12 +109,13 @@ __device__ __forceinline__ Seg<KD, FA, FB> seg(FA a, FB b) {
 // v_mfma_f32_16x16x4_f32 (full fp32), the G tiles in flight together.
 // Lane l supplies a(m0 + l % 16, k0 + l / 16) and b(k0 + l / 16, n0 + l % 16)
 // and holds rows m0 + 4 (l / 16) + i, column n0 + l % 16 of a tile.
-template <int G, int KD, typename FA, typename FB>
+// UNR0: contraction steps unrolled (0: all of a contraction of up to 32,
+// else 2, which keeps register use low where two waves share a SIMD).
+template <int G, int UNR0 = 0, int KD, typename FA, typename FB>
 __device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], const int (&n0)[G],
                                          int ng, int r, int kq, const Seg<KD, FA, FB>& s) {
   static_assert(KD % 4 == 0, "contraction length");
-  // short contractions fully unrolled: all their operand reads in flight
-  constexpr int UNR = KD <= 32 ? KD / 4 : 2;
+  constexpr int UNR = UNR0 > 0 ? (UNR0 < KD / 4 ? UNR0 : KD / 4) : (KD <= 32 ? KD / 4 : 2);
 #pragma unroll UNR
   for (int k0 = 0; k0 < KD; k0 += 4) {
     float av[G], bv[G];
@@ -124,7 +131,7 @@ __device__ __forceinline__ void seg_mfma(f32x4 (&acc)[G], const int (&m0)[G], co
 
 // out(m, n, sum over the segments) for an M x N result: 16 x 16 tiles dealt
 // round-robin to the NT / 64 waves, up to 4 of them in flight per wave.
-template <int NT, int M, int N, typename FO, typename... Segs>
+template <int NT, int M, int N, int UNR = 0, typename FO, typename... Segs>
 __device__ __forceinline__ void mmx(int tid, FO&& out, const Segs&... segs) {
   static_assert(M % 16 == 0 && N % 16 == 0, "16 x 16 tiles");
   constexpr int TNt = N / 16, NTILE = (M / 16) * TNt, NW = NT / 64;
@@ -143,7 +150,7 @@ __device__ __forceinline__ void mmx(int tid, FO&& out, const Segs&... segs) {
     f32x4 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-    (seg_mfma<G>(acc, m0, n0, ng, r, kq, segs), ...);
+    (seg_mfma<G, UNR>(acc, m0, n0, ng, r, kq, segs), ...);
 #pragma unroll
     for (int g = 0; g < G; ++g)
       if (g < ng) {
