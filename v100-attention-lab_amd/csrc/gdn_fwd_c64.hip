@@ -67,6 +67,26 @@ struct Rec {
 };
 inline int64_t rec_size(int K) { return 2 * C * C + (int64_t)C * K + 3 * C; }
 
+// The record for 16-bit inputs, in the same bytes: P, W and T diag(beta) as
+// fp16 hi + lo pairs (x = hi + lo to about 2^-22 relative; offsets in
+// halves), then the gates as floats (offset GF in floats).
+template <int K>
+struct Rec16 {
+  static constexpr int PH = 0, PL = C * C, WH = 2 * C * C, WL = 2 * C * C + C * K;
+  static constexpr int TH = 2 * C * C + 2 * C * K, TL = 3 * C * C + 2 * C * K;
+  static constexpr int NH = 4 * C * C + 2 * C * K;
+  static constexpr int GF = NH / 2;
+};
+static_assert(Rec16<128>::GF + 3 * C == Rec<128>::SIZE && Rec16<32>::GF + 3 * C == Rec<32>::SIZE,
+              "the two records take the same bytes");
+
+// x as an fp16 pair hi + lo.
+__device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
+  x = pin(x);
+  hi = (f16)x;
+  lo = (f16)(x - (float)hi);
+}
+
 // ---------------------------------------------------------------------------
 // 1. prep
 // ---------------------------------------------------------------------------
@@ -153,16 +173,24 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
     }
   }
   __syncthreads();
+  constexpr bool kF32 = std::is_same<TIn, float>::value;
+  using R16 = Rec16<K>;
+  f16* const rh = reinterpret_cast<f16*>(rec);
   for (int e = tid; e < C * C; e += NT) {
     const int t = e / C, j = e % C;
     const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
-    rec[R::PM + e] = mv * s.qk[t][j];
+    if constexpr (kF32) {
+      rec[R::PM + e] = mv * s.qk[t][j];
+    } else {
+      split_f16(mv * s.qk[t][j], rh[R16::PH + e], rh[R16::PL + e]);
+    }
     s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
   }
   if (tid < C) {
-    rec[R::G + tid] = s.gam[tid];
-    rec[R::G + C + tid] = s.D[tid];
-    rec[R::G + 2 * C + tid] = tid == 0 ? s.gC : 0.f;
+    float* const gr = kF32 ? rec + R::G : rec + R16::GF;
+    gr[tid] = s.gam[tid];
+    gr[C + tid] = s.D[tid];
+    gr[2 * C + tid] = tid == 0 ? s.gC : 0.f;
   }
   __syncthreads();
   // T11 = (I + A11)^-1 (lanes 0-31 of wave 0) and T22 = (I + A22)^-1 (lanes
@@ -193,11 +221,21 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
                   seg<32>([&](int m, int kk) { return s.t[32 + m][32 + kk]; },
                           [&](int kk, int n) { return s.qk[kk][n]; }));
   __syncthreads();
-  for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
+  if constexpr (kF32) {
+    for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
+  } else {
+    // T diag(beta), the operand of U = T diag(beta) V
+    for (int e = tid; e < C * C; e += NT)
+      split_f16(s.t[e / C][e % C] * s.bt[e % C], rh[R16::TH + e], rh[R16::TL + e]);
+  }
   // W = T diag(beta gam) K
-  mmx<NT, C, K, UNR>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
-                seg<C>([&](int m, int kk) { return s.t[m][kk]; },
-                       [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
+  mmx<NT, C, K, UNR>(tid,
+                     [&](int m, int n, float x) {
+                       if constexpr (kF32) rec[R::W + m * K + n] = x;
+                       else split_f16(x, rh[R16::WH + m * K + n], rh[R16::WL + m * K + n]);
+                     },
+                     seg<C>([&](int m, int kk) { return s.t[m][kk]; },
+                            [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
 }
 
 // ---------------------------------------------------------------------------
@@ -365,10 +403,306 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 2b. scan for 16-bit inputs: fp16 MFMA on hi + lo operand pairs
+// ---------------------------------------------------------------------------
+//
+// v_mfma_f32_16x16x32_f16 contracts 32 at once: lane (r, kq) supplies row r
+// of A and row r of B^T, 8 consecutive contraction indices 8 kq .. from
+// each 32-block, so every operand is stored with the contraction index
+// contiguous (K^T, V^T, S^T and u^T transposed).  q, k and v are exact in
+// fp16; every fp32 operand is an fp16 pair hi + lo, and a product of two
+// fp32 values is hi*hi + hi*lo + lo*hi (to about 2^-22 relative).  The
+// fp32 state S lives in the accumulators of waves 0-3 (rows 16 (w + 4 j)
+// of K); its hi / lo copies in LDS feed W S and Q S.
+
+constexpr int HP = 8;  // LDS row padding in halves (rows stay 16-byte aligned)
+
+template <int K>
+struct alignas(16) S16mem {
+  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
+  f16 wh[C][K + HP], wl[C][K + HP];
+  f16 q[C][K + HP];
+  f16 kt[K][C + HP];                   // K^T
+  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
+  f16 ph[C][C + HP], pl[C][C + HP];    // P
+  f16 vt[BV][C + HP];                  // V^T of the slice
+  f16 uh[BV][C + HP], ul[BV][C + HP];  // u^T
+  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
+  float gam[C], D[C];
+  float gC;
+};
+
+__device__ __forceinline__ f16x8 frag8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
+
+// ROWS x COLS halves, rows `ld` halves apart in global memory -> LDS rows of
+// LD halves, 16 bytes per lane.
+template <int ROWS, int COLS>
+struct HalfRows {
+  static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
+  u32x4 r[N];
+  __device__ __forceinline__ void load(int tid, const f16* src, int64_t ld) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT;
+      if (e < NV) r[i] = *reinterpret_cast<const u32x4*>(src + (e / RV) * ld + (e % RV) * 8);
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT;
+      if (e < NV) *reinterpret_cast<u32x4*>(&dst[e / RV][(e % RV) * 8]) = r[i];
+    }
+  }
+};
+
+// ROWS x COLS block of a 16-bit input (rows >= nvalid read as zero) in
+// 8-element vectors, handed out row-fastest (vector e: row e % ROWS) so that
+// the transposed LDS stores of a wave hit consecutive halves.
+template <typename TIn, int ROWS, int COLS>
+struct InRows {
+  static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
+  uint4 r[N];
+  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid, bool transposed) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT;
+      const int t = transposed ? e % ROWS : e / RV, c = transposed ? e / ROWS : e % RV;
+      r[i] = uint4{0u, 0u, 0u, 0u};
+      if (e < NV && t < nvalid) r[i] = *reinterpret_cast<const uint4*>(src + t * ld + 8 * c);
+    }
+  }
+  // dst[t][8c + j] (row-major) or dst[8c + j][t] (transposed), as fp16
+  template <int LD>
+  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD], bool transposed) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT;
+      if (e >= NV) continue;
+      f16 x[8];
+      InTraits<TIn>::to_op(r[i], x);
+      if (transposed) {
+        const int t = e % ROWS, c = e / ROWS;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[8 * c + j][t] = x[j];
+      } else {
+        *reinterpret_cast<f16x8*>(&dst[e / RV][8 * (e % RV)]) =
+            f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+      }
+    }
+  }
+};
+
+// Next chunk's record and rows, in registers.
+template <typename TIn, int K>
+struct Next16 {
+  using R = Rec16<K>;
+  HalfRows<C, C> ph, pl, th, tl;
+  HalfRows<C, K> wh, wl;
+  InRows<TIn, C, K> q, k;
+  InRows<TIn, C, BV> v;
+  float gm, dv, gc;
+  __device__ __forceinline__ void load(const FArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
+                                       const TIn* vg, int t0, int nval) {
+    const float* const rec = p.rec + ri * (int64_t)Rec<K>::SIZE;
+    const f16* const rh = reinterpret_cast<const f16*>(rec);
+    ph.load(tid, rh + R::PH, C);
+    pl.load(tid, rh + R::PL, C);
+    th.load(tid, rh + R::TH, C);
+    tl.load(tid, rh + R::TL, C);
+    wh.load(tid, rh + R::WH, K);
+    wl.load(tid, rh + R::WL, K);
+    q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval, false);
+    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval, true);
+    v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval, true);
+    gm = tid < C ? rec[R::GF + tid] : 0.f;
+    dv = tid < C ? rec[R::GF + C + tid] : 0.f;
+    gc = tid == 0 ? rec[R::GF + 2 * C] : 0.f;
+  }
+  __device__ __forceinline__ void store(S16mem<K>& s, int tid) const {
+    ph.store(tid, s.ph);
+    pl.store(tid, s.pl);
+    th.store(tid, s.th);
+    tl.store(tid, s.tl);
+    wh.store(tid, s.wh);
+    wl.store(tid, s.wl);
+    q.store(tid, s.q, false);
+    k.store(tid, s.kt, true);
+    v.store(tid, s.vt, true);
+    if (tid < C) {
+      s.gam[tid] = gm;
+      s.D[tid] = dv;
+    }
+    if (tid == 0) s.gC = gc;
+  }
+};
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
+  __shared__ S16mem<K> s;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  int unit = blockIdx.x;
+  if (p.xcd_remap) unit = (blockIdx.x & 7) * (p.units >> 3) + (blockIdx.x >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const int v0 = vs * BV;
+  const RowSpan rs = row_span(p.cu, p.T, bi);
+  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
+  const int nch = (rs.T + C - 1) / C;
+  const float scale = p.scale;
+  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  const int64_t ob = head_base(rs, hi, p.so) + v0;
+
+  // waves 0-3: the state rows 16 (w + 4 j) of K (accumulator layout: rows
+  // 4 kq + i, column r), u rows 16 w; waves 4-7: Q S and o rows 16 (w - 4)
+  constexpr int NST = (K / 16 + 3) / 4;
+  const bool upper = wave < 4;
+  const int um0 = 16 * (wave & 3);
+  f32x4 st[NST];
+  // S^T hi / lo for the products with S
+  auto put_state = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+        f16 h[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) split_f16(st[j][i], h[i], l[i]);
+        *reinterpret_cast<f16x4*>(&s.sh[r][m0 + 4 * kq]) = f16x4{h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<f16x4*>(&s.sl[r][m0 + 4 * kq]) = f16x4{l[0], l[1], l[2], l[3]};
+      }
+    }
+  };
+  if (upper) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st[j][i] = (p.h0 && m0 < K)
+                       ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + (m0 + 4 * kq + i) * p.sh0[2] + (v0 + r) * p.sh0[3]]
+                       : 0.f;
+    }
+    put_state();
+  }
+  Next16<TIn, K> nx;
+  if (nch > 0) {
+    nx.load(p, tid, slot0 * p.H + hi, qg, kg, vg, 0, min(C, rs.T));
+    nx.store(s, tid);
+  }
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * C, nval = min(C, rs.T - t0);
+    if (c + 1 < nch) nx.load(p, tid, (slot0 + c + 1) * p.H + hi, qg, kg, vg, t0 + C, min(C, rs.T - t0 - C));
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (upper) {
+      // u = T diag(beta) V - W S for rows um0 ..
+      f32x4 aw = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jb = 0; jb < C; jb += 32) {
+        const f16x8 b = frag8(&s.vt[r][jb + 8 * kq]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.th[um0 + r][jb + 8 * kq]), b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][jb + 8 * kq]), b, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 wh = frag8(&s.wh[um0 + r][kb + 8 * kq]), sh = frag8(&s.sh[r][kb + 8 * kq]);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, sh, aw, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, frag8(&s.sl[r][kb + 8 * kq]), aw, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.wl[um0 + r][kb + 8 * kq]), sh, aw, 0, 0, 0);
+      }
+      // u^T and (diag(D) u)^T as fp16 pairs: lane holds u rows um0 + 4 kq + i, column r
+      f16 uh[4], ul[4], dh[4], dl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float u = acc[i] - aw[i];
+        split_f16(u, uh[i], ul[i]);
+        split_f16(s.D[um0 + 4 * kq + i] * u, dh[i], dl[i]);
+      }
+      *reinterpret_cast<f16x4*>(&s.uh[r][um0 + 4 * kq]) = f16x4{uh[0], uh[1], uh[2], uh[3]};
+      *reinterpret_cast<f16x4*>(&s.ul[r][um0 + 4 * kq]) = f16x4{ul[0], ul[1], ul[2], ul[3]};
+      *reinterpret_cast<f16x4*>(&s.dh[r][um0 + 4 * kq]) = f16x4{dh[0], dh[1], dh[2], dh[3]};
+      *reinterpret_cast<f16x4*>(&s.dl[r][um0 + 4 * kq]) = f16x4{dl[0], dl[1], dl[2], dl[3]};
+    } else {
+      // Q S for rows um0 .. (q exact in fp16)
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 a = frag8(&s.q[um0 + r][kb + 8 * kq]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, frag8(&s.sh[r][kb + 8 * kq]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, frag8(&s.sl[r][kb + 8 * kq]), acc, 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (upper) {
+      // S <- gam_C S + K^T diag(D) u (k exact in fp16)
+#pragma unroll
+      for (int j = 0; j < NST; ++j) {
+        const int m0 = 16 * (wave + 4 * j);
+        if (m0 < K) {
+          f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int tb = 0; tb < C; tb += 32) {
+            const f16x8 kt = frag8(&s.kt[m0 + r][tb + 8 * kq]);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][tb + 8 * kq]), a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][tb + 8 * kq]), a, 0, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[j][i] = s.gC * st[j][i] + a[i];
+        }
+      }
+      put_state();
+    } else {
+      // o = scale (P u + diag(gam) Q S)
+      f32x4 ao = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jb = 0; jb < C; jb += 32) {
+        const f16x8 ph = frag8(&s.ph[um0 + r][jb + 8 * kq]), uh = frag8(&s.uh[r][jb + 8 * kq]);
+        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, uh, ao, 0, 0, 0);
+        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
+        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.pl[um0 + r][jb + 8 * kq]), uh, ao, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = um0 + 4 * kq + i;
+        if (row < nval)
+          store_scalar(p.o, ob + (int64_t)(t0 + row) * p.so[1] + r, p.o_dtype,
+                       scale * (ao[i] + s.gam[row] * acc[i]));
+      }
+    }
+    __syncthreads();
+    if (c + 1 < nch) {
+      nx.store(s, tid);
+      __syncthreads();
+    }
+  }
+  if (upper) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p.fs[bi * p.sfs[0] + hi * p.sfs[1] + (m0 + 4 * kq + i) * p.sfs[2] + (v0 + r) * p.sfs[3]] = st[j][i];
+      }
+    }
+  }
+}
+
 template <typename TIn, int K>
 int launch_k(const FArgs& a, int64_t nrec, hipStream_t s) {
   if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NT), 0, s, a);
-  hipLaunchKernelGGL((scan_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
+  if constexpr (std::is_same<TIn, float>::value)
+    hipLaunchKernelGGL((scan_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((scan16_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
   return (int)hipGetLastError();
 }
 
