@@ -97,21 +97,25 @@ def _params(L, **kw):
 
 def test_fwd_workspace_size(lib, pkg):
     """Fused kernels need no workspace; 64-row chunks with K <= 128 take one
-    fp32 record per (chunk slot, head): T and P (C x C), W (C x K), three
-    gate rows."""
+    record per (chunk slot, head).  fp32 inputs: T and P (C x C), W (C x K)
+    in fp32, then three gate rows.  16-bit inputs: T diag(beta) (C x C) as
+    an fp16 hi/lo pair, then four fp32 gate rows."""
     L = pkg._lib
     size = lambda **kw: lib.gdn_fwd_workspace_size(ctypes.byref(_params(L, **kw)))
     assert size() == 0                                   # C = 32: pipelined, none
     assert size(chunk_size=64, K=256) == 0               # phased kernel, none
     assert size(chunk_size=64, flags=1) == 0             # phased forced, none
     C, K, H = 64, 128, 16
-    rec = 4 * (2 * C * C + C * K + 3 * C)
-    want = 2 * (4096 // C) * H * rec
-    assert want <= size(chunk_size=64) < want + 256
+    rec32 = 4 * (2 * C * C + C * K + 3 * C)
+    rec16 = 2 * 2 * C * C + 4 * 4 * C
+    for dt, rec in ((0, rec32), (1, rec16), (2, rec16)):
+        want = 2 * (4096 // C) * H * rec
+        assert want <= size(chunk_size=64, qkv_dtype=dt) < want + 256
     # packed sequences: slots ceil(T / C) + N = 2 + 3
     got = size(chunk_size=64, B=3, T=100, cu_seqlens=0x2000)
-    assert 5 * H * rec <= got < 5 * H * rec + 256
+    assert 5 * H * rec16 <= got < 5 * H * rec16 + 256
     assert size(chunk_size=64, B=0) == -1
+    assert size(chunk_size=64, qkv_dtype=9) == -1
     assert lib.gdn_fwd_workspace_size(None) == -1
 
 

@@ -79,8 +79,9 @@ int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
   if (prm == nullptr) return -1;
   const GdnFwdParams& P = *prm;
   if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0) return -1;
+  if (!valid_dtype(P.qkv_dtype)) return -1;
   if (!uses_c64(P)) return 0;
-  return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0);
+  return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
 }
 
 int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
@@ -114,7 +115,7 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
   if (c64) {
-    const int64_t need = c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0);
+    const int64_t need = c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
     if (P.T > 0 && (P.workspace == nullptr || reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 ||
                     P.workspace_bytes < need))
       return GDN_ERR_WORKSPACE;

@@ -1,25 +1,27 @@
 // The forward for 64-row chunks, as two launches (fp16, bf16 and fp32
-// inputs; K in {32, 64, 128}; fp32 arithmetic on v_mfma_f32_16x16x4_f32).
+// inputs; K in {32, 64, 128}).
 //
 // Per chunk (C = 64 rows, b = in-chunk cumsum of g, gam = e^b, D_j =
 // e^{bC - b_j}, M[t][j] = e^{b_t - b_j} for j <= t), as in gdn_ref.py:48-99:
 //   A = tril_-1(beta_t M K K^T),  T = (I + A)^-1,  W = T diag(beta gam) K,
-//   u = T diag(beta) V - W S,
+//   u = T diag(beta) V - W S = T diag(beta) (V - diag(gam) K S),
 //   o = scale (P u + diag(gam) Q S),  P = M o (Q K^T),
 //   S' = gam_C S + K^T diag(D) u.
-// Only u, o and S' involve the carried state S.  With 64-row chunks the
-// state-independent half (the K K^T and Q K^T products, the 64 x 64
-// substitution, W) is the larger one, and it runs first, for every chunk at
-// once:
-//   1. prep_kernel, one workgroup per (chunk, head): gates, T (two 32 x 32
+// Only u, o and S' involve the carried state S.  The 64 x 64 substitution
+// for T is the long serial step and does not depend on S; it runs first,
+// for every chunk at once:
+//   1. prep, one workgroup per (chunk, head): gates and T (two 32 x 32
 //      diagonal solves, one lane per column, then the off-diagonal block
-//      T21 = -T22 A21 T11 on the matrix cores), W and P, written to a
-//      per-chunk record in the caller's workspace;
-//   2. scan_kernel, one workgroup per (sequence, head, 16-column V slice):
-//      walks the chunks with S resident in LDS (O(B H K V) state: no chunk
-//      state is written), loading the next chunk's record and rows while the
-//      current one computes.  Waves 0-3 compute u (16 rows each), then the
-//      state update; waves 4-7 compute Q S for the same rows, then o.
+//      T21 = -T22 A21 T11 on the matrix cores), written to a per-chunk
+//      record in the caller's workspace;
+//   2. scan, one workgroup per (sequence, head, 16-column V slice): walks
+//      the chunks with S on chip (no chunk state is written), loading the
+//      next chunk's record and rows while the current one computes.
+// fp32 inputs (prep_kernel, scan_kernel: fp32 MFMA) also keep W and P in
+// the record.  16-bit inputs (prep16_kernel, scan16_kernel: fp16 MFMA on hi
+// + lo pairs) keep only T diag(beta) and the gates there; the scan forms
+// K S, u, P and o from the q, k, v rows it loads anyway, and reads 57 KB
+// per chunk and V slice instead of 98 KB (K = 128).
 // Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
 // onwards, as in the backward.
 
@@ -57,28 +59,26 @@ struct FArgs {
   int xcd_remap;
 };
 
-// Per-(slot, head) record, in floats: T and P as [C][C], W as [C][K], then
-// gam and D as [C] each and gam_C (first of a [C] row).
+// Per-(slot, head) record for fp32 inputs, in floats: T and P as [C][C], W
+// as [C][K], then gam and D as [C] each and gam_C (first of a [C] row).
 template <int K>
 struct Rec {
   static constexpr int T = 0, PM = C * C, W = 2 * C * C;
   static constexpr int G = W + C * K;
   static constexpr int SIZE = G + 3 * C;
 };
-inline int64_t rec_size(int K) { return 2 * C * C + (int64_t)C * K + 3 * C; }
-
-// The record for 16-bit inputs, in the same bytes: P, W and T diag(beta) as
-// fp16 hi + lo pairs (x = hi + lo to about 2^-22 relative; offsets in
-// halves), then the gates as floats (offset GF in floats).
-template <int K>
+// The record for 16-bit inputs: T diag(beta) as an fp16 pair hi + lo (x =
+// hi + lo to about 2^-22 relative; offsets TH, TL in halves), then gam, D
+// and b as [C] floats each and gam_C (first of a [C] row; offset GF in
+// floats).
 struct Rec16 {
-  static constexpr int PH = 0, PL = C * C, WH = 2 * C * C, WL = 2 * C * C + C * K;
-  static constexpr int TH = 2 * C * C + 2 * C * K, TL = 3 * C * C + 2 * C * K;
-  static constexpr int NH = 4 * C * C + 2 * C * K;
-  static constexpr int GF = NH / 2;
+  static constexpr int TH = 0, TL = C * C;
+  static constexpr int GF = C * C;
+  static constexpr int SIZE = GF + 4 * C;
 };
-static_assert(Rec16<128>::GF + 3 * C == Rec<128>::SIZE && Rec16<32>::GF + 3 * C == Rec<32>::SIZE,
-              "the two records take the same bytes");
+// floats per record (fp32 or 16-bit inputs)
+constexpr int64_t rec_floats(int K, bool half) { return half ? Rec16::SIZE : 2 * C * C + (int64_t)C * K + 3 * C; }
+static_assert(Rec<128>::SIZE == rec_floats(128, false) && Rec<32>::SIZE == rec_floats(32, false), "record sizes");
 
 // x as an fp16 pair hi + lo.
 __device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
@@ -91,6 +91,56 @@ __device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
 // 1. prep
 // ---------------------------------------------------------------------------
 
+// In-chunk gates from g (gl), in lanes 0 .. C-1: b as a plain running sum
+// (the association order of a sequential cumsum), gam = e^b, D = e^{b_C - b}
+// and gam_C.
+__device__ __forceinline__ void chunk_gates(int tid, const float* gl, float* b, float* gam, float* D, float& gC) {
+  if (tid < C) {
+    float bt = 0.f, bc = 0.f;
+    for (int j = 0; j < C; ++j) {
+      bc += gl[j];
+      if (j == tid) bt = bc;
+    }
+    b[tid] = bt;
+    gam[tid] = expf(bt);
+    D[tid] = expf(bc - bt);
+    if (tid == C - 1) gC = expf(bc);
+  }
+}
+
+// T = (I + A)^-1 for a strictly lower 64 x 64 A (a barrier passed since A
+// was written): T11 = (I + A11)^-1 (lanes 0-31 of wave 0) and T22 =
+// (I + A22)^-1 (lanes 0-31 of wave 1), one column per lane held in
+// registers, T12 = 0; then X = A21 T11 (x: 32 x 32 scratch) and
+// T21 = -T22 X on the matrix cores.  Ends with a barrier.
+template <int XLD>
+__device__ __forceinline__ void solve_t(int tid, float (*a)[C + PAD], float (*t)[C + PAD], float (*x)[XLD]) {
+  if ((tid & 63) < 32 && tid < 128) {
+    const int o = tid < 64 ? 0 : 32, cc = tid & 31;
+    float col[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      float v = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) v = __builtin_fmaf(-a[o + i][o + j], col[j], v);
+      col[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      t[o + i][o + cc] = col[i];
+      t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21 overwritten below)
+    }
+  }
+  __syncthreads();
+  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { x[m][n] = v; },
+                       seg<32>([&](int m, int kk) { return a[32 + m][kk]; }, [&](int kk, int n) { return t[kk][n]; }));
+  __syncthreads();
+  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { t[32 + m][n] = -v; },
+                       seg<32>([&](int m, int kk) { return t[32 + m][32 + kk]; },
+                               [&](int kk, int n) { return x[kk][n]; }));
+  __syncthreads();
+}
+
 template <int K>
 struct alignas(16) PSmem {
   float q[C][K + PAD], k[C][K + PAD];
@@ -101,7 +151,8 @@ struct alignas(16) PSmem {
   float gC;
 };
 
-template <typename TIn, int K>
+// fp32 inputs: record T, P, W and the gates.
+template <int K>
 __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
   using R = Rec<K>;
   __shared__ PSmem<K> s;
@@ -115,9 +166,9 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
   float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
 
   {
-    RowLoad<TIn, C, K, NT> lq, lk;
-    lq.load(tid, static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq) + t0 * p.sq[1], p.sq[1], nval);
-    lk.load(tid, static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + t0 * p.sk[1], p.sk[1], nval);
+    RowLoad<float, C, K, NT> lq, lk;
+    lq.load(tid, static_cast<const float*>(p.q) + head_base(rs, hi, p.sq) + t0 * p.sq[1], p.sq[1], nval);
+    lk.load(tid, static_cast<const float*>(p.k) + head_base(rs, hi, p.sk) + t0 * p.sk[1], p.sk[1], nval);
     float gv = 0.f, bv = 0.f;
     if (tid < nval) {
       gv = load_scalar(p.g, head_base(rs, hi, p.sg) + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
@@ -131,109 +182,28 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
     }
   }
   __syncthreads();
-  if (tid < C) {
-    // sequential cumsum in each lane (the association order of a plain
-    // running sum)
-    float bt = 0.f, bc = 0.f;
-    for (int j = 0; j < C; ++j) {
-      bc += s.gl[j];
-      if (j == tid) bt = bc;
-    }
-    s.b[tid] = bt;
-    s.gam[tid] = expf(bt);
-    s.D[tid] = expf(bc - bt);
-    if (tid == C - 1) s.gC = expf(bc);
-  }
-  if constexpr (std::is_same<TIn, float>::value) {
-    mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
-                       seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-    mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
-                       seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-  } else {
-    // 16-bit inputs are exact in fp16 (bf16 values within the fp16 range,
-    // as in the fused kernels): K K^T and Q K^T on v_mfma_f32_16x16x32_f16,
-    // exact products with fp32 accumulation.  Lane (r, kq) supplies 8
-    // consecutive k of row r; 2 x 16 tiles over the 8 waves.
-    const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
-    auto frag8 = [&](const float* row) {
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(row), hi = *reinterpret_cast<const f32x4*>(row + 4);
-      return f16x8{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3], (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
-    };
-    for (int job = tid >> 6; job < 2 * (C / 16) * (C / 16); job += NT / 64) {
-      const int mat = job / ((C / 16) * (C / 16)), mt = (job / (C / 16)) % (C / 16), nt = job % (C / 16);
-      const float* arow = (mat ? &s.q[0][0] : &s.k[0][0]) + (16 * mt + r) * (K + PAD) + 8 * kq;
-      const float* brow = &s.k[0][0] + (16 * nt + r) * (K + PAD) + 8 * kq;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < K / 32; ++kb)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(arow + 32 * kb), frag8(brow + 32 * kb), acc, 0, 0, 0);
-      float(*dst)[C + PAD] = mat ? s.qk : s.a;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[16 * mt + 4 * kq + i][16 * nt + r] = acc[i];
-    }
-  }
+  chunk_gates(tid, s.gl, s.b, s.gam, s.D, s.gC);
+  mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
+                     seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                     seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
   __syncthreads();
-  constexpr bool kF32 = std::is_same<TIn, float>::value;
-  using R16 = Rec16<K>;
-  f16* const rh = reinterpret_cast<f16*>(rec);
   for (int e = tid; e < C * C; e += NT) {
     const int t = e / C, j = e % C;
     const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
-    if constexpr (kF32) {
-      rec[R::PM + e] = mv * s.qk[t][j];
-    } else {
-      split_f16(mv * s.qk[t][j], rh[R16::PH + e], rh[R16::PL + e]);
-    }
+    rec[R::PM + e] = mv * s.qk[t][j];
     s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
   }
   if (tid < C) {
-    float* const gr = kF32 ? rec + R::G : rec + R16::GF;
-    gr[tid] = s.gam[tid];
-    gr[C + tid] = s.D[tid];
-    gr[2 * C + tid] = tid == 0 ? s.gC : 0.f;
+    rec[R::G + tid] = s.gam[tid];
+    rec[R::G + C + tid] = s.D[tid];
+    rec[R::G + 2 * C + tid] = tid == 0 ? s.gC : 0.f;
   }
   __syncthreads();
-  // T11 = (I + A11)^-1 (lanes 0-31 of wave 0) and T22 = (I + A22)^-1 (lanes
-  // 0-31 of wave 1): one column per lane, the column in registers
-  if ((tid & 63) < 32 && tid < 128) {
-    const int o = tid < 64 ? 0 : 32, cc = tid & 31;
-    float col[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      float x = (i == cc) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) x = __builtin_fmaf(-s.a[o + i][o + j], col[j], x);
-      col[i] = x;
-    }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      s.t[o + i][o + cc] = col[i];
-      s.t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21 overwritten below)
-    }
-  }
-  __syncthreads();
-  // X = A21 T11 -> qk
-  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
-                  seg<32>([&](int m, int kk) { return s.a[32 + m][kk]; }, [&](int kk, int n) { return s.t[kk][n]; }));
-  __syncthreads();
-  // T21 = -T22 X
-  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float x) { s.t[32 + m][n] = -x; },
-                  seg<32>([&](int m, int kk) { return s.t[32 + m][32 + kk]; },
-                          [&](int kk, int n) { return s.qk[kk][n]; }));
-  __syncthreads();
-  if constexpr (kF32) {
-    for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
-  } else {
-    // T diag(beta), the operand of U = T diag(beta) V
-    for (int e = tid; e < C * C; e += NT)
-      split_f16(s.t[e / C][e % C] * s.bt[e % C], rh[R16::TH + e], rh[R16::TL + e]);
-  }
+  solve_t<C + PAD>(tid, s.a, s.t, s.qk);
+  for (int e = tid; e < C * C; e += NT) rec[R::T + e] = s.t[e / C][e % C];
   // W = T diag(beta gam) K
-  mmx<NT, C, K, UNR>(tid,
-                     [&](int m, int n, float x) {
-                       if constexpr (kF32) rec[R::W + m * K + n] = x;
-                       else split_f16(x, rh[R16::WH + m * K + n], rh[R16::WL + m * K + n]);
-                     },
+  mmx<NT, C, K, UNR>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
                      seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                             [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
 }
@@ -404,141 +374,280 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2b. scan for 16-bit inputs: fp16 MFMA on hi + lo operand pairs
+// 3. 16-bit inputs: fp16 MFMA on hi + lo operand pairs
 // ---------------------------------------------------------------------------
 //
-// v_mfma_f32_16x16x32_f16 contracts 32 at once: lane (r, kq) supplies row r
-// of A and row r of B^T, 8 consecutive contraction indices 8 kq .. from
-// each 32-block, so every operand is stored with the contraction index
-// contiguous (K^T, V^T, S^T and u^T transposed).  q, k and v are exact in
-// fp16; every fp32 operand is an fp16 pair hi + lo, and a product of two
-// fp32 values is hi*hi + hi*lo + lo*hi (to about 2^-22 relative).  The
-// fp32 state S lives in the accumulators of waves 0-3 (rows 16 (w + 4 j)
-// of K); its hi / lo copies in LDS feed W S and Q S.
+// v_mfma_f32_16x16x32_f16: lane (r, kq) (r = lane % 16, kq = lane / 16)
+// supplies row r of A and row r of B^T, 8 consecutive contraction indices
+// 8 kq .. from each 32-block, so every operand is stored with the
+// contraction index contiguous; the accumulator holds rows 4 kq + i,
+// column r.  q, k and v are exact in fp16 (bf16 values within the fp16
+// range, as in the fused kernels); every fp32 operand is an fp16 pair
+// hi + lo, and a product of two fp32 values is hi*hi + hi*lo + lo*hi (to
+// about 2^-22 relative).
 
 constexpr int HP = 8;  // LDS row padding in halves (rows stay 16-byte aligned)
 
-template <int K>
-struct alignas(16) S16mem {
-  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
-  f16 wh[C][K + HP], wl[C][K + HP];
-  f16 q[C][K + HP];
-  f16 kt[K][C + HP];                   // K^T
-  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
-  f16 ph[C][C + HP], pl[C][C + HP];    // P
-  f16 vt[BV][C + HP];                  // V^T of the slice
-  f16 uh[BV][C + HP], ul[BV][C + HP];  // u^T
-  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
-  float gam[C], D[C];
-  float gC;
-};
-
 __device__ __forceinline__ f16x8 frag8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
+
+// Row m0 + r of K^T, contraction indices t0 + 8 kq .. t0 + 8 kq + 7, from
+// row-major K in LDS by two ds_read_b64_tr_b16: in each group of 16 lanes,
+// lane i receives as element j halfword i % 4 of the 8 bytes addressed by
+// lane 4 j + i / 4 of the group.  Lane (r, kq) addresses
+// k[t0 + 8 kq + 4 h + r / 4][m0 + 4 (r % 4)] and so receives
+// K[t0 + 8 kq + 4 h + j][m0 + r], j = 0..3, for h = 0, 1.
+template <int LD>
+__device__ __forceinline__ f16x8 frag8_t(const f16 (*k)[LD], int t0, int m0, int r, int kq) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const f16* const a0 = &k[t0 + 8 * kq + (r >> 2)][m0 + 4 * (r & 3)];
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0 + 4 * LD));
+  union {
+    s16x4 h[2];
+    f16x8 f;
+  } u;
+  u.h[0] = lo;
+  u.h[1] = hi;
+  return u.f;
+}
+
+__device__ __forceinline__ void store_pair4(f16* hi, f16* lo, const float (&x)[4]) {
+  f16 h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) split_f16(x[i], h[i], l[i]);
+  *reinterpret_cast<f16x4*>(hi) = f16x4{h[0], h[1], h[2], h[3]};
+  *reinterpret_cast<f16x4*>(lo) = f16x4{l[0], l[1], l[2], l[3]};
+}
+
+// The loaders below load unconditionally, guarded at most by a wave-uniform
+// test (none when the vectors fill every lane): a lane-masked load, a zero
+// written into a register a load may still target, or a load that a later
+// path may leave unconsumed, makes the wave wait for every load in flight.
 
 // ROWS x COLS halves, rows `ld` halves apart in global memory -> LDS rows of
 // LD halves, 16 bytes per lane.
 template <int ROWS, int COLS>
 struct HalfRows {
   static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
+  static_assert(NV % 64 == 0, "whole waves");
   u32x4 r[N];
   __device__ __forceinline__ void load(int tid, const f16* src, int64_t ld) {
+    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int e = tid + i * NT;
-      if (e < NV) r[i] = *reinterpret_cast<const u32x4*>(src + (e / RV) * ld + (e % RV) * 8);
+      if (NV % NT == 0 || w0 + i * NT < NV) r[i] = *reinterpret_cast<const u32x4*>(src + (e / RV) * ld + (e % RV) * 8);
     }
   }
   template <int LD>
   __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
+    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int e = tid + i * NT;
-      if (e < NV) *reinterpret_cast<u32x4*>(&dst[e / RV][(e % RV) * 8]) = r[i];
+      if (NV % NT == 0 || w0 + i * NT < NV) *reinterpret_cast<u32x4*>(&dst[e / RV][(e % RV) * 8]) = r[i];
     }
   }
 };
 
-// ROWS x COLS block of a 16-bit input (rows >= nvalid read as zero) in
-// 8-element vectors, handed out row-fastest (vector e: row e % ROWS) so that
-// the transposed LDS stores of a wave hit consecutive halves.
+// ROWS x COLS block of a 16-bit input, row-major, in 8-element vectors
+// (vector e: row e / RV), stored as fp16.  Rows >= nvalid (>= 1) load row
+// nvalid - 1 and are stored as zero.
 template <typename TIn, int ROWS, int COLS>
 struct InRows {
   static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
+  static_assert(NV % 64 == 0, "whole waves");
   uint4 r[N];
-  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid, bool transposed) {
+  int nv;
+  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid) {
+    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
+    nv = nvalid;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int e = tid + i * NT;
-      const int t = transposed ? e % ROWS : e / RV, c = transposed ? e / ROWS : e % RV;
-      r[i] = uint4{0u, 0u, 0u, 0u};
-      if (e < NV && t < nvalid) r[i] = *reinterpret_cast<const uint4*>(src + t * ld + 8 * c);
+      if (NV % NT == 0 || w0 + i * NT < NV)
+        r[i] = *reinterpret_cast<const uint4*>(src + min(e / RV, nvalid - 1) * ld + 8 * (e % RV));
     }
   }
-  // dst[t][8c + j] (row-major) or dst[8c + j][t] (transposed), as fp16
   template <int LD>
-  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD], bool transposed) const {
+  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
+    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int e = tid + i * NT;
-      if (e >= NV) continue;
-      f16 x[8];
-      InTraits<TIn>::to_op(r[i], x);
-      if (transposed) {
-        const int t = e % ROWS, c = e / ROWS;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dst[8 * c + j][t] = x[j];
-      } else {
-        *reinterpret_cast<f16x8*>(&dst[e / RV][8 * (e % RV)]) =
-            f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+      if (NV % NT == 0 || w0 + i * NT < NV) {
+        const bool ok = e / RV < nv;
+        const uint4 v = {ok ? r[i].x : 0u, ok ? r[i].y : 0u, ok ? r[i].z : 0u, ok ? r[i].w : 0u};
+        f16 x[8];
+        InTraits<TIn>::to_op(v, x);
+        *reinterpret_cast<f16x8*>(&dst[e / RV][8 * (e % RV)]) = f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
       }
     }
   }
 };
 
-// Next chunk's record and rows, in registers.
-template <typename TIn, int K>
-struct Next16 {
-  using R = Rec16<K>;
-  HalfRows<C, C> ph, pl, th, tl;
-  HalfRows<C, K> wh, wl;
-  InRows<TIn, C, K> q, k;
-  InRows<TIn, C, BV> v;
-  float gm, dv, gc;
-  __device__ __forceinline__ void load(const FArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
-                                       const TIn* vg, int t0, int nval) {
-    const float* const rec = p.rec + ri * (int64_t)Rec<K>::SIZE;
-    const f16* const rh = reinterpret_cast<const f16*>(rec);
-    ph.load(tid, rh + R::PH, C);
-    pl.load(tid, rh + R::PL, C);
-    th.load(tid, rh + R::TH, C);
-    tl.load(tid, rh + R::TL, C);
-    wh.load(tid, rh + R::WH, K);
-    wl.load(tid, rh + R::WL, K);
-    q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval, false);
-    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval, true);
-    v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval, true);
-    gm = tid < C ? rec[R::GF + tid] : 0.f;
-    dv = tid < C ? rec[R::GF + C + tid] : 0.f;
-    gc = tid == 0 ? rec[R::GF + 2 * C] : 0.f;
+// The C x BV slice of V, one pair of elements per lane (row lane / (BV / 2)),
+// stored transposed as fp16 (dst[column][row]).  Rows >= nvalid (>= 1) load
+// row nvalid - 1 and are stored as zero.
+template <typename TIn>
+struct VPairs {
+  static_assert(C * BV / 2 == NT, "one pair per lane");
+  uint32_t r;
+  int nv;
+  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid) {
+    nv = nvalid;
+    r = *reinterpret_cast<const uint32_t*>(src + min(tid / (BV / 2), nvalid - 1) * ld + 2 * (tid % (BV / 2)));
   }
-  __device__ __forceinline__ void store(S16mem<K>& s, int tid) const {
-    ph.store(tid, s.ph);
-    pl.store(tid, s.pl);
-    th.store(tid, s.th);
-    tl.store(tid, s.tl);
-    wh.store(tid, s.wh);
-    wl.store(tid, s.wl);
-    q.store(tid, s.q, false);
-    k.store(tid, s.kt, true);
-    v.store(tid, s.vt, true);
-    if (tid < C) {
-      s.gam[tid] = gm;
-      s.D[tid] = dv;
+  template <int LD>
+  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
+    const int t = tid / (BV / 2), c = tid % (BV / 2);
+    const uint32_t v = t < nv ? r : 0u;
+    const uint16_t l16 = (uint16_t)(v & 0xffffu), h16 = (uint16_t)(v >> 16);
+    if constexpr (std::is_same<TIn, f16>::value) {
+      dst[2 * c][t] = __builtin_bit_cast(f16, l16);
+      dst[2 * c + 1][t] = __builtin_bit_cast(f16, h16);
+    } else {
+      dst[2 * c][t] = (f16)bf16_bits_to_float(l16);
+      dst[2 * c + 1][t] = (f16)bf16_bits_to_float(h16);
     }
-    if (tid == 0) s.gC = gc;
   }
 };
 
+template <int K>
+struct alignas(16) P16mem {
+  f16 k[C][K + HP];
+  float a[C][C + PAD];    // K K^T, then A
+  float x[32][32 + PAD];  // A21 T11
+  float t[C][C + PAD];
+  float gl[C], bt[C], b[C], gam[C], D[C];
+  float gC;
+};
+
+// 16-bit inputs: record T diag(beta) and the gates.  58 KB of LDS at
+// K = 128, so two workgroups share a CU.
+template <typename TIn, int K>
+__global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
+  __shared__ P16mem<K> s;
+  const int tid = threadIdx.x;
+  const int64_t slot = blockIdx.x / p.H;
+  const int hi = blockIdx.x % p.H;
+  RowSpan rs;
+  int c;
+  if (!slot_chunk<C>(p, slot, rs, c)) return;
+  const int t0 = c * C, nval = min(C, rs.T - t0);
+  float* const rec = p.rec + (slot * p.H + hi) * (int64_t)Rec16::SIZE;
+  f16* const rh = reinterpret_cast<f16*>(rec);
+
+  {
+    InRows<TIn, C, K> lk;
+    lk.load(tid, static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    float gv = 0.f, bv = 0.f;
+    if (tid < nval) {
+      gv = load_scalar(p.g, head_base(rs, hi, p.sg) + (int64_t)(t0 + tid) * p.sg[1], p.g_dtype);
+      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype);
+    }
+    lk.store(tid, s.k);
+    if (tid < C) {
+      s.gl[tid] = gv;
+      s.bt[tid] = bv;
+    }
+  }
+  __syncthreads();
+  chunk_gates(tid, s.gl, s.b, s.gam, s.D, s.gC);
+  {
+    // K K^T on the 10 tiles on or below the diagonal (exact products, fp32
+    // accumulation); the tiles above are masked out below
+    const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
+    for (int job = tid >> 6; job < 10; job += NT / 64) {
+      const int mt = job < 1 ? 0 : job < 3 ? 1 : job < 6 ? 2 : 3;
+      const int nt = job - mt * (mt + 1) / 2;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * mt + r][kb + 8 * kq]),
+                                                     frag8(&s.k[16 * nt + r][kb + 8 * kq]), acc, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s.a[16 * mt + 4 * kq + i][16 * nt + r] = acc[i];
+    }
+  }
+  __syncthreads();
+  // A = tril_-1(beta_t M K K^T)
+  for (int e = tid; e < C * C; e += NT) {
+    const int t = e / C, j = e % C;
+    const float mv = expf(j < t ? s.b[t] - s.b[j] : 0.f);
+    s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
+  }
+  if (tid < C) {
+    float* const gr = rec + Rec16::GF;
+    gr[tid] = s.gam[tid];
+    gr[C + tid] = s.D[tid];
+    gr[2 * C + tid] = s.b[tid];
+    gr[3 * C + tid] = tid == 0 ? s.gC : 0.f;
+  }
+  __syncthreads();
+  solve_t<32 + PAD>(tid, s.a, s.t, s.x);
+  // T diag(beta) as fp16 pairs, 8 consecutive entries of a row per lane
+  static_assert(C * C == 8 * NT, "one 8-entry piece per lane");
+  {
+    const int t = tid / 8, j0 = 8 * (tid % 8);
+    f16 h[8], l[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) split_f16(s.t[t][j0 + jj] * s.bt[j0 + jj], h[jj], l[jj]);
+    *reinterpret_cast<f16x8*>(rh + Rec16::TH + t * C + j0) = f16x8{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+    *reinterpret_cast<f16x8*>(rh + Rec16::TL + t * C + j0) = f16x8{l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+  }
+}
+
+template <int K>
+struct alignas(16) S16mem {
+  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
+  f16 q[C][K + HP], k[C][K + HP];
+  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
+  f16 ph[C][C + HP], pl[C][C + HP];    // P
+  f16 vt[BV][C + HP];                  // V^T of the slice
+  f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
+  f16 uh[BV][C + HP], ul[BV][C + HP];  // u^T
+  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
+  // gam, D, b, {gam_C, 0 ..}: the record's gate rows, staged by every lane
+  // (rows 4 .. 7 repeat them)
+  float gv[NT / C][C];
+};
+
+// Next chunk's record and rows, in registers.
+template <typename TIn, int K>
+struct Next16 {
+  HalfRows<C, C> th, tl;
+  InRows<TIn, C, K> q, k;
+  VPairs<TIn> v;
+  float gate;
+  __device__ __forceinline__ void load(const FArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
+                                       const TIn* vg, int t0, int nval) {
+    const float* const rec = p.rec + ri * (int64_t)Rec16::SIZE;
+    const f16* const rh = reinterpret_cast<const f16*>(rec);
+    th.load(tid, rh + Rec16::TH, C);
+    tl.load(tid, rh + Rec16::TL, C);
+    q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
+    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
+    gate = rec[Rec16::GF + (tid & (4 * C - 1))];
+  }
+  __device__ __forceinline__ void store(S16mem<K>& s, int tid) const {
+    th.store(tid, s.th);
+    tl.store(tid, s.tl);
+    q.store(tid, s.q);
+    k.store(tid, s.k);
+    v.store(tid, s.vt);
+    s.gv[tid / C][tid % C] = gate;
+  }
+};
+
+// Per chunk: (A) K S on waves 0-3 and Q S on waves 4-7 (rows 16 (w & 3) ..),
+// then Y = V - diag(gam) K S; (A2) u = T diag(beta) Y on waves 0-3 while
+// waves 4-7 form P; (B) the state update on waves 0-3 while waves 4-7 write
+// o; then the next chunk's rows are staged.  The fp32 state S lives in the
+// accumulators of waves 0-3 (rows 16 (w + 4 j) of K); its hi / lo copies
+// in LDS feed K S and Q S.
 template <typename TIn, int K>
 __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   __shared__ S16mem<K> s;
@@ -561,8 +670,6 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
   const int64_t ob = head_base(rs, hi, p.so) + v0;
 
-  // waves 0-3: the state rows 16 (w + 4 j) of K (accumulator layout: rows
-  // 4 kq + i, column r), u rows 16 w; waves 4-7: Q S and o rows 16 (w - 4)
   constexpr int NST = (K / 16 + 3) / 4;
   const bool upper = wave < 4;
   const int um0 = 16 * (wave & 3);
@@ -573,11 +680,8 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
     for (int j = 0; j < NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        f16 h[4], l[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) split_f16(st[j][i], h[i], l[i]);
-        *reinterpret_cast<f16x4*>(&s.sh[r][m0 + 4 * kq]) = f16x4{h[0], h[1], h[2], h[3]};
-        *reinterpret_cast<f16x4*>(&s.sl[r][m0 + 4 * kq]) = f16x4{l[0], l[1], l[2], l[3]};
+        const float x[4] = {st[j][0], st[j][1], st[j][2], st[j][3]};
+        store_pair4(&s.sh[r][m0 + 4 * kq], &s.sl[r][m0 + 4 * kq], x);
       }
     }
   };
@@ -601,48 +705,78 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
     const int t0 = c * C, nval = min(C, rs.T - t0);
-    if (c + 1 < nch) nx.load(p, tid, (slot0 + c + 1) * p.H + hi, qg, kg, vg, t0 + C, min(C, rs.T - t0 - C));
+    // the next chunk's record and rows (the last chunk's again at the end:
+    // every load is then consumed by the staging below, on every path)
+    const int cn = min(c + 1, nch - 1);
+    nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, vg, cn * C, min(C, rs.T - cn * C));
+    // K S (waves 0-3) or Q S (waves 4-7) for rows um0 ..
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    {
+      const f16(*const a)[K + HP] = upper ? s.k : s.q;
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 af = frag8(&a[um0 + r][kb + 8 * kq]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8(&s.sh[r][kb + 8 * kq]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8(&s.sl[r][kb + 8 * kq]), acc, 0, 0, 0);
+      }
+    }
     if (upper) {
-      // u = T diag(beta) V - W S for rows um0 ..
-      f32x4 aw = {0.f, 0.f, 0.f, 0.f};
+      // Y = V - diag(gam) K S, rows um0 + 4 kq + i, column r, as Y^T pairs
+      const int t = um0 + 4 * kq;
+      const f16x4 vv = *reinterpret_cast<const f16x4*>(&s.vt[r][t]);
+      float y[4];
 #pragma unroll
-      for (int jb = 0; jb < C; jb += 32) {
-        const f16x8 b = frag8(&s.vt[r][jb + 8 * kq]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.th[um0 + r][jb + 8 * kq]), b, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][jb + 8 * kq]), b, acc, 0, 0, 0);
-      }
+      for (int i = 0; i < 4; ++i) y[i] = (float)vv[i] - s.gv[0][t + i] * acc[i];
+      store_pair4(&s.yh[r][t], &s.yl[r][t], y);
+    }
+    __syncthreads();
+    if (upper) {
+      // u = T diag(beta) Y for rows um0 .. (T lower triangular: the 32-blocks
+      // of columns below um0 + 16)
+      f32x4 au = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 wh = frag8(&s.wh[um0 + r][kb + 8 * kq]), sh = frag8(&s.sh[r][kb + 8 * kq]);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, sh, aw, 0, 0, 0);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, frag8(&s.sl[r][kb + 8 * kq]), aw, 0, 0, 0);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.wl[um0 + r][kb + 8 * kq]), sh, aw, 0, 0, 0);
-      }
+      for (int jb = 0; jb < C; jb += 32)
+        if (jb < um0 + 16) {
+          const f16x8 th = frag8(&s.th[um0 + r][jb + 8 * kq]), yh = frag8(&s.yh[r][jb + 8 * kq]);
+          au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, yh, au, 0, 0, 0);
+          au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8(&s.yl[r][jb + 8 * kq]), au, 0, 0, 0);
+          au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][jb + 8 * kq]), yh, au, 0, 0, 0);
+        }
       // u^T and (diag(D) u)^T as fp16 pairs: lane holds u rows um0 + 4 kq + i, column r
-      f16 uh[4], ul[4], dh[4], dl[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float u = acc[i] - aw[i];
-        split_f16(u, uh[i], ul[i]);
-        split_f16(s.D[um0 + 4 * kq + i] * u, dh[i], dl[i]);
-      }
-      *reinterpret_cast<f16x4*>(&s.uh[r][um0 + 4 * kq]) = f16x4{uh[0], uh[1], uh[2], uh[3]};
-      *reinterpret_cast<f16x4*>(&s.ul[r][um0 + 4 * kq]) = f16x4{ul[0], ul[1], ul[2], ul[3]};
-      *reinterpret_cast<f16x4*>(&s.dh[r][um0 + 4 * kq]) = f16x4{dh[0], dh[1], dh[2], dh[3]};
-      *reinterpret_cast<f16x4*>(&s.dl[r][um0 + 4 * kq]) = f16x4{dl[0], dl[1], dl[2], dl[3]};
+      const int t = um0 + 4 * kq;
+      const float u[4] = {au[0], au[1], au[2], au[3]};
+      const float du[4] = {s.gv[1][t] * au[0], s.gv[1][t + 1] * au[1], s.gv[1][t + 2] * au[2], s.gv[1][t + 3] * au[3]};
+      store_pair4(&s.uh[r][t], &s.ul[r][t], u);
+      store_pair4(&s.dh[r][t], &s.dl[r][t], du);
     } else {
-      // Q S for rows um0 .. (q exact in fp16)
+      // P = M o (Q K^T) by tiles of P^T = K Q^T (lane: P[16 tt + r][16 jt +
+      // 4 kq + i]): the 10 tiles on or below the diagonal and the two zero
+      // tiles above it that the 32-wide products with u read, three per wave.
+      // The mask is e^{b_t - b_j}, with e^{-inf} = 0 above the diagonal.
 #pragma unroll
-      for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 a = frag8(&s.q[um0 + r][kb + 8 * kq]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, frag8(&s.sh[r][kb + 8 * kq]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, frag8(&s.sl[r][kb + 8 * kq]), acc, 0, 0, 0);
+      for (int it = 0; it < 3; ++it) {
+        const int job = wave - 4 + 4 * it;
+        const int tt = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
+        const int jt = job < 4 ? job & 1 : (job - 4) % 4;
+        f32x4 ap = {0.f, 0.f, 0.f, 0.f};
+        if (jt <= tt) {
+#pragma unroll
+          for (int kb = 0; kb < K; kb += 32)
+            ap = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * jt + r][kb + 8 * kq]),
+                                                        frag8(&s.q[16 * tt + r][kb + 8 * kq]), ap, 0, 0, 0);
+        }
+        const int t = 16 * tt + r, j = 16 * jt + 4 * kq;
+        const float bt = s.gv[2][t];
+        const f32x4 bj = *reinterpret_cast<const f32x4*>(&s.gv[2][j]);
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] = expf(j + i <= t ? bt - bj[i] : -__builtin_huge_valf()) * ap[i];
+        store_pair4(&s.ph[t][j], &s.pl[t][j], pv);
       }
     }
     __syncthreads();
     if (upper) {
-      // S <- gam_C S + K^T diag(D) u (k exact in fp16)
+      // S <- gam_C S + K^T diag(D) u (K^T read transposed from k)
 #pragma unroll
       for (int j = 0; j < NST; ++j) {
         const int m0 = 16 * (wave + 4 * j);
@@ -650,12 +784,12 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
           f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int tb = 0; tb < C; tb += 32) {
-            const f16x8 kt = frag8(&s.kt[m0 + r][tb + 8 * kq]);
+            const f16x8 kt = frag8_t(s.k, tb, m0, r, kq);
             a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][tb + 8 * kq]), a, 0, 0, 0);
             a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][tb + 8 * kq]), a, 0, 0, 0);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) st[j][i] = s.gC * st[j][i] + a[i];
+          for (int i = 0; i < 4; ++i) st[j][i] = s.gv[3][0] * st[j][i] + a[i];
         }
       }
       put_state();
@@ -663,25 +797,24 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       // o = scale (P u + diag(gam) Q S)
       f32x4 ao = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jb = 0; jb < C; jb += 32) {
-        const f16x8 ph = frag8(&s.ph[um0 + r][jb + 8 * kq]), uh = frag8(&s.uh[r][jb + 8 * kq]);
-        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, uh, ao, 0, 0, 0);
-        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
-        ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.pl[um0 + r][jb + 8 * kq]), uh, ao, 0, 0, 0);
-      }
+      for (int jb = 0; jb < C; jb += 32)
+        if (jb < um0 + 16) {
+          const f16x8 ph = frag8(&s.ph[um0 + r][jb + 8 * kq]), uh = frag8(&s.uh[r][jb + 8 * kq]);
+          ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, uh, ao, 0, 0, 0);
+          ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
+          ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.pl[um0 + r][jb + 8 * kq]), uh, ao, 0, 0, 0);
+        }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = um0 + 4 * kq + i;
         if (row < nval)
           store_scalar(p.o, ob + (int64_t)(t0 + row) * p.so[1] + r, p.o_dtype,
-                       scale * (ao[i] + s.gam[row] * acc[i]));
+                       scale * (ao[i] + s.gv[0][row] * acc[i]));
       }
     }
     __syncthreads();
-    if (c + 1 < nch) {
-      nx.store(s, tid);
-      __syncthreads();
-    }
+    nx.store(s, tid);
+    __syncthreads();
   }
   if (upper) {
 #pragma unroll
@@ -698,11 +831,13 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 
 template <typename TIn, int K>
 int launch_k(const FArgs& a, int64_t nrec, hipStream_t s) {
-  if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NT), 0, s, a);
-  if constexpr (std::is_same<TIn, float>::value)
+  if constexpr (std::is_same<TIn, float>::value) {
+    if (nrec > 0) hipLaunchKernelGGL((prep_kernel<K>), dim3((unsigned)nrec), dim3(NT), 0, s, a);
     hipLaunchKernelGGL((scan_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
-  else
+  } else {
+    if (nrec > 0) hipLaunchKernelGGL((prep16_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NT), 0, s, a);
     hipLaunchKernelGGL((scan16_kernel<TIn, K>), dim3(a.units), dim3(NT), 0, s, a);
+  }
   return (int)hipGetLastError();
 }
 
@@ -721,10 +856,10 @@ inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 }  // namespace c64
 
 // Chunk slots x heads x record size, in bytes.
-int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq) {
+int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype) {
   const int64_t nch = (T + c64::C - 1) / c64::C;
   const int64_t nslot = n_seq > 0 ? nch + n_seq : (int64_t)B * nch;
-  return c64::align256(nslot * H * c64::rec_size(K) * 4);
+  return c64::align256(nslot * H * c64::rec_floats(K, qkv_dtype != GDN_DTYPE_F32) * 4);
 }
 
 bool c64_supported(int K, int C, int V) { return C == c64::C && (K == 32 || K == 64 || K == 128) && V % 16 == 0; }

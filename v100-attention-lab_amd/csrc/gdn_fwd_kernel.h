@@ -774,7 +774,7 @@ int launch_pipe_bf16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
 // 64-row chunks with K in {32, 64, 128} run as two launches (gdn_fwd_c64.hip)
 // over a caller-owned workspace of per-chunk records.
 bool c64_supported(int K, int C, int V);
-int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq);
+int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype);
 int c64_launch(const GdnFwdParams& P, hipStream_t stream);
 
 }  // namespace gdn
