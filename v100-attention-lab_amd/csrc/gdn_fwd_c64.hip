@@ -751,26 +751,34 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
     } else {
       // P = M o (Q K^T) by tiles of P^T = K Q^T (lane: P[16 tt + r][16 jt +
       // 4 kq + i]): the 10 tiles on or below the diagonal and the two zero
-      // tiles above it that the 32-wide products with u read, three per wave.
-      // The mask is e^{b_t - b_j}, with e^{-inf} = 0 above the diagonal.
+      // tiles above it that the 32-wide products with u read, three per wave,
+      // their products interleaved.  The mask is 2^{(b_t - b_j) log2 e} on
+      // v_exp_f32 (about 1e-6 relative), with 2^{-inf} = 0 above the diagonal.
+      f32x4 ap[3];
+      int tt[3], jt[3];
 #pragma unroll
       for (int it = 0; it < 3; ++it) {
         const int job = wave - 4 + 4 * it;
-        const int tt = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
-        const int jt = job < 4 ? job & 1 : (job - 4) % 4;
-        f32x4 ap = {0.f, 0.f, 0.f, 0.f};
-        if (jt <= tt) {
+        tt[it] = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
+        jt[it] = job < 4 ? job & 1 : (job - 4) % 4;
+        ap[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-          for (int kb = 0; kb < K; kb += 32)
-            ap = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * jt + r][kb + 8 * kq]),
-                                                        frag8(&s.q[16 * tt + r][kb + 8 * kq]), ap, 0, 0, 0);
-        }
-        const int t = 16 * tt + r, j = 16 * jt + 4 * kq;
+      for (int kb = 0; kb < K; kb += 32)
+#pragma unroll
+        for (int it = 0; it < 3; ++it)
+          ap[it] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * jt[it] + r][kb + 8 * kq]),
+                                                          frag8(&s.q[16 * tt[it] + r][kb + 8 * kq]), ap[it], 0, 0, 0);
+#pragma unroll
+      for (int it = 0; it < 3; ++it) {
+        const int t = 16 * tt[it] + r, j = 16 * jt[it] + 4 * kq;
         const float bt = s.gv[2][t];
         const f32x4 bj = *reinterpret_cast<const f32x4*>(&s.gv[2][j]);
         float pv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pv[i] = expf(j + i <= t ? bt - bj[i] : -__builtin_huge_valf()) * ap[i];
+        for (int i = 0; i < 4; ++i)
+          pv[i] = __builtin_amdgcn_exp2f(j + i <= t ? (bt - bj[i]) * 1.44269504f : -__builtin_huge_valf()) *
+                  ap[it][i];
         store_pair4(&s.ph[t][j], &s.pl[t][j], pv);
       }
     }
