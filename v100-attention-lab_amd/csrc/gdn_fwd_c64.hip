@@ -412,6 +412,19 @@ __device__ __forceinline__ f16x8 frag8_t(const f16 (*k)[LD], int t0, int m0, int
   return u.f;
 }
 
+// o[base + i * rs] = v[i] for the i < lim of 4 consecutive rows.
+template <typename TOut>
+__device__ __forceinline__ void store_o4(void* o, int64_t base, int64_t rs, int lim, const float (&v)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < lim) {
+      if constexpr (std::is_same<TOut, f16>::value) static_cast<f16*>(o)[base + i * rs] = (f16)v[i];
+      else if constexpr (std::is_same<TOut, bf16_t>::value) static_cast<uint16_t*>(o)[base + i * rs] = float_to_bf16_bits(v[i]);
+      else static_cast<float*>(o)[base + i * rs] = v[i];
+    }
+  }
+}
+
 __device__ __forceinline__ void store_pair4(f16* hi, f16* lo, const float (&x)[4]) {
   f16 h[4], l[4];
 #pragma unroll
@@ -812,13 +825,14 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
           ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
           ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.pl[um0 + r][jb + 8 * kq]), uh, ao, 0, 0, 0);
         }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = um0 + 4 * kq + i;
-        if (row < nval)
-          store_scalar(p.o, ob + (int64_t)(t0 + row) * p.so[1] + r, p.o_dtype,
-                       scale * (ao[i] + s.gv[0][row] * acc[i]));
-      }
+      const int row0 = um0 + 4 * kq;
+      const f32x4 gm = *reinterpret_cast<const f32x4*>(&s.gv[0][row0]);
+      const float ov[4] = {scale * (ao[0] + gm[0] * acc[0]), scale * (ao[1] + gm[1] * acc[1]),
+                           scale * (ao[2] + gm[2] * acc[2]), scale * (ao[3] + gm[3] * acc[3])};
+      const int64_t base = ob + (int64_t)(t0 + row0) * p.so[1] + r;
+      if (p.o_dtype == GDN_DTYPE_F16) store_o4<f16>(p.o, base, p.so[1], nval - row0, ov);
+      else if (p.o_dtype == GDN_DTYPE_BF16) store_o4<bf16_t>(p.o, base, p.so[1], nval - row0, ov);
+      else store_o4<float>(p.o, base, p.so[1], nval - row0, ov);
     }
     __syncthreads();
     nx.store(s, tid);
