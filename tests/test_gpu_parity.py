@@ -205,6 +205,49 @@ def test_t_zero_returns_h0(pkg, cuda):
 # 64-row chunks: the two-launch path (per-chunk record, then the scan)
 # --------------------------------------------------------------------------
 
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+def test_c64_unaligned_output_rows(pkg, cuda, odt):
+    """Through the C ABI: o rows that cannot take 4-element vector stores (base
+    one element off, odd row pitch) are written element by element, with the
+    same values as an aligned o; the pad column and the leading element stay
+    untouched."""
+    import ctypes
+    L = pkg._lib
+    lib = L.load_library()
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+    B, T, H, K, V = 1, 150, 2, 64, 32
+    q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=13, dtype=torch.float16)
+    dq, dk, dv, dg, db = (t.to(cuda) for t in (q, k, v, g, beta))
+    o_ref, fs_ref = pkg.gdn_fwd(dq, dk, dv, dg, db, chunk_size=64, output_dtype=odt)
+    pitch = V + 1
+    obuf = torch.full((1 + B * T * H * pitch,), float("nan"), dtype=odt, device=cuda)
+    fs = torch.empty(B, H, K, V, dtype=torch.float32, device=cuda)
+    P = L.GdnFwdParams()
+    P.q, P.k, P.v, P.g, P.beta = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), db.data_ptr()
+    P.o = obuf.data_ptr() + obuf.element_size()
+    P.final_state = fs.data_ptr()
+    P.q_stride[:] = dq.stride()[:3]
+    P.k_stride[:] = dk.stride()[:3]
+    P.v_stride[:] = dv.stride()[:3]
+    P.g_stride[:] = dg.stride()
+    P.beta_stride[:] = db.stride()
+    P.o_stride[:] = (T * H * pitch, H * pitch, pitch)
+    P.fs_stride[:] = fs.stride()
+    P.B, P.T, P.H, P.K, P.V = B, T, H, K, V
+    P.scale, P.chunk_size, P.block_v = 1.0, 64, 0
+    P.qkv_dtype, P.g_dtype, P.beta_dtype, P.o_dtype = 1, code[g.dtype], code[beta.dtype], code[odt]
+    n = lib.gdn_fwd_workspace_size(ctypes.byref(P))
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=cuda)
+    P.workspace, P.workspace_bytes = ws.data_ptr(), n
+    rc = lib.gdn_fwd_launch(ctypes.byref(P), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    rows = obuf[1:].view(B, T, H, pitch)
+    assert torch.equal(rows[..., :V].cpu(), o_ref.cpu())
+    assert torch.equal(fs.cpu(), fs_ref.cpu())
+    assert torch.isnan(obuf[0].float()) and torch.isnan(rows[..., V].float()).all()
+
+
 @pytest.mark.parametrize("K,V,T", [(32, 48, 200), (64, 64, 129), (128, 48, 64), (128, 128, 333)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_c64_two_launch(pkg, cuda, dtype, K, V, T):

@@ -57,6 +57,7 @@ struct FArgs {
   int g_dtype, beta_dtype, o_dtype;
   const int64_t* cu;
   int xcd_remap;
+  int o_vec;  // o rows take 4-element vector stores (base and strides aligned)
 };
 
 // Per-(slot, head) record for fp32 inputs, in floats: T and P as [C][C], W
@@ -425,6 +426,20 @@ __device__ __forceinline__ void store_o4(void* o, int64_t base, int64_t rs, int 
   }
 }
 
+// 4 consecutive elements of o at o + off (aligned for the vector store).
+template <typename TOut>
+__device__ __forceinline__ void store_o_vec4(void* o, int64_t off, const f32x4& v) {
+  if constexpr (std::is_same<TOut, f16>::value) {
+    *reinterpret_cast<f16x4*>(static_cast<f16*>(o) + off) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+  } else if constexpr (std::is_same<TOut, bf16_t>::value) {
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(o) + off) =
+        uint2{float_to_bf16_bits(v[0]) | ((uint32_t)float_to_bf16_bits(v[1]) << 16),
+              float_to_bf16_bits(v[2]) | ((uint32_t)float_to_bf16_bits(v[3]) << 16)};
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = v;
+  }
+}
+
 __device__ __forceinline__ void store_pair4(f16* hi, f16* lo, const float (&x)[4]) {
   f16 h[4], l[4];
 #pragma unroll
@@ -625,6 +640,7 @@ struct alignas(16) S16mem {
   // gam, D, b, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
   float gv[NT / C][C];
+  float ot[4][16][BV + 4];  // o rows of waves 4-7, for vector stores
 };
 
 // Next chunk's record and rows, in registers.
@@ -767,7 +783,7 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       // tiles above it that the 32-wide products with u read, three per wave,
       // their products interleaved.  The mask is 2^{(b_t - b_j) log2 e} on
       // v_exp_f32 (about 1e-6 relative), with 2^{-inf} = 0 above the diagonal.
-      f32x4 ap[3];
+      f32x4 ap[3], mk[3];
       int tt[3], jt[3];
 #pragma unroll
       for (int it = 0; it < 3; ++it) {
@@ -775,6 +791,16 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
         tt[it] = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
         jt[it] = job < 4 ? job & 1 : (job - 4) % 4;
         ap[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      // the mask first: its LDS reads and exponentials overlap the products
+#pragma unroll
+      for (int it = 0; it < 3; ++it) {
+        const int t = 16 * tt[it] + r, j = 16 * jt[it] + 4 * kq;
+        const float bt = s.gv[2][t];
+        const f32x4 bj = *reinterpret_cast<const f32x4*>(&s.gv[2][j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          mk[it][i] = __builtin_amdgcn_exp2f(j + i <= t ? (bt - bj[i]) * 1.44269504f : -__builtin_huge_valf());
       }
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32)
@@ -785,13 +811,8 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 #pragma unroll
       for (int it = 0; it < 3; ++it) {
         const int t = 16 * tt[it] + r, j = 16 * jt[it] + 4 * kq;
-        const float bt = s.gv[2][t];
-        const f32x4 bj = *reinterpret_cast<const f32x4*>(&s.gv[2][j]);
-        float pv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pv[i] = __builtin_amdgcn_exp2f(j + i <= t ? (bt - bj[i]) * 1.44269504f : -__builtin_huge_valf()) *
-                  ap[it][i];
+        const float pv[4] = {mk[it][0] * ap[it][0], mk[it][1] * ap[it][1], mk[it][2] * ap[it][2],
+                             mk[it][3] * ap[it][3]};
         store_pair4(&s.ph[t][j], &s.pl[t][j], pv);
       }
     }
@@ -829,10 +850,25 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       const f32x4 gm = *reinterpret_cast<const f32x4*>(&s.gv[0][row0]);
       const float ov[4] = {scale * (ao[0] + gm[0] * acc[0]), scale * (ao[1] + gm[1] * acc[1]),
                            scale * (ao[2] + gm[2] * acc[2]), scale * (ao[3] + gm[3] * acc[3])};
-      const int64_t base = ob + (int64_t)(t0 + row0) * p.so[1] + r;
-      if (p.o_dtype == GDN_DTYPE_F16) store_o4<f16>(p.o, base, p.so[1], nval - row0, ov);
-      else if (p.o_dtype == GDN_DTYPE_BF16) store_o4<bf16_t>(p.o, base, p.so[1], nval - row0, ov);
-      else store_o4<float>(p.o, base, p.so[1], nval - row0, ov);
+      if (p.o_vec) {
+        // through this wave's LDS tile: lane -> row lane / 4, columns 4 (lane % 4) ..
+        float(*const ot)[BV + 4] = s.ot[wave - 4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ot[4 * kq + i][r] = ov[i];
+        const int rr = lane >> 2, c4 = 4 * (lane & 3);
+        const f32x4 w = *reinterpret_cast<const f32x4*>(&ot[rr][c4]);
+        if (um0 + rr < nval) {
+          const int64_t off = ob + (int64_t)(t0 + um0 + rr) * p.so[1] + c4;
+          if (p.o_dtype == GDN_DTYPE_F16) store_o_vec4<f16>(p.o, off, w);
+          else if (p.o_dtype == GDN_DTYPE_BF16) store_o_vec4<bf16_t>(p.o, off, w);
+          else store_o_vec4<float>(p.o, off, w);
+        }
+      } else {
+        const int64_t base = ob + (int64_t)(t0 + row0) * p.so[1] + r;
+        if (p.o_dtype == GDN_DTYPE_F16) store_o4<f16>(p.o, base, p.so[1], nval - row0, ov);
+        else if (p.o_dtype == GDN_DTYPE_BF16) store_o4<bf16_t>(p.o, base, p.so[1], nval - row0, ov);
+        else store_o4<float>(p.o, base, p.so[1], nval - row0, ov);
+      }
     }
     __syncthreads();
     nx.store(s, tid);
@@ -906,6 +942,12 @@ int c64_launch(const GdnFwdParams& P, hipStream_t stream) {
   a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.o_dtype = P.o_dtype;
   a.cu = P.cu_seqlens;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+  {
+    const int64_t vb = 4 * (P.o_dtype == GDN_DTYPE_F32 ? 4 : 2);  // bytes of a 4-element store
+    const int64_t eb = vb / 4;
+    a.o_vec = reinterpret_cast<uintptr_t>(P.o) % vb == 0 && (P.o_stride[0] * eb) % vb == 0 &&
+              (P.o_stride[1] * eb) % vb == 0 && (P.o_stride[2] * eb) % vb == 0;
+  }
   const int64_t nslot = n_seq > 0 ? a.nchmax + n_seq : (int64_t)P.B * a.nchmax;
   const int64_t nrec = P.T > 0 ? nslot * P.H : 0;
   if (nrec > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
