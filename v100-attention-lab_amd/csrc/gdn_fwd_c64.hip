@@ -109,32 +109,34 @@ __device__ __forceinline__ void chunk_gates(int tid, const float* gl, float* b, 
   }
 }
 
-// T = (I + A)^-1 for a strictly lower 64 x 64 A (a barrier passed since A
-// was written): T11 = (I + A11)^-1 (lanes 0-31 of wave 0) and T22 =
-// (I + A22)^-1 (lanes 0-31 of wave 1), one column per lane held in
-// registers, T12 = 0; then X = A21 T11 (x: 32 x 32 scratch) and
+// T = (I + A)^-1 for a strictly lower 64 x 64 A, given as at = A^T (a
+// barrier passed since it was written): T11 = (I + A11)^-1 (lanes 0-31 of
+// wave 0) and T22 = (I + A22)^-1 (lanes 0-31 of wave 1), one column per lane
+// held in registers, T12 = 0; then X = A21 T11 (x: 32 x 32 scratch) and
 // T21 = -T22 X on the matrix cores.  Ends with a barrier.
 template <int XLD>
-__device__ __forceinline__ void solve_t(int tid, float (*a)[C + PAD], float (*t)[C + PAD], float (*x)[XLD]) {
+__device__ __forceinline__ void solve_t(int tid, float (*at)[C + PAD], float (*t)[C + PAD], float (*x)[XLD]) {
   if ((tid & 63) < 32 && tid < 128) {
     const int o = tid < 64 ? 0 : 32, cc = tid & 31;
-    float col[32];
+    // right-looking substitution: once v[j] is final it is subtracted from
+    // every row below (row i still sums its terms in the order j = 0, 1, ..,
+    // but the dependent chain is 32 steps long, not 496)
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+#pragma unroll
+      for (int i = j + 1; i < 32; ++i) v[i] = __builtin_fmaf(-at[o + j][o + i], v[j], v[i]);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      float v = (i == cc) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) v = __builtin_fmaf(-a[o + i][o + j], col[j], v);
-      col[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      t[o + i][o + cc] = col[i];
+      t[o + i][o + cc] = v[i];
       t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21 overwritten below)
     }
   }
   __syncthreads();
   mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { x[m][n] = v; },
-                       seg<32>([&](int m, int kk) { return a[32 + m][kk]; }, [&](int kk, int n) { return t[kk][n]; }));
+                       seg<32>([&](int m, int kk) { return at[kk][32 + m]; }, [&](int kk, int n) { return t[kk][n]; }));
   __syncthreads();
   mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { t[32 + m][n] = -v; },
                        seg<32>([&](int m, int kk) { return t[32 + m][32 + kk]; },
@@ -145,7 +147,7 @@ __device__ __forceinline__ void solve_t(int tid, float (*a)[C + PAD], float (*t)
 template <int K>
 struct alignas(16) PSmem {
   float q[C][K + PAD], k[C][K + PAD];
-  float a[C][C + PAD];   // K K^T, then A
+  float a[C][C + PAD];   // (K K^T)^T, then A^T
   float qk[C][C + PAD];  // Q K^T, then A21 T11
   float t[C][C + PAD];
   float gl[C], bt[C], b[C], gam[C], D[C];
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
   }
   __syncthreads();
   chunk_gates(tid, s.gl, s.b, s.gam, s.D, s.gC);
-  mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.a[m][n] = x; },
+  mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.a[n][m] = x; },
                      seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
   mmx<NT, C, C, UNR>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
                      seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
     const int t = e / C, j = e % C;
     const float mv = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
     rec[R::PM + e] = mv * s.qk[t][j];
-    s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
+    s.a[j][t] = j < t ? s.bt[t] * mv * s.a[j][t] : 0.f;  // A^T
   }
   if (tid < C) {
     rec[R::G + tid] = s.gam[tid];
@@ -544,16 +546,18 @@ struct VPairs {
 
 template <int K>
 struct alignas(16) P16mem {
-  f16 k[C][K + HP];
-  float a[C][C + PAD];    // K K^T, then A
+  union {
+    f16 k[C][K + HP];  // until K K^T is formed
+    float t[C][C + PAD];
+  };
+  float a[C][C + PAD];    // K K^T (upper tiles), then A^T
   float x[32][32 + PAD];  // A21 T11
-  float t[C][C + PAD];
   float gl[C], bt[C], b[C], gam[C], D[C];
   float gC;
 };
 
-// 16-bit inputs: record T diag(beta) and the gates.  58 KB of LDS at
-// K = 128, so two workgroups share a CU.
+// 16-bit inputs: record T diag(beta) and the gates.  41 KB of LDS at
+// K = 128 (k and T share their rows), so three workgroups share a CU.
 template <typename TIn, int K>
 __global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
   __shared__ P16mem<K> s;
@@ -585,7 +589,8 @@ __global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
   chunk_gates(tid, s.gl, s.b, s.gam, s.D, s.gC);
   {
     // K K^T on the 10 tiles on or below the diagonal (exact products, fp32
-    // accumulation); the tiles above are masked out below
+    // accumulation), each stored transposed, i.e. into the tiles on or above
+    // it (K K^T is symmetric): a lane's 4 rows become 4 consecutive columns
     const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
     for (int job = tid >> 6; job < 10; job += NT / 64) {
       const int mt = job < 1 ? 0 : job < 3 ? 1 : job < 6 ? 2 : 3;
@@ -595,16 +600,15 @@ __global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
       for (int kb = 0; kb < K; kb += 32)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * mt + r][kb + 8 * kq]),
                                                      frag8(&s.k[16 * nt + r][kb + 8 * kq]), acc, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s.a[16 * mt + 4 * kq + i][16 * nt + r] = acc[i];
+      *reinterpret_cast<f32x4*>(&s.a[16 * nt + r][16 * mt + 4 * kq]) = acc;
     }
   }
   __syncthreads();
-  // A = tril_-1(beta_t M K K^T)
+  // A^T, A = tril_-1(beta_t M K K^T) (consecutive lanes along a row of A^T)
   for (int e = tid; e < C * C; e += NT) {
-    const int t = e / C, j = e % C;
+    const int j = e / C, t = e % C;
     const float mv = expf(j < t ? s.b[t] - s.b[j] : 0.f);
-    s.a[t][j] = j < t ? s.bt[t] * mv * s.a[t][j] : 0.f;
+    s.a[j][t] = j < t ? s.bt[t] * mv * s.a[j][t] : 0.f;
   }
   if (tid < C) {
     float* const gr = rec + Rec16::GF;
