@@ -98,8 +98,8 @@ def _params(L, **kw):
 def test_fwd_workspace_size(lib, pkg):
     """Fused kernels need no workspace; 64-row chunks with K <= 128 take one
     record per (chunk slot, head).  fp32 inputs: T and P (C x C), W (C x K)
-    in fp32, then three gate rows.  16-bit inputs: T diag(beta) (C x C) as
-    an fp16 hi/lo pair, then four fp32 gate rows."""
+    in fp32, then three gate rows.  16-bit inputs: T diag(beta) and P (C x C)
+    as fp16 hi/lo pairs, then four fp32 gate rows."""
     L = pkg._lib
     size = lambda **kw: lib.gdn_fwd_workspace_size(ctypes.byref(_params(L, **kw)))
     assert size() == 0                                   # C = 32: pipelined, none
@@ -107,7 +107,7 @@ def test_fwd_workspace_size(lib, pkg):
     assert size(chunk_size=64, flags=1) == 0             # phased forced, none
     C, K, H = 64, 128, 16
     rec32 = 4 * (2 * C * C + C * K + 3 * C)
-    rec16 = 2 * 2 * C * C + 4 * 4 * C
+    rec16 = 2 * 4 * C * C + 4 * 4 * C
     for dt, rec in ((0, rec32), (1, rec16), (2, rec16)):
         want = 2 * (4096 // C) * H * rec
         assert want <= size(chunk_size=64, qkv_dtype=dt) < want + 256

@@ -17,11 +17,11 @@
 //   2. scan, one workgroup per (sequence, head, 16-column V slice): walks
 //      the chunks with S on chip (no chunk state is written), loading the
 //      next chunk's record and rows while the current one computes.
-// fp32 inputs (prep_kernel, scan_kernel: fp32 MFMA) also keep W and P in
-// the record.  16-bit inputs (prep16_kernel, scan16_kernel: fp16 MFMA on hi
-// + lo pairs) keep only T diag(beta) and the gates there; the scan forms
-// K S, u, P and o from the q, k, v rows it loads anyway, and reads 57 KB
-// per chunk and V slice instead of 98 KB (K = 128).
+// fp32 inputs (prep_kernel, scan_kernel: fp32 MFMA) keep T, P and W in the
+// record.  16-bit inputs (prep16_kernel, scan16_kernel: fp16 MFMA on hi + lo
+// pairs) keep T diag(beta), P and the gates there; the scan forms K S, u and
+// o from the q, k, v rows it loads anyway, and reads 73 KB per chunk and V
+// slice instead of 98 KB with W (K = 128).
 // Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
 // onwards, as in the backward.
 
@@ -68,13 +68,13 @@ struct Rec {
   static constexpr int G = W + C * K;
   static constexpr int SIZE = G + 3 * C;
 };
-// The record for 16-bit inputs: T diag(beta) as an fp16 pair hi + lo (x =
-// hi + lo to about 2^-22 relative; offsets TH, TL in halves), then gam, D
-// and b as [C] floats each and gam_C (first of a [C] row; offset GF in
-// floats).
+// The record for 16-bit inputs: T diag(beta) and P as fp16 pairs hi + lo
+// (x = hi + lo to about 2^-22 relative; offsets TH, TL, PH, PL in halves),
+// then gam, D and b as [C] floats each and gam_C (first of a [C] row;
+// offset GF in floats).
 struct Rec16 {
-  static constexpr int TH = 0, TL = C * C;
-  static constexpr int GF = C * C;
+  static constexpr int TH = 0, TL = C * C, PH = 2 * C * C, PL = 3 * C * C;
+  static constexpr int GF = 2 * C * C;
   static constexpr int SIZE = GF + 4 * C;
 };
 // floats per record (fp32 or 16-bit inputs)
@@ -556,10 +556,10 @@ struct alignas(16) P16mem {
   float gC;
 };
 
-// 16-bit inputs: record T diag(beta) and the gates.  41 KB of LDS at
-// K = 128 (k and T share their rows), so three workgroups share a CU.
+// 16-bit inputs: record T diag(beta), P and the gates.  41 KB of LDS at
+// K = 128 (k and T share their rows), so four workgroups share a CU.
 template <typename TIn, int K>
-__global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(K == 64 ? 6 : 8))) void prep16_kernel(const FArgs p) {
   __shared__ P16mem<K> s;
   const int tid = threadIdx.x;
   const int64_t slot = blockIdx.x / p.H;
@@ -610,6 +610,42 @@ __global__ __launch_bounds__(NT) void prep16_kernel(const FArgs p) {
     const float mv = expf(j < t ? s.b[t] - s.b[j] : 0.f);
     s.a[j][t] = j < t ? s.bt[t] * mv * s.a[j][t] : 0.f;
   }
+  {
+    // P = M o (Q K^T) as fp16 pairs, by tiles of P^T = K Q^T (lane: P[16 tt
+    // + r][16 jt + 4 kq + i]): the 10 tiles on or below the diagonal and the
+    // two zero tiles above it that the scan's 32-wide products read.  The Q
+    // fragments come straight from global memory (rows >= nval read row
+    // nval - 1 and are zeroed); the mask is 2^{(b_t - b_j) log2 e} on
+    // v_exp_f32 (about 1e-6 relative), 2^{-inf} = 0 above the diagonal.
+    const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
+    const TIn* const qb = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1];
+    for (int job = tid >> 6; job < 12; job += NT / 64) {
+      const int tt = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
+      const int jt = job < 4 ? job & 1 : (job - 4) % 4;
+      const int t = 16 * tt + r, j = 16 * jt + 4 * kq;
+      const TIn* const qr = qb + (int64_t)min(t, nval - 1) * p.sq[1] + 8 * kq;
+      uint4 qv[K / 32];
+#pragma unroll
+      for (int kb = 0; kb < K / 32; ++kb) qv[kb] = *reinterpret_cast<const uint4*>(qr + 32 * kb);
+      f32x4 ap = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K / 32; ++kb) {
+        f16 x[8];
+        InTraits<TIn>::to_op(qv[kb], x);
+        const f16x8 qf = t < nval ? f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]} : f16x8{};
+        ap = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * jt + r][32 * kb + 8 * kq]), qf, ap, 0, 0, 0);
+      }
+      const float bt = s.b[t];
+      f16 h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        split_f16(__builtin_amdgcn_exp2f(j + i <= t ? (bt - s.b[j + i]) * 1.44269504f : -__builtin_huge_valf()) *
+                      ap[i],
+                  h[i], l[i]);
+      *reinterpret_cast<f16x4*>(rh + Rec16::PH + t * C + j) = f16x4{h[0], h[1], h[2], h[3]};
+      *reinterpret_cast<f16x4*>(rh + Rec16::PL + t * C + j) = f16x4{l[0], l[1], l[2], l[3]};
+    }
+  }
   if (tid < C) {
     float* const gr = rec + Rec16::GF;
     gr[tid] = s.gam[tid];
@@ -650,7 +686,7 @@ struct alignas(16) S16mem {
 // Next chunk's record and rows, in registers.
 template <typename TIn, int K>
 struct Next16 {
-  HalfRows<C, C> th, tl;
+  HalfRows<C, C> th, tl, ph, pl;
   InRows<TIn, C, K> q, k;
   VPairs<TIn> v;
   float gate;
@@ -660,6 +696,8 @@ struct Next16 {
     const f16* const rh = reinterpret_cast<const f16*>(rec);
     th.load(tid, rh + Rec16::TH, C);
     tl.load(tid, rh + Rec16::TL, C);
+    ph.load(tid, rh + Rec16::PH, C);
+    pl.load(tid, rh + Rec16::PL, C);
     q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
     k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
     v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
@@ -668,6 +706,8 @@ struct Next16 {
   __device__ __forceinline__ void store(S16mem<K>& s, int tid) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
+    ph.store(tid, s.ph);
+    pl.store(tid, s.pl);
     q.store(tid, s.q);
     k.store(tid, s.k);
     v.store(tid, s.vt);
@@ -676,9 +716,9 @@ struct Next16 {
 };
 
 // Per chunk: (A) K S on waves 0-3 and Q S on waves 4-7 (rows 16 (w & 3) ..),
-// then Y = V - diag(gam) K S; (A2) u = T diag(beta) Y on waves 0-3 while
-// waves 4-7 form P; (B) the state update on waves 0-3 while waves 4-7 write
-// o; then the next chunk's rows are staged.  The fp32 state S lives in the
+// then Y = V - diag(gam) K S; (A2) u = T diag(beta) Y on waves 0-3; (B) the
+// state update on waves 0-3 while waves 4-7 write o; then the next chunk's
+// record and rows are staged.  The fp32 state S lives in the
 // accumulators of waves 0-3 (rows 16 (w + 4 j) of K); its hi / lo copies
 // in LDS feed K S and Q S.
 template <typename TIn, int K>
@@ -781,44 +821,6 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       const float du[4] = {s.gv[1][t] * au[0], s.gv[1][t + 1] * au[1], s.gv[1][t + 2] * au[2], s.gv[1][t + 3] * au[3]};
       store_pair4(&s.uh[r][t], &s.ul[r][t], u);
       store_pair4(&s.dh[r][t], &s.dl[r][t], du);
-    } else {
-      // P = M o (Q K^T) by tiles of P^T = K Q^T (lane: P[16 tt + r][16 jt +
-      // 4 kq + i]): the 10 tiles on or below the diagonal and the two zero
-      // tiles above it that the 32-wide products with u read, three per wave,
-      // their products interleaved.  The mask is 2^{(b_t - b_j) log2 e} on
-      // v_exp_f32 (about 1e-6 relative), with 2^{-inf} = 0 above the diagonal.
-      f32x4 ap[3], mk[3];
-      int tt[3], jt[3];
-#pragma unroll
-      for (int it = 0; it < 3; ++it) {
-        const int job = wave - 4 + 4 * it;
-        tt[it] = job < 4 ? job >> 1 : 2 + (job - 4) / 4;
-        jt[it] = job < 4 ? job & 1 : (job - 4) % 4;
-        ap[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      // the mask first: its LDS reads and exponentials overlap the products
-#pragma unroll
-      for (int it = 0; it < 3; ++it) {
-        const int t = 16 * tt[it] + r, j = 16 * jt[it] + 4 * kq;
-        const float bt = s.gv[2][t];
-        const f32x4 bj = *reinterpret_cast<const f32x4*>(&s.gv[2][j]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          mk[it][i] = __builtin_amdgcn_exp2f(j + i <= t ? (bt - bj[i]) * 1.44269504f : -__builtin_huge_valf());
-      }
-#pragma unroll
-      for (int kb = 0; kb < K; kb += 32)
-#pragma unroll
-        for (int it = 0; it < 3; ++it)
-          ap[it] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.k[16 * jt[it] + r][kb + 8 * kq]),
-                                                          frag8(&s.q[16 * tt[it] + r][kb + 8 * kq]), ap[it], 0, 0, 0);
-#pragma unroll
-      for (int it = 0; it < 3; ++it) {
-        const int t = 16 * tt[it] + r, j = 16 * jt[it] + 4 * kq;
-        const float pv[4] = {mk[it][0] * ap[it][0], mk[it][1] * ap[it][1], mk[it][2] * ap[it][2],
-                             mk[it][3] * ap[it][3]};
-        store_pair4(&s.ph[t][j], &s.pl[t][j], pv);
-      }
     }
     __syncthreads();
     if (upper) {
