@@ -20,8 +20,8 @@
 // fp32 inputs (prep_kernel, scan_kernel: fp32 MFMA) keep T, P and W in the
 // record.  16-bit inputs (prep16_kernel, scan16_kernel: fp16 MFMA on hi + lo
 // pairs) keep T diag(beta), P and the gates there; the scan forms K S, u and
-// o from the q, k, v rows it loads anyway, and reads 73 KB per chunk and V
-// slice instead of 98 KB with W (K = 128).
+// o from the q, k, v rows it loads anyway, and reads 67 KB per chunk and V
+// slice (K = 128; 98 KB with W in the record).
 // Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
 // onwards, as in the backward.
 
