@@ -442,6 +442,7 @@ __device__ __forceinline__ void store_o_vec4(void* o, int64_t off, const f32x4& 
   }
 }
 
+// 4 consecutive values as fp16 pairs: hi[0..3] and lo[0..3].
 __device__ __forceinline__ void store_pair4(f16* hi, f16* lo, const float (&x)[4]) {
   f16 h[4], l[4];
 #pragma unroll
