@@ -280,12 +280,13 @@ __device__ __forceinline__ void solve_rows(const float* at, int c, float (&xc)[C
       for (int q4 = (i - 1) / 4; q4 < C / 4; ++q4)
         r2[q4] = *reinterpret_cast<const f32x4*>(at + (i - 2) * C + 4 * q4);
     }
+    // oldest terms first: only the last product waits for xc[i + 1]
     float a0 = (c == i) ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-    for (int q4 = (i + 1) / 4; q4 < C / 4; ++q4) {
+    for (int q4 = C / 4 - 1; q4 >= (i + 1) / 4; --q4) {
       float& acc = (q4 & 1) ? a1 : a0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int e = 3; e >= 0; --e)
         if (4 * q4 + e > i) acc = fmaf(-r0[q4][e], xc[4 * q4 + e], acc);
     }
     xc[i] = a0 + a1;
@@ -314,12 +315,13 @@ __device__ __forceinline__ void solve_rows1(const float* at, int c, float (&xc)[
       for (int q4 = i / 4; q4 < C / 4; ++q4)
         nxt[q4] = *reinterpret_cast<const f32x4*>(at + (i - 1) * C + 4 * q4);
     }
+    // oldest terms first: only the last product waits for xc[i + 1]
     float a0 = (c == i) ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-    for (int q4 = (i + 1) / 4; q4 < C / 4; ++q4) {
+    for (int q4 = C / 4 - 1; q4 >= (i + 1) / 4; --q4) {
       float& acc = (q4 & 1) ? a1 : a0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int e = 3; e >= 0; --e)
         if (4 * q4 + e > i) acc = fmaf(-cur[q4][e], xc[4 * q4 + e], acc);
     }
     xc[i] = a0 + a1;
