@@ -69,17 +69,19 @@ def test_bwd_fp32_vs_autograd(pkg, cuda, T, K, V, gate):
     _compare(got, want, torch.float32, f"fp32 T={T} K={K} V={V}")
 
 
+@pytest.mark.parametrize("T,K,V", [(200, 128, 32), (77, 64, 48), (33, 32, 16)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_bwd_lowp_vs_autograd(pkg, cuda, dtype):
-    B, T, H, K, V = 1, 200, 3, 128, 32
+def test_bwd_lowp_vs_autograd(pkg, cuda, dtype, T, K, V):
+    """16-bit q, k, v and dO: the recurrences run on fp16 hi / lo pairs."""
+    B, H = 1, 3
     q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=5)
     d = lambda t: t.to(cuda)
-    print(f"[bwd] {dtype}", flush=True)
+    print(f"[bwd] {dtype} T={T} K={K} V={V}", flush=True)
     got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=1.0)
     torch.cuda.synchronize()
     assert got[0].dtype == dtype and got[2].dtype == dtype and got[3].dtype == torch.float32
     want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin)
-    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, str(dtype))
+    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, f"{dtype} K={K} V={V}")
 
 
 def test_autograd_through_gdn_fwd(pkg, cuda):
@@ -117,18 +119,19 @@ def test_autograd_through_gdn_fwd(pkg, cuda):
     _compare(got3, want3, torch.float16, "head_first")
 
 
-def test_bwd_varlen_equals_separate_runs(pkg, cuda):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_bwd_varlen_equals_separate_runs(pkg, cuda, dtype):
     lens = [40, 0, 1, 64, 75]
     H, K, V = 2, 64, 32
     T = sum(lens)
-    q, k, v, g, beta, _, do, _ = _inputs(1, T, H, K, V, torch.float32, seed=12)
+    q, k, v, g, beta, _, do, _ = _inputs(1, T, H, K, V, dtype, seed=12)
     n = len(lens)
     gen = torch.Generator().manual_seed(13)
     h0 = 0.1 * torch.randn(n, H, K, V, generator=gen)
     dfin = torch.randn(n, H, K, V, generator=gen)
     cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int64)
     d = lambda t: t.to(cuda)
-    print(f"[bwd] varlen {lens}", flush=True)
+    print(f"[bwd] varlen {lens} {dtype}", flush=True)
     got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=0.9,
                       cu_seqlens=d(cu))
     torch.cuda.synchronize()

@@ -43,7 +43,7 @@
 // i onwards, one per chunk; the ranges are disjoint, so every launch handles
 // packed sequences like a batch.
 
-#include "gdn_tiles_f32.h"
+#include "gdn_tiles_f16.h"
 
 namespace gdn {
 namespace bwd {
@@ -75,6 +75,8 @@ struct BArgs {
   float* ckD;  // per (slot, head): dS', the gradient of the state after the chunk, [K][V]
   float* uu;   // per (slot, head): u, [C][V]
   float* du;   // per (slot, head): du, [C][V]
+  f16* r16;    // per (slot, head): T diag(beta), P and W as fp16 pairs (16-bit walks)
+  int w16;     // the recurrences run on fp16 pairs (16-bit q, k, v and dO)
   int64_t sq[3], sk[3], sv[3], sg[3], sb[3], sdo[3], sdq[3], sdk[3], sdv[3], sdg[3], sdb[3];
   int64_t sh0[4], sdfs[4], sdh0[4];
   int B, T, H, V, nv, nchmax, units;
@@ -93,6 +95,15 @@ struct Rec {
   static constexpr int SIZE = G + 4 * C;
 };
 inline int64_t rec_size(int K) { return 3 * C * C + (int64_t)C * K + 4 * C; }
+// The same chunk's operands of the 16-bit recurrences, in halves: T diag(beta)
+// and P as [C][C], W as [C][K], each an fp16 pair hi + lo.
+template <int K>
+struct Rec16 {
+  static constexpr int TBH = 0, TBL = C * C, PH = 2 * C * C, PL = 3 * C * C;
+  static constexpr int WH = 4 * C * C, WL = 4 * C * C + C * K;
+  static constexpr int SIZE = 4 * C * C + 2 * C * K;
+};
+inline int64_t rec16_size(int K) { return 4 * C * C + 2 * (int64_t)C * K; }
 
 // ---------------------------------------------------------------------------
 // 1. prep: the state-independent half of a chunk's forward
@@ -118,6 +129,7 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
   if (!slot_chunk<C>(p, slot, rs, c)) return;
   const int t0 = c * C, nval = min(C, rs.T - t0);
   float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
+  f16* const rh = p.r16 + (slot * p.H + hi) * (int64_t)Rec16<K>::SIZE;
 
   {
     RowLoad<TIn, C, K, NTP> lq, lk;
@@ -158,6 +170,7 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     s.a[t][j] = j < t ? s.bt[t] * mv * s.kk[t][j] : 0.f;
     rec[R::PM + e] = mv * s.qk[t][j];
     rec[R::KK + e] = s.kk[t][j];
+    if (p.w16) tiles16::split_f16(mv * s.qk[t][j], rh[Rec16<K>::PH + e], rh[Rec16<K>::PL + e]);
   }
   if (tid < C) {
     rec[R::G + tid] = s.b[tid];
@@ -184,9 +197,36 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     }
   }
   __syncthreads();
-  mmx<NTP, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
+  // the 16-bit recurrences' operands: W as fp16 pairs staged in q's rows (q
+  // is no longer read), T diag(beta) written 4 entries per lane
+  f16(*const wst)[K] = reinterpret_cast<f16(*)[K]>(&s.q[0][0]);
+  static_assert(2 * C * K * sizeof(f16) <= sizeof(s.q), "W pairs fit in q's rows");
+  if (p.w16) {
+    static_assert(C * C == 4 * NTP, "4 entries of T per lane");
+    const int t = tid / (C / 4), j0 = 4 * (tid % (C / 4));
+    f16 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tiles16::split_f16(s.t[t][j0 + i] * s.bt[j0 + i], h[i], l[i]);
+    *reinterpret_cast<f16x4*>(rh + Rec16<K>::TBH + t * C + j0) = f16x4{h[0], h[1], h[2], h[3]};
+    *reinterpret_cast<f16x4*>(rh + Rec16<K>::TBL + t * C + j0) = f16x4{l[0], l[1], l[2], l[3]};
+  }
+  mmx<NTP, C, K>(tid,
+                 [&](int m, int n, float x) {
+                   rec[R::W + m * K + n] = x;
+                   if (p.w16) tiles16::split_f16(x, wst[m][n], wst[C + m][n]);
+                 },
                  seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                         [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
+  if (p.w16) {
+    __syncthreads();
+    // rows 0 .. C-1 of wst are W hi, rows C .. 2C-1 W lo: WH and WL are
+    // adjacent in the record, so this is one contiguous copy
+    static_assert(Rec16<K>::WL == Rec16<K>::WH + C * K, "W pairs adjacent");
+    constexpr int NV = 2 * C * K / 8;
+#pragma unroll
+    for (int e = tid; e < NV; e += NTP)
+      *reinterpret_cast<u32x4*>(rh + Rec16<K>::WH + 8 * e) = *reinterpret_cast<const u32x4*>(&wst[0][0] + 8 * e);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -504,6 +544,345 @@ __global__ __launch_bounds__(NTP) void recur_kernel(const BArgs p) {
   const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
   if (backward) walk_backward<TIn, K>(p, sm.r, rs, bi, hi, vs * BV, slot0);
   else walk_forward<TIn, K>(p, sm.f, rs, bi, hi, vs * BV, slot0);
+}
+
+// ---------------------------------------------------------------------------
+// 2b. the two recurrences for 16-bit q, k, v and dO: fp16 MFMA on hi + lo
+//     operand pairs (v_mfma_f32_16x16x32_f16, lane layout in
+//     gdn_tiles_f16.h).  The carried state (S or dS) lives in fp32 in the
+//     accumulators of the four waves (rows 16 (w + 4 j) of K); an fp16 hi /
+//     lo copy of its transpose in LDS feeds the products through it.  K^T,
+//     Q^T, P^T and W^T are read from row-major LDS copies by transposing
+//     reads.  Per chunk: the u (du) tiles on waves 0-1, then the state
+//     update on all four waves, then the next chunk's inputs are staged.
+// ---------------------------------------------------------------------------
+
+namespace w16 {
+
+using tiles16::HP;
+using tiles16::frag8;
+using tiles16::frag8_t;
+using tiles16::store_pair4;
+
+template <int K>
+struct alignas(16) FMem {
+  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
+  f16 wh[C][K + HP], wl[C][K + HP];    // W
+  f16 k[C][K + HP];
+  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
+  f16 vt[BV][C + HP];                  // V^T of the slice
+  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
+  // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
+  // (rows 4 .. 7 repeat them)
+  float gv[NTP / C][C];
+};
+
+template <int K>
+struct alignas(16) RMem {
+  f16 sh[BV][K + HP], sl[BV][K + HP];  // dS'^T
+  f16 q[C][K + HP], k[C][K + HP];
+  f16 wh[C][K + HP], wl[C][K + HP];    // W
+  f16 ph[C][C + HP], pl[C][C + HP];    // P
+  f16 dot[BV][C + HP];                 // dO^T of the slice
+  f16 gh[BV][C + HP], gl[BV][C + HP];  // (diag(gam) dO)^T
+  f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
+  float gv[NTP / C][C];
+};
+
+template <int K>
+union Mem {
+  FMem<K> f;
+  RMem<K> r;
+};
+
+// The state block of this wave (accumulator layout) <-> fp32 rows of a
+// [K][V] array, and its S^T hi / lo copy in LDS.
+template <int K>
+struct State {
+  static constexpr int NST = (K / 16 + 3) / 4;
+  f32x4 st[NST];
+  __device__ __forceinline__ void load(const float* src, const int64_t (&sd)[4], int bi, int hi, int v0, int wave,
+                                       int r, int kq) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st[j][i] = (src && m0 < K) ? src[bi * sd[0] + hi * sd[1] + (m0 + 4 * kq + i) * sd[2] + (v0 + r) * sd[3]] : 0.f;
+    }
+  }
+  __device__ __forceinline__ void store_rows(float* dst, int64_t ld, int wave, int r, int kq) const {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(int64_t)(m0 + 4 * kq + i) * ld + r] = st[j][i];
+      }
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void put(f16 (*sh)[LD], f16 (*sl)[LD], int wave, int r, int kq) const {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+        const float x[4] = {st[j][0], st[j][1], st[j][2], st[j][3]};
+        store_pair4(&sh[r][m0 + 4 * kq], &sl[r][m0 + 4 * kq], x);
+      }
+    }
+  }
+};
+
+// Next chunk's inputs of the forward walk, in registers.
+template <typename TIn, int K>
+struct FNext16 {
+  tiles16::HalfRows<C, C, NTP> th, tl;
+  tiles16::HalfRows<C, K, NTP> wh, wl;
+  tiles16::InRows<TIn, C, K, NTP> k;
+  tiles16::SlicePairs<TIn, C, BV, NTP> v;
+  float gate;
+  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* kg, const TIn* vg, int t0,
+                                       int nval) {
+    using R16 = Rec16<K>;
+    const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
+    th.load(tid, rh + R16::TBH, C);
+    tl.load(tid, rh + R16::TBL, C);
+    wh.load(tid, rh + R16::WH, K);
+    wl.load(tid, rh + R16::WL, K);
+    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
+    gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
+  }
+  __device__ __forceinline__ void store(FMem<K>& s, int tid) const {
+    th.store(tid, s.th);
+    tl.store(tid, s.tl);
+    wh.store(tid, s.wh);
+    wl.store(tid, s.wl);
+    k.store(tid, s.k);
+    v.store(tid, s.vt);
+    s.gv[tid / C][tid % C] = gate;
+  }
+};
+
+// Forward walk: S at each chunk start -> ckS, u -> uu.
+template <typename TIn, int K>
+__device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const RowSpan& rs, int bi, int hi,
+                                               int v0, int64_t slot0) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int nch = (rs.T + C - 1) / C;
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  State<K> S;
+  S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq);
+  S.put(s.sh, s.sl, wave, r, kq);
+  FNext16<TIn, K> nx;
+  if (nch > 0) {
+    nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
+    nx.store(s, tid);
+  }
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int64_t ri = (slot0 + c) * p.H + hi;
+    // the next chunk's inputs (the last chunk's again at the end: every load
+    // is then consumed by the staging below, on every path)
+    const int cn = min(c + 1, nch - 1);
+    nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
+    S.store_rows(p.ckS + ri * (int64_t)K * p.V + v0, p.V, wave, r, kq);
+    if (wave < 2) {
+      // u = T diag(beta) V - W S, rows 16 w ..
+      const int um0 = 16 * wave;
+      f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
+      const f16x8 vb = frag8(&s.vt[r][8 * kq]);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.th[um0 + r][8 * kq]), vb, au, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][8 * kq]), vb, au, 0, 0, 0);
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 wf = frag8(&s.wh[um0 + r][kb + 8 * kq]), sf = frag8(&s.sh[r][kb + 8 * kq]);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, sf, aw, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, frag8(&s.sl[r][kb + 8 * kq]), aw, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.wl[um0 + r][kb + 8 * kq]), sf, aw, 0, 0, 0);
+      }
+      const int t = um0 + 4 * kq;
+      float u[4], du[4];
+      float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u[i] = au[i] - aw[i];
+        du[i] = s.gv[2][t + i] * u[i];
+        uo[(int64_t)(t + i) * p.V + r] = u[i];
+      }
+      store_pair4(&s.dh[r][t], &s.dl[r][t], du);
+    }
+    __syncthreads();
+    // S <- gam_C S + K^T diag(D) u
+#pragma unroll
+    for (int j = 0; j < State<K>::NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+        const f16x8 kt = frag8_t(s.k, 0, m0, r, kq);
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][8 * kq]), a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][8 * kq]), a, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S.st[j][i] = s.gv[3][0] * S.st[j][i] + a[i];
+      }
+    }
+    S.put(s.sh, s.sl, wave, r, kq);
+    __syncthreads();
+    nx.store(s, tid);
+    __syncthreads();
+  }
+}
+
+// Next chunk's inputs of the backward walk, in registers.
+template <typename TIn, int K>
+struct RNext16 {
+  tiles16::HalfRows<C, C, NTP> ph, pl;
+  tiles16::HalfRows<C, K, NTP> wh, wl;
+  tiles16::InRows<TIn, C, K, NTP> q, k;
+  tiles16::SlicePairs<TIn, C, BV, NTP> d;
+  float gate;
+  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
+                                       const TIn* dg, int t0, int nval) {
+    using R16 = Rec16<K>;
+    const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
+    ph.load(tid, rh + R16::PH, C);
+    pl.load(tid, rh + R16::PL, C);
+    wh.load(tid, rh + R16::WH, K);
+    wl.load(tid, rh + R16::WL, K);
+    q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
+    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
+    d.load(tid, dg + (int64_t)t0 * p.sdo[1], p.sdo[1], nval);
+    gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
+  }
+  __device__ __forceinline__ void store(RMem<K>& s, int tid) const {
+    ph.store(tid, s.ph);
+    pl.store(tid, s.pl);
+    wh.store(tid, s.wh);
+    wl.store(tid, s.wl);
+    q.store(tid, s.q);
+    k.store(tid, s.k);
+    d.store(tid, s.dot);
+    s.gv[tid / C][tid % C] = gate;
+  }
+};
+
+// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.
+template <typename TIn, int K>
+__device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, const RowSpan& rs, int bi, int hi,
+                                                int v0, int64_t slot0) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int nch = (rs.T + C - 1) / C;
+  const float scale = p.scale;
+  const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
+  const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
+  const TIn* const dg = static_cast<const TIn*>(p.d_o) + head_base(rs, hi, p.sdo) + v0;
+  State<K> S;
+  S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq);
+  S.put(s.sh, s.sl, wave, r, kq);
+  RNext16<TIn, K> nx;
+  if (nch > 0) {
+    const int t0 = (nch - 1) * C;
+    nx.load(p, tid, (slot0 + nch - 1) * p.H + hi, qg, kg, dg, t0, rs.T - t0);
+    nx.store(s, tid);
+  }
+  __syncthreads();
+  for (int c = nch - 1; c >= 0; --c) {
+    const int64_t ri = (slot0 + c) * p.H + hi;
+    // the previous chunk's inputs (chunk 0's again at the end)
+    const int cn = max(c - 1, 0);
+    nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
+    S.store_rows(p.ckD + ri * (int64_t)K * p.V + v0, p.V, wave, r, kq);
+    if (wave < 2) {
+      // du = scale P^T dO + diag(D) K dS', rows 16 w ..
+      const int um0 = 16 * wave;
+      f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+      const f16x8 df = frag8(&s.dot[r][8 * kq]);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(s.ph, 0, um0, r, kq), df, a1, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(s.pl, 0, um0, r, kq), df, a1, 0, 0, 0);
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 kf = frag8(&s.k[um0 + r][kb + 8 * kq]);
+        a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), a2, 0, 0, 0);
+        a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), a2, 0, 0, 0);
+      }
+      const int t = um0 + 4 * kq;
+      float du[4];
+      float* const duo = p.du + ri * (int64_t)C * p.V + v0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        du[i] = scale * a1[i] + s.gv[2][t + i] * a2[i];
+        duo[(int64_t)(t + i) * p.V + r] = du[i];
+      }
+      store_pair4(&s.uh[r][t], &s.ul[r][t], du);
+    } else {
+      // (diag(gam) dO)^T as pairs: lane -> column tid % 16, rows 4 (tid / 16) ..
+      const int l = tid - 128, col = l & 15, t4 = 4 * (l >> 4);
+      const f16x4 dv = *reinterpret_cast<const f16x4*>(&s.dot[col][t4]);
+      const float x[4] = {s.gv[1][t4] * (float)dv[0], s.gv[1][t4 + 1] * (float)dv[1],
+                          s.gv[1][t4 + 2] * (float)dv[2], s.gv[1][t4 + 3] * (float)dv[3]};
+      store_pair4(&s.gh[col][t4], &s.gl[col][t4], x);
+    }
+    __syncthreads();
+    // dS <- scale Q^T diag(gam) dO + gam_C dS' - W^T du
+#pragma unroll
+    for (int j = 0; j < State<K>::NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+        const f16x8 qt = frag8_t(s.q, 0, m0, r, kq);
+        const f16x8 wth = frag8_t(s.wh, 0, m0, r, kq), wtl = frag8_t(s.wl, 0, m0, r, kq);
+        const f16x8 uh = frag8(&s.uh[r][8 * kq]);
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gh[r][8 * kq]), a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gl[r][8 * kq]), a, 0, 0, 0);
+        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wth, uh, b, 0, 0, 0);
+        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wth, frag8(&s.ul[r][8 * kq]), b, 0, 0, 0);
+        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wtl, uh, b, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S.st[j][i] = scale * a[i] + s.gv[3][0] * S.st[j][i] - b[i];
+      }
+    }
+    S.put(s.sh, s.sl, wave, r, kq);
+    __syncthreads();
+    nx.store(s, tid);
+    __syncthreads();
+  }
+  if (p.dh0 != nullptr) {
+#pragma unroll
+    for (int j = 0; j < State<K>::NST; ++j) {
+      const int m0 = 16 * (wave + 4 * j);
+      if (m0 < K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p.dh0[bi * p.sdh0[0] + hi * p.sdh0[1] + (m0 + 4 * kq + i) * p.sdh0[2] + (v0 + r) * p.sdh0[3]] = S.st[j][i];
+      }
+    }
+  }
+}
+
+}  // namespace w16
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(NTP) void recur16_kernel(const BArgs p) {
+  __shared__ w16::Mem<K> sm;
+  int blk = blockIdx.x;
+  const bool backward = blk >= p.units;
+  if (backward) blk -= p.units;
+  int unit = blk;
+  if (p.xcd_remap) unit = (blk & 7) * (p.units >> 3) + (blk >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const RowSpan rs = row_span(p.cu, p.T, bi);
+  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
+  if (backward) w16::walk_backward16<TIn, K>(p, sm.r, rs, bi, hi, vs * BV, slot0);
+  else w16::walk_forward16<TIn, K>(p, sm.f, rs, bi, hi, vs * BV, slot0);
 }
 
 // ---------------------------------------------------------------------------
@@ -863,7 +1242,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 
 // Workspace layout (each part 256-byte aligned).
 struct Layout {
-  int64_t rec, ckS, ckD, uu, du, total;  // offsets in bytes
+  int64_t rec, ckS, ckD, uu, du, r16, total;  // offsets in bytes
   int64_t nslot;
 };
 
@@ -885,6 +1264,8 @@ inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
   off = align256(off + nr * C * V * 4);
   L.du = off;
   off = align256(off + nr * C * V * 4);
+  L.r16 = off;
+  off = align256(off + nr * rec16_size(K) * 2);
   L.total = off;
   return L;
 }
@@ -892,7 +1273,12 @@ inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
 template <typename TIn, int K>
 int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
   if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
-  hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
+  if constexpr (!std::is_same<TIn, float>::value) {
+    if (a.w16) hipLaunchKernelGGL((recur16_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
+    else hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
+  }
   if (nrec > 0) {
     if (a.V % 32 == 0)
       hipLaunchKernelGGL((grad_kernel<TIn, K, 32>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
@@ -967,6 +1353,7 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   a.ckD = reinterpret_cast<float*>(ws + L.ckD);
   a.uu = reinterpret_cast<float*>(ws + L.uu);
   a.du = reinterpret_cast<float*>(ws + L.du);
+  a.r16 = reinterpret_cast<f16*>(ws + L.r16);
   for (int d = 0; d < 3; ++d) {
     a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
     a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.sdo[d] = P.do_stride[d];
@@ -983,6 +1370,11 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.do_dtype = P.do_dtype;
   a.cu = P.cu_seqlens;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+  // fp16 pair recurrences: 16-bit q, k, v with dO of the same type, whose
+  // rows take 4-byte element-pair loads
+  a.w16 = P.qkv_dtype != GDN_DTYPE_F32 && P.do_dtype == P.qkv_dtype &&
+          reinterpret_cast<uintptr_t>(P.d_o) % 4 == 0 && P.do_stride[0] % 2 == 0 && P.do_stride[1] % 2 == 0 &&
+          P.do_stride[2] % 2 == 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nrec_launch = P.T > 0 ? nrec : 0;

@@ -25,12 +25,13 @@
 // Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
 // onwards, as in the backward.
 
-#include "gdn_tiles_f32.h"
+#include "gdn_tiles_f16.h"
 
 namespace gdn {
 namespace c64 {
 
 using namespace tiles;
+using namespace tiles16;
 
 constexpr int C = 64;
 constexpr int BV = 16;
@@ -80,13 +81,6 @@ struct Rec16 {
 // floats per record (fp32 or 16-bit inputs)
 constexpr int64_t rec_floats(int K, bool half) { return half ? Rec16::SIZE : 2 * C * C + (int64_t)C * K + 3 * C; }
 static_assert(Rec<128>::SIZE == rec_floats(128, false) && Rec<32>::SIZE == rec_floats(32, false), "record sizes");
-
-// x as an fp16 pair hi + lo.
-__device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
-  x = pin(x);
-  hi = (f16)x;
-  lo = (f16)(x - (float)hi);
-}
 
 // ---------------------------------------------------------------------------
 // 1. prep
@@ -389,32 +383,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
 // hi + lo, and a product of two fp32 values is hi*hi + hi*lo + lo*hi (to
 // about 2^-22 relative).
 
-constexpr int HP = 8;  // LDS row padding in halves (rows stay 16-byte aligned)
-
-__device__ __forceinline__ f16x8 frag8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
-
-// Row m0 + r of K^T, contraction indices t0 + 8 kq .. t0 + 8 kq + 7, from
-// row-major K in LDS by two ds_read_b64_tr_b16: in each group of 16 lanes,
-// lane i receives as element j halfword i % 4 of the 8 bytes addressed by
-// lane 4 j + i / 4 of the group.  Lane (r, kq) addresses
-// k[t0 + 8 kq + 4 h + r / 4][m0 + 4 (r % 4)] and so receives
-// K[t0 + 8 kq + 4 h + j][m0 + r], j = 0..3, for h = 0, 1.
-template <int LD>
-__device__ __forceinline__ f16x8 frag8_t(const f16 (*k)[LD], int t0, int m0, int r, int kq) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  const f16* const a0 = &k[t0 + 8 * kq + (r >> 2)][m0 + 4 * (r & 3)];
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0);
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0 + 4 * LD));
-  union {
-    s16x4 h[2];
-    f16x8 f;
-  } u;
-  u.h[0] = lo;
-  u.h[1] = hi;
-  return u.f;
-}
-
 // o[base + i * rs] = v[i] for the i < lim of 4 consecutive rows.
 template <typename TOut>
 __device__ __forceinline__ void store_o4(void* o, int64_t base, int64_t rs, int lim, const float (&v)[4]) {
@@ -441,109 +409,6 @@ __device__ __forceinline__ void store_o_vec4(void* o, int64_t off, const f32x4& 
     *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = v;
   }
 }
-
-// 4 consecutive values as fp16 pairs: hi[0..3] and lo[0..3].
-__device__ __forceinline__ void store_pair4(f16* hi, f16* lo, const float (&x)[4]) {
-  f16 h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) split_f16(x[i], h[i], l[i]);
-  *reinterpret_cast<f16x4*>(hi) = f16x4{h[0], h[1], h[2], h[3]};
-  *reinterpret_cast<f16x4*>(lo) = f16x4{l[0], l[1], l[2], l[3]};
-}
-
-// The loaders below load unconditionally, guarded at most by a wave-uniform
-// test (none when the vectors fill every lane): a lane-masked load, a zero
-// written into a register a load may still target, or a load that a later
-// path may leave unconsumed, makes the wave wait for every load in flight.
-
-// ROWS x COLS halves, rows `ld` halves apart in global memory -> LDS rows of
-// LD halves, 16 bytes per lane.
-template <int ROWS, int COLS>
-struct HalfRows {
-  static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
-  static_assert(NV % 64 == 0, "whole waves");
-  u32x4 r[N];
-  __device__ __forceinline__ void load(int tid, const f16* src, int64_t ld) {
-    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int e = tid + i * NT;
-      if (NV % NT == 0 || w0 + i * NT < NV) r[i] = *reinterpret_cast<const u32x4*>(src + (e / RV) * ld + (e % RV) * 8);
-    }
-  }
-  template <int LD>
-  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
-    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int e = tid + i * NT;
-      if (NV % NT == 0 || w0 + i * NT < NV) *reinterpret_cast<u32x4*>(&dst[e / RV][(e % RV) * 8]) = r[i];
-    }
-  }
-};
-
-// ROWS x COLS block of a 16-bit input, row-major, in 8-element vectors
-// (vector e: row e / RV), stored as fp16.  Rows >= nvalid (>= 1) load row
-// nvalid - 1 and are stored as zero.
-template <typename TIn, int ROWS, int COLS>
-struct InRows {
-  static constexpr int RV = COLS / 8, NV = ROWS * RV, N = (NV + NT - 1) / NT;
-  static_assert(NV % 64 == 0, "whole waves");
-  uint4 r[N];
-  int nv;
-  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid) {
-    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
-    nv = nvalid;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int e = tid + i * NT;
-      if (NV % NT == 0 || w0 + i * NT < NV)
-        r[i] = *reinterpret_cast<const uint4*>(src + min(e / RV, nvalid - 1) * ld + 8 * (e % RV));
-    }
-  }
-  template <int LD>
-  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
-    const int w0 = __builtin_amdgcn_readfirstlane(tid & ~63);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int e = tid + i * NT;
-      if (NV % NT == 0 || w0 + i * NT < NV) {
-        const bool ok = e / RV < nv;
-        const uint4 v = {ok ? r[i].x : 0u, ok ? r[i].y : 0u, ok ? r[i].z : 0u, ok ? r[i].w : 0u};
-        f16 x[8];
-        InTraits<TIn>::to_op(v, x);
-        *reinterpret_cast<f16x8*>(&dst[e / RV][8 * (e % RV)]) = f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-      }
-    }
-  }
-};
-
-// The C x BV slice of V, one pair of elements per lane (row lane / (BV / 2)),
-// stored transposed as fp16 (dst[column][row]).  Rows >= nvalid (>= 1) load
-// row nvalid - 1 and are stored as zero.
-template <typename TIn>
-struct VPairs {
-  static_assert(C * BV / 2 == NT, "one pair per lane");
-  uint32_t r;
-  int nv;
-  __device__ __forceinline__ void load(int tid, const TIn* src, int64_t ld, int nvalid) {
-    nv = nvalid;
-    r = *reinterpret_cast<const uint32_t*>(src + min(tid / (BV / 2), nvalid - 1) * ld + 2 * (tid % (BV / 2)));
-  }
-  template <int LD>
-  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
-    const int t = tid / (BV / 2), c = tid % (BV / 2);
-    const uint32_t v = t < nv ? r : 0u;
-    const uint16_t l16 = (uint16_t)(v & 0xffffu), h16 = (uint16_t)(v >> 16);
-    if constexpr (std::is_same<TIn, f16>::value) {
-      dst[2 * c][t] = __builtin_bit_cast(f16, l16);
-      dst[2 * c + 1][t] = __builtin_bit_cast(f16, h16);
-    } else {
-      dst[2 * c][t] = (f16)bf16_bits_to_float(l16);
-      dst[2 * c + 1][t] = (f16)bf16_bits_to_float(h16);
-    }
-  }
-};
 
 template <int K>
 struct alignas(16) P16mem {
@@ -573,7 +438,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(K == 64 ? 6 
   f16* const rh = reinterpret_cast<f16*>(rec);
 
   {
-    InRows<TIn, C, K> lk;
+    InRows<TIn, C, K, NT> lk;
     lk.load(tid, static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1], p.sk[1], nval);
     float gv = 0.f, bv = 0.f;
     if (tid < nval) {
@@ -687,9 +552,9 @@ struct alignas(16) S16mem {
 // Next chunk's record and rows, in registers.
 template <typename TIn, int K>
 struct Next16 {
-  HalfRows<C, C> th, tl, ph, pl;
-  InRows<TIn, C, K> q, k;
-  VPairs<TIn> v;
+  HalfRows<C, C, NT> th, tl, ph, pl;
+  InRows<TIn, C, K, NT> q, k;
+  SlicePairs<TIn, C, BV, NT> v;
   float gate;
   __device__ __forceinline__ void load(const FArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
                                        const TIn* vg, int t0, int nval) {
