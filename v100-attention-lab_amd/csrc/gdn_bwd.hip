@@ -575,6 +575,7 @@ struct alignas(16) FMem {
   // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
   float gv[NTP / C][C];
+  float s32[K][BV + 4];  // S in fp32, for 16-byte stores of its rows
 };
 
 template <int K>
@@ -587,6 +588,7 @@ struct alignas(16) RMem {
   f16 gh[BV][C + HP], gl[BV][C + HP];  // (diag(gam) dO)^T
   f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
   float gv[NTP / C][C];
+  float s32[K][BV + 4];  // dS' in fp32, for 16-byte stores of its rows
 };
 
 template <int K>
@@ -611,13 +613,15 @@ struct State {
         st[j][i] = (src && m0 < K) ? src[bi * sd[0] + hi * sd[1] + (m0 + 4 * kq + i) * sd[2] + (v0 + r) * sd[3]] : 0.f;
     }
   }
-  __device__ __forceinline__ void store_rows(float* dst, int64_t ld, int wave, int r, int kq) const {
+  // into the fp32 LDS copy (read back by copy_rows after a barrier)
+  template <int LD>
+  __device__ __forceinline__ void put32(float (*s32)[LD], int wave, int r, int kq) const {
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(int64_t)(m0 + 4 * kq + i) * ld + r] = st[j][i];
+        for (int i = 0; i < 4; ++i) s32[m0 + 4 * kq + i][r] = st[j][i];
       }
     }
   }
@@ -633,6 +637,19 @@ struct State {
     }
   }
 };
+
+// The K x BV fp32 state copy -> rows of a [K][V] array, 16 bytes per lane.
+template <int K, int LD>
+__device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, int64_t ld, int tid) {
+  constexpr int NV = K * BV / 4;
+#pragma unroll
+  for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
+    const int e = tid + i * NTP;
+    if (NV % NTP == 0 || e < NV)
+      *reinterpret_cast<f32x4*>(dst + (int64_t)(e / 4) * ld + 4 * (e % 4)) =
+          *reinterpret_cast<const f32x4*>(&s32[e / 4][4 * (e % 4)]);
+  }
+}
 
 // Next chunk's inputs of the forward walk, in registers.
 template <typename TIn, int K>
@@ -678,6 +695,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
   State<K> S;
   S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq);
   S.put(s.sh, s.sl, wave, r, kq);
+  S.put32(s.s32, wave, r, kq);
   FNext16<TIn, K> nx;
   if (nch > 0) {
     nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
@@ -690,7 +708,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     // is then consumed by the staging below, on every path)
     const int cn = min(c + 1, nch - 1);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
-    S.store_rows(p.ckS + ri * (int64_t)K * p.V + v0, p.V, wave, r, kq);
+    copy_rows<K>(s.s32, p.ckS + ri * (int64_t)K * p.V + v0, p.V, tid);
     if (wave < 2) {
       // u = T diag(beta) V - W S, rows 16 w ..
       const int um0 = 16 * wave;
@@ -731,6 +749,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
+    S.put32(s.s32, wave, r, kq);
     __syncthreads();
     nx.store(s, tid);
     __syncthreads();
@@ -785,6 +804,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
   State<K> S;
   S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq);
   S.put(s.sh, s.sl, wave, r, kq);
+  S.put32(s.s32, wave, r, kq);
   RNext16<TIn, K> nx;
   if (nch > 0) {
     const int t0 = (nch - 1) * C;
@@ -797,7 +817,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     // the previous chunk's inputs (chunk 0's again at the end)
     const int cn = max(c - 1, 0);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
-    S.store_rows(p.ckD + ri * (int64_t)K * p.V + v0, p.V, wave, r, kq);
+    copy_rows<K>(s.s32, p.ckD + ri * (int64_t)K * p.V + v0, p.V, tid);
     if (wave < 2) {
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
@@ -848,6 +868,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
+    S.put32(s.s32, wave, r, kq);
     __syncthreads();
     nx.store(s, tid);
     __syncthreads();
