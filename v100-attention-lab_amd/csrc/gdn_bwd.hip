@@ -25,15 +25,17 @@
 //
 // Only S (forward) and dS (backward) carry from chunk to chunk, and each
 // needs a few products per chunk; everything else is independent per chunk.
-// So the backward is three launches, all fp32 on the fp32 matrix cores
-// (v_mfma_f32_16x16x4_f32):
+// So the backward is three launches, on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32) except the 16-bit recurrences:
 //   1. prep_kernel, one workgroup per (chunk, head): gates, K K^T, P, T and
 //      W, written once to a per-chunk record (the state-independent half of
-//      the chunk's forward, shared by every V-slice below);
-//   2. recur_kernel, one workgroup per (sequence, head, 16-column V slice)
-//      and direction, both directions in one launch: the forward walk stores
-//      each chunk's start state S and u; the backward walk stores each
-//      chunk's dS' and du and finally dh0;
+//      the chunk's forward, shared by every V-slice below), and for 16-bit
+//      inputs T diag(beta), P and W as fp16 pairs as well;
+//   2. recur_kernel (fp32) or recur16_kernel (16-bit q, k, v, dO: fp16 MFMA
+//      on hi + lo pairs), one workgroup per (sequence, head, 16-column V
+//      slice) and direction, both directions in one launch: the forward
+//      walk stores each chunk's start state S and u; the backward walk
+//      stores each chunk's dS' and du and finally dh0;
 //   3. grad_kernel, one workgroup per (chunk, head) over all of V: every
 //      gradient of the chunk from the stored S, dS', u, du and the record,
 //      written directly in the output dtypes (V is walked in 32-column steps,
