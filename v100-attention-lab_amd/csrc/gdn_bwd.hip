@@ -161,10 +161,35 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     s.D[tid] = expf(bc - bt);
     if (tid == C - 1) s.gC = expf(bc);
   }
-  mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.kk[m][n] = x; },
-                 seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
-  mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
-                 seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  if constexpr (std::is_same<TIn, float>::value) {
+    mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.kk[m][n] = x; },
+                   seg<K>([&](int m, int kk) { return s.k[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+    mmx<NTP, C, C>(tid, [&](int m, int n, float x) { s.qk[m][n] = x; },
+                   seg<K>([&](int m, int kk) { return s.q[m][kk]; }, [&](int kk, int n) { return s.k[n][kk]; }));
+  } else {
+    // 16-bit q and k are exact in fp16: K K^T and Q K^T on
+    // v_mfma_f32_16x16x32_f16 (exact products, fp32 accumulation), the 8
+    // tiles over the 4 waves
+    const int lane = tid & 63, r = lane & 15, kq = lane >> 4;
+    auto frag = [](const float* row) __attribute__((always_inline)) {
+      f16x8 f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (f16)row[e];
+      return f;
+    };
+    for (int job = tid >> 6; job < 8; job += NTP / 64) {
+      const int mat = job >> 2, mt = (job >> 1) & 1, nt = job & 1;
+      const float* const arow = (mat ? &s.q[0][0] : &s.k[0][0]) + (16 * mt + r) * (K + 1) + 8 * kq;
+      const float* const brow = &s.k[0][0] + (16 * nt + r) * (K + 1) + 8 * kq;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag(arow + kb), frag(brow + kb), acc, 0, 0, 0);
+      float(*const dst)[C + 1] = mat ? s.qk : s.kk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[16 * mt + 4 * kq + i][16 * nt + r] = acc[i];
+    }
+  }
   __syncthreads();
   for (int e = tid; e < C * C; e += NTP) {
     const int t = e / C, j = e % C;
