@@ -111,6 +111,12 @@ def test_fwd_workspace_size(lib, pkg):
     for dt, rec in ((0, rec32), (1, rec16), (2, rec16)):
         want = 2 * (4096 // C) * H * rec
         assert want <= size(chunk_size=64, qkv_dtype=dt) < want + 256
+    # the 16-bit record does not depend on K, the fp32 one does (W is C x K)
+    for k_ in (32, 64):
+        want16 = 2 * (4096 // C) * H * rec16
+        want32 = 2 * (4096 // C) * H * 4 * (2 * C * C + C * k_ + 3 * C)
+        assert want16 <= size(chunk_size=64, K=k_) < want16 + 256
+        assert want32 <= size(chunk_size=64, K=k_, qkv_dtype=0) < want32 + 256
     # packed sequences: slots ceil(T / C) + N = 2 + 3
     got = size(chunk_size=64, B=3, T=100, cu_seqlens=0x2000)
     assert 5 * H * rec16 <= got < 5 * H * rec16 + 256
