@@ -594,10 +594,10 @@ using tiles16::store_pair4;
 template <int K>
 struct alignas(16) FMem {
   f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
-  f16 wh[C][K + HP], wl[C][K + HP];    // W
   f16 k[C][K + HP];
   f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
   f16 vt[BV][C + HP];                  // V^T of the slice
+  f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
   f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
   // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
@@ -682,7 +682,6 @@ __device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, in
 template <typename TIn, int K>
 struct FNext16 {
   tiles16::HalfRows<C, C, NTP> th, tl;
-  tiles16::HalfRows<C, K, NTP> wh, wl;
   tiles16::InRows<TIn, C, K, NTP> k;
   tiles16::SlicePairs<TIn, C, BV, NTP> v;
   float gate;
@@ -692,8 +691,6 @@ struct FNext16 {
     const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
     th.load(tid, rh + R16::TBH, C);
     tl.load(tid, rh + R16::TBL, C);
-    wh.load(tid, rh + R16::WH, K);
-    wl.load(tid, rh + R16::WL, K);
     k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
     v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
@@ -701,8 +698,6 @@ struct FNext16 {
   __device__ __forceinline__ void store(FMem<K>& s, int tid) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
-    wh.store(tid, s.wh);
-    wl.store(tid, s.wl);
     k.store(tid, s.k);
     v.store(tid, s.vt);
     s.gv[tid / C][tid % C] = gate;
@@ -737,27 +732,37 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
     copy_rows<K>(s.s32, p.ckS + ri * (int64_t)K * p.V + v0, p.V, tid);
     if (wave < 2) {
-      // u = T diag(beta) V - W S, rows 16 w ..
+      // Y = V - diag(gam) K S for rows 16 w .. (k exact in fp16), as Y^T pairs
       const int um0 = 16 * wave;
-      f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
-      const f16x8 vb = frag8(&s.vt[r][8 * kq]);
-      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.th[um0 + r][8 * kq]), vb, au, 0, 0, 0);
-      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][8 * kq]), vb, au, 0, 0, 0);
+      f32x4 ak = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 wf = frag8(&s.wh[um0 + r][kb + 8 * kq]), sf = frag8(&s.sh[r][kb + 8 * kq]);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, sf, aw, 0, 0, 0);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, frag8(&s.sl[r][kb + 8 * kq]), aw, 0, 0, 0);
-        aw = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.wl[um0 + r][kb + 8 * kq]), sf, aw, 0, 0, 0);
+        const f16x8 kf = frag8(&s.k[um0 + r][kb + 8 * kq]);
+        ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), ak, 0, 0, 0);
+        ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), ak, 0, 0, 0);
       }
       const int t = um0 + 4 * kq;
-      float u[4], du[4];
+      const f16x4 vv = *reinterpret_cast<const f16x4*>(&s.vt[r][t]);
+      const float y[4] = {(float)vv[0] - s.gv[1][t] * ak[0], (float)vv[1] - s.gv[1][t + 1] * ak[1],
+                          (float)vv[2] - s.gv[1][t + 2] * ak[2], (float)vv[3] - s.gv[1][t + 3] * ak[3]};
+      store_pair4(&s.yh[r][t], &s.yl[r][t], y);
+    }
+    __syncthreads();
+    if (wave < 2) {
+      // u = T diag(beta) Y, rows 16 w .. (W S = T diag(beta) diag(gam) K S)
+      const int um0 = 16 * wave;
+      f32x4 au = {0.f, 0.f, 0.f, 0.f};
+      const f16x8 th = frag8(&s.th[um0 + r][8 * kq]), yh = frag8(&s.yh[r][8 * kq]);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, yh, au, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8(&s.yl[r][8 * kq]), au, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][8 * kq]), yh, au, 0, 0, 0);
+      const int t = um0 + 4 * kq;
+      float du[4];
       float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        u[i] = au[i] - aw[i];
-        du[i] = s.gv[2][t + i] * u[i];
-        uo[(int64_t)(t + i) * p.V + r] = u[i];
+        du[i] = s.gv[2][t + i] * au[i];
+        uo[(int64_t)(t + i) * p.V + r] = au[i];
       }
       store_pair4(&s.dh[r][t], &s.dl[r][t], du);
     }
