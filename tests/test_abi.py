@@ -331,9 +331,9 @@ def test_fla_surface_and_prep_reject_cpu_tensors(pkg):
 def test_bwd_workspace_size(lib):
     # cfg2, per (chunk, head): the record (T, P, K K^T as C x C, W as C x K,
     # four gate rows), S and dS' (K x V), u and du (C x V), all fp32; then
-    # T diag(beta), P (C x C) and W (C x K) as fp16 pairs
+    # T diag(beta) and P (C x C) as fp16 pairs
     C, K, V, nrec = 32, 128, 128, 2 * (4096 // 32) * 16
-    want = nrec * 4 * ((3 * C * C + C * K + 4 * C) + 2 * K * V + 2 * C * V) + nrec * 2 * (4 * C * C + 2 * C * K)
+    want = nrec * 4 * ((3 * C * C + C * K + 4 * C) + 2 * K * V + 2 * C * V) + nrec * 2 * (4 * C * C)
     got = lib.gdn_bwd_workspace_size(2, 4096, 16, 128, 128, 0)
     assert want <= got <= want + 6 * 256
     assert lib.gdn_bwd_workspace_size(2, 4096, 16, 256, 128, 0) == -1

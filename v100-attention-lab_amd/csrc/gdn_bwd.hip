@@ -28,9 +28,10 @@
 // So the backward is three launches, on the fp32 matrix cores
 // (v_mfma_f32_16x16x4_f32) except the 16-bit recurrences:
 //   1. prep_kernel, one workgroup per (chunk, head): gates, K K^T, P, T and
-//      W, written once to a per-chunk record (the state-independent half of
-//      the chunk's forward, shared by every V-slice below), and for 16-bit
-//      inputs T diag(beta), P and W as fp16 pairs as well;
+//      (fp32 only) W, written once to a per-chunk record (the
+//      state-independent half of the chunk's forward, shared by every
+//      V-slice below), and for 16-bit inputs T diag(beta) and P as fp16
+//      pairs as well;
 //   2. recur_kernel (fp32) or recur16_kernel (16-bit q, k, v, dO: fp16 MFMA
 //      on hi + lo pairs), one workgroup per (sequence, head, 16-column V
 //      slice) and direction, both directions in one launch: the forward
@@ -77,7 +78,7 @@ struct BArgs {
   float* ckD;  // per (slot, head): dS', the gradient of the state after the chunk, [K][V]
   float* uu;   // per (slot, head): u, [C][V]
   float* du;   // per (slot, head): du, [C][V]
-  f16* r16;    // per (slot, head): T diag(beta), P and W as fp16 pairs (16-bit walks)
+  f16* r16;    // per (slot, head): T diag(beta) and P as fp16 pairs (16-bit walks)
   int w16;     // the recurrences run on fp16 pairs (16-bit q, k, v and dO)
   int64_t sq[3], sk[3], sv[3], sg[3], sb[3], sdo[3], sdq[3], sdk[3], sdv[3], sdg[3], sdb[3];
   int64_t sh0[4], sdfs[4], sdh0[4];
@@ -98,14 +99,12 @@ struct Rec {
 };
 inline int64_t rec_size(int K) { return 3 * C * C + (int64_t)C * K + 4 * C; }
 // The same chunk's operands of the 16-bit recurrences, in halves: T diag(beta)
-// and P as [C][C], W as [C][K], each an fp16 pair hi + lo.
-template <int K>
+// and P as [C][C], each an fp16 pair hi + lo.
 struct Rec16 {
   static constexpr int TBH = 0, TBL = C * C, PH = 2 * C * C, PL = 3 * C * C;
-  static constexpr int WH = 4 * C * C, WL = 4 * C * C + C * K;
-  static constexpr int SIZE = 4 * C * C + 2 * C * K;
+  static constexpr int SIZE = 4 * C * C;
 };
-inline int64_t rec16_size(int K) { return 4 * C * C + 2 * (int64_t)C * K; }
+inline int64_t rec16_size(int) { return 4 * C * C; }
 
 // ---------------------------------------------------------------------------
 // 1. prep: the state-independent half of a chunk's forward
@@ -131,7 +130,7 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
   if (!slot_chunk<C>(p, slot, rs, c)) return;
   const int t0 = c * C, nval = min(C, rs.T - t0);
   float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
-  f16* const rh = p.r16 + (slot * p.H + hi) * (int64_t)Rec16<K>::SIZE;
+  f16* const rh = p.r16 + (slot * p.H + hi) * (int64_t)Rec16::SIZE;
 
   {
     RowLoad<TIn, C, K, NTP> lq, lk;
@@ -197,7 +196,7 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     s.a[t][j] = j < t ? s.bt[t] * mv * s.kk[t][j] : 0.f;
     rec[R::PM + e] = mv * s.qk[t][j];
     rec[R::KK + e] = s.kk[t][j];
-    if (p.w16) tiles16::split_f16(mv * s.qk[t][j], rh[Rec16<K>::PH + e], rh[Rec16<K>::PL + e]);
+    if (p.w16) tiles16::split_f16(mv * s.qk[t][j], rh[Rec16::PH + e], rh[Rec16::PL + e]);
   }
   if (tid < C) {
     rec[R::G + tid] = s.b[tid];
@@ -224,36 +223,22 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     }
   }
   __syncthreads();
-  // the 16-bit recurrences' operands: W as fp16 pairs staged in q's rows (q
-  // is no longer read), T diag(beta) written 4 entries per lane
-  f16(*const wst)[K] = reinterpret_cast<f16(*)[K]>(&s.q[0][0]);
-  static_assert(2 * C * K * sizeof(f16) <= sizeof(s.q), "W pairs fit in q's rows");
+  // the 16-bit recurrences' operand T diag(beta) as fp16 pairs, 4 entries
+  // per lane
   if (p.w16) {
     static_assert(C * C == 4 * NTP, "4 entries of T per lane");
     const int t = tid / (C / 4), j0 = 4 * (tid % (C / 4));
     f16 h[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) tiles16::split_f16(s.t[t][j0 + i] * s.bt[j0 + i], h[i], l[i]);
-    *reinterpret_cast<f16x4*>(rh + Rec16<K>::TBH + t * C + j0) = f16x4{h[0], h[1], h[2], h[3]};
-    *reinterpret_cast<f16x4*>(rh + Rec16<K>::TBL + t * C + j0) = f16x4{l[0], l[1], l[2], l[3]};
+    *reinterpret_cast<f16x4*>(rh + Rec16::TBH + t * C + j0) = f16x4{h[0], h[1], h[2], h[3]};
+    *reinterpret_cast<f16x4*>(rh + Rec16::TBL + t * C + j0) = f16x4{l[0], l[1], l[2], l[3]};
   }
-  mmx<NTP, C, K>(tid,
-                 [&](int m, int n, float x) {
-                   rec[R::W + m * K + n] = x;
-                   if (p.w16) tiles16::split_f16(x, wst[m][n], wst[C + m][n]);
-                 },
-                 seg<C>([&](int m, int kk) { return s.t[m][kk]; },
-                        [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
-  if (p.w16) {
-    __syncthreads();
-    // rows 0 .. C-1 of wst are W hi, rows C .. 2C-1 W lo: WH and WL are
-    // adjacent in the record, so this is one contiguous copy
-    static_assert(Rec16<K>::WL == Rec16<K>::WH + C * K, "W pairs adjacent");
-    constexpr int NV = 2 * C * K / 8;
-#pragma unroll
-    for (int e = tid; e < NV; e += NTP)
-      *reinterpret_cast<u32x4*>(rh + Rec16<K>::WH + 8 * e) = *reinterpret_cast<const u32x4*>(&wst[0][0] + 8 * e);
-  }
+  // W = T diag(beta gam) K, read by the fp32 recurrences only
+  if (!p.w16)
+    mmx<NTP, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
+                   seg<C>([&](int m, int kk) { return s.t[m][kk]; },
+                          [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
 }
 
 // ---------------------------------------------------------------------------
@@ -609,11 +594,12 @@ template <int K>
 struct alignas(16) RMem {
   f16 sh[BV][K + HP], sl[BV][K + HP];  // dS'^T
   f16 q[C][K + HP], k[C][K + HP];
-  f16 wh[C][K + HP], wl[C][K + HP];    // W
+  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
   f16 ph[C][C + HP], pl[C][C + HP];    // P
   f16 dot[BV][C + HP];                 // dO^T of the slice
   f16 gh[BV][C + HP], gl[BV][C + HP];  // (diag(gam) dO)^T
   f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
+  f16 zh[BV][C + HP], zl[BV][C + HP];  // (diag(gam) (T diag(beta))^T du)^T
   float gv[NTP / C][C];
   float s32[K][BV + 4];  // dS' in fp32, for 16-byte stores of its rows
 };
@@ -687,7 +673,7 @@ struct FNext16 {
   float gate;
   __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* kg, const TIn* vg, int t0,
                                        int nval) {
-    using R16 = Rec16<K>;
+    using R16 = Rec16;
     const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
     th.load(tid, rh + R16::TBH, C);
     tl.load(tid, rh + R16::TBL, C);
@@ -791,29 +777,28 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
 // Next chunk's inputs of the backward walk, in registers.
 template <typename TIn, int K>
 struct RNext16 {
-  tiles16::HalfRows<C, C, NTP> ph, pl;
-  tiles16::HalfRows<C, K, NTP> wh, wl;
+  tiles16::HalfRows<C, C, NTP> th, tl, ph, pl;
   tiles16::InRows<TIn, C, K, NTP> q, k;
   tiles16::SlicePairs<TIn, C, BV, NTP> d;
   float gate;
   __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
                                        const TIn* dg, int t0, int nval) {
-    using R16 = Rec16<K>;
+    using R16 = Rec16;
     const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
+    th.load(tid, rh + R16::TBH, C);
+    tl.load(tid, rh + R16::TBL, C);
     ph.load(tid, rh + R16::PH, C);
     pl.load(tid, rh + R16::PL, C);
-    wh.load(tid, rh + R16::WH, K);
-    wl.load(tid, rh + R16::WL, K);
     q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
     k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
     d.load(tid, dg + (int64_t)t0 * p.sdo[1], p.sdo[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
   }
   __device__ __forceinline__ void store(RMem<K>& s, int tid) const {
+    th.store(tid, s.th);
+    tl.store(tid, s.tl);
     ph.store(tid, s.ph);
     pl.store(tid, s.pl);
-    wh.store(tid, s.wh);
-    wl.store(tid, s.wl);
     q.store(tid, s.q);
     k.store(tid, s.k);
     d.store(tid, s.dot);
@@ -881,22 +866,50 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       store_pair4(&s.gh[col][t4], &s.gl[col][t4], x);
     }
     __syncthreads();
-    // dS <- scale Q^T diag(gam) dO + gam_C dS' - W^T du
+    // W^T du = K^T diag(beta gam) T^T du = K^T (diag(gam) (T diag(beta))^T du):
+    // z on waves 0-1 (rows 16 w .. of z, T diag(beta) transposed by the
+    // reads) while waves 2-3 form their Q^T diag(gam) dO term
+    f32x4 aq[State<K>::NST];
+    auto q_term = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < State<K>::NST; ++j) {
+        const int m0 = 16 * (wave + 4 * j);
+        aq[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (m0 < K) {
+          const f16x8 qt = frag8_t(s.q, 0, m0, r, kq);
+          aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gh[r][8 * kq]), aq[j], 0, 0, 0);
+          aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gl[r][8 * kq]), aq[j], 0, 0, 0);
+        }
+      }
+    };
+    if (wave < 2) {
+      const int um0 = 16 * wave;
+      const f16x8 tth = frag8_t(s.th, 0, um0, r, kq), ttl = frag8_t(s.tl, 0, um0, r, kq);
+      const f16x8 uh = frag8(&s.uh[r][8 * kq]);
+      f32x4 az = {0.f, 0.f, 0.f, 0.f};
+      az = __builtin_amdgcn_mfma_f32_16x16x32_f16(tth, uh, az, 0, 0, 0);
+      az = __builtin_amdgcn_mfma_f32_16x16x32_f16(tth, frag8(&s.ul[r][8 * kq]), az, 0, 0, 0);
+      az = __builtin_amdgcn_mfma_f32_16x16x32_f16(ttl, uh, az, 0, 0, 0);
+      const int t = um0 + 4 * kq;
+      const float z[4] = {s.gv[1][t] * az[0], s.gv[1][t + 1] * az[1], s.gv[1][t + 2] * az[2],
+                          s.gv[1][t + 3] * az[3]};
+      store_pair4(&s.zh[r][t], &s.zl[r][t], z);
+    } else {
+      q_term();
+    }
+    __syncthreads();
+    if (wave < 2) q_term();
+    // dS <- scale Q^T diag(gam) dO + gam_C dS' - K^T z
 #pragma unroll
     for (int j = 0; j < State<K>::NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        const f16x8 qt = frag8_t(s.q, 0, m0, r, kq);
-        const f16x8 wth = frag8_t(s.wh, 0, m0, r, kq), wtl = frag8_t(s.wl, 0, m0, r, kq);
-        const f16x8 uh = frag8(&s.uh[r][8 * kq]);
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gh[r][8 * kq]), a, 0, 0, 0);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gl[r][8 * kq]), a, 0, 0, 0);
-        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wth, uh, b, 0, 0, 0);
-        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wth, frag8(&s.ul[r][8 * kq]), b, 0, 0, 0);
-        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(wtl, uh, b, 0, 0, 0);
+        const f16x8 kt = frag8_t(s.k, 0, m0, r, kq);
+        f32x4 b = {0.f, 0.f, 0.f, 0.f};
+        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zh[r][8 * kq]), b, 0, 0, 0);
+        b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zl[r][8 * kq]), b, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S.st[j][i] = scale * a[i] + s.gv[3][0] * S.st[j][i] - b[i];
+        for (int i = 0; i < 4; ++i) S.st[j][i] = scale * aq[j][i] + s.gv[3][0] * S.st[j][i] - b[i];
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
