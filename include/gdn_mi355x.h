@@ -201,7 +201,8 @@ typedef struct GdnBwdParams {
   const void* g;
   const void* beta;
   const float* h0;           /* nullable */
-  const void* d_o;           /* [B,T,H,V] */
+  const void* d_o;           /* [B,T,H,V], unit stride along V (any b/t/h
+                                strides, 0 included) */
   const float* d_final_state;/* nullable, [B,H,K,V] */
   void* dq;
   void* dk;

@@ -190,3 +190,63 @@ def test_autograd_fla_varlen_bf16(pkg, cuda):
         got = (sl(leaves[0].grad.cpu()), sl(leaves[1].grad.cpu()), sl(leaves[2].grad.cpu()),
                sl(leaves[4].grad.cpu()), sl(leaves[3].grad.cpu()), leaves[5].grad[i:i + 1].cpu())
         _compare(got, want, torch.bfloat16, f"varlen seq {i}")
+
+
+def test_autograd_sum_losses_expanded_grads(pkg, cuda):
+    """o.sum().backward() hands the backward a stride-0 expansion of one
+    element as dO (and fs.sum() one as d_final_state): the gradients equal
+    the oracle's with dO = ones (dfinal = ones).  Weak gates keep dh0 of
+    order one: under the recipe's gates a state gradient that only enters
+    through d_final_state decays by about e^-56 over 70 steps, below the
+    range of the fp16 image the recurrences carry (as the reference's own
+    fp16 cast of the state, gdn_triton.py:87)."""
+    B, T, H, K, V = 1, 70, 2, 64, 32
+    q, k, v, g, beta, h0, _, _ = _inputs(B, T, H, K, V, torch.float16, seed=31, gate=0.05)
+    ones_o = torch.ones(B, T, H, V)
+    ones_s = torch.ones(B, H, K, V)
+    for which in ("o", "fs"):
+        leaves = [t.to(cuda).requires_grad_(True) for t in (q, k, v, g, beta, h0)]
+        print(f"[bwd] {which}.sum().backward()", flush=True)
+        o, fs = pkg.gdn_fwd(*leaves, scale=0.6)
+        (o.sum() if which == "o" else fs.sum()).backward()
+        torch.cuda.synchronize()
+        if which == "o":
+            want = ref.recurrent_grads(q, k, v, beta, g, h0, ones_o, None, scale=0.6)
+        else:
+            want = ref.recurrent_grads(q, k, v, beta, g, h0, torch.zeros(B, T, H, V), ones_s,
+                                       scale=0.6)
+        got = [t.grad for t in leaves]
+        _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, torch.float16,
+                 f"{which}.sum()")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_bwd_lowp_inputs_fp32_do(pkg, cuda, dtype):
+    """16-bit q, k, v with an fp32 dO run the fp32 recurrences, which read
+    the record's fp32 W (the path taken when the forward wrote o in fp32)."""
+    B, H, T, K, V = 1, 3, 150, 128, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=41)
+    do32 = torch.randn(B, T, H, V, generator=torch.Generator().manual_seed(42))
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] {dtype} inputs, fp32 dO", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do32), d(dfin), scale=1.0)
+    torch.cuda.synchronize()
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do32, dfin)
+    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, f"{dtype} fp32 dO")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_autograd_fp32_output(pkg, cuda, dtype):
+    """loss.backward() through gdn_fwd(output_dtype=float32): dO arrives in
+    fp32 while q, k, v are 16-bit."""
+    B, T, H, K, V = 1, 100, 2, 64, 48
+    q, k, v, g, beta, h0, _, dfin = _inputs(B, T, H, K, V, dtype, seed=51)
+    do = torch.randn(B, T, H, V, generator=torch.Generator().manual_seed(52))
+    leaves = [t.to(cuda).requires_grad_(True) for t in (q, k, v, g, beta, h0)]
+    print(f"[bwd] autograd {dtype} output_dtype=float32", flush=True)
+    o, fs = pkg.gdn_fwd(*leaves, scale=0.9, output_dtype=torch.float32)
+    assert o.dtype == torch.float32
+    ((o * do.to(cuda)).sum() + (fs * dfin.to(cuda)).sum()).backward()
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=0.9)
+    got = [t.grad for t in leaves]
+    _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, f"{dtype} fp32 o")

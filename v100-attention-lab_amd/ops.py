@@ -542,6 +542,11 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         if tuple(dfinal.shape) != (B, H, K, V) or dfinal.dtype != torch.float32:
             raise ValueError(f"dfinal must be float32 [{B}, {H}, {K}, {V}]")
     _check_devices(q, k, v, g, beta, h0, do, dfinal)
+    # The kernels index dO rows by their (b, t, h) strides with a unit step
+    # along V.  autograd may hand over any layout, e.g. the stride-0 expansion
+    # of a scalar for o.sum().backward(): give the kernels a dense copy then.
+    if do.stride(-1) != 1:
+        do = do.contiguous()
     dev = q.device
     lib = _lib.load_library()
     ws_bytes = lib.gdn_bwd_workspace_size(B, T, H, K, V, n_seq or 0)
