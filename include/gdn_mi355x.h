@@ -72,7 +72,10 @@ enum GdnStatus {
 enum GdnFlags {
   /* Use the phase-by-phase kernel even where the pipelined one applies
    * (testing and comparison). */
-  GDN_FLAG_PHASED_KERNEL = 1
+  GDN_FLAG_PHASED_KERNEL = 1,
+  /* 32-row chunks: use the single fused pipelined kernel (no workspace)
+   * even when a workspace is given (testing and comparison). */
+  GDN_FLAG_FUSED_KERNEL = 2
 };
 
 typedef struct GdnFwdParams {
@@ -116,16 +119,25 @@ typedef struct GdnFwdParams {
 /* Enqueue one chunked GDN forward on `stream` (a hipStream_t; NULL = the
  * legacy default stream).  Returns a GdnStatus / hipError_t value.
  * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140).
- * C = 32 (and K = 256 or GDN_FLAG_PHASED_KERNEL) runs one fused kernel with
- * no workspace.  C = 64 with K in {32, 64, 128} runs two launches (a
- * per-chunk record, then the scan over chunks; block_v is 16 there) and
- * needs params->workspace; the state stays on chip in both. */
+ *   - C = 32, fp16 q/k/v, K in {64, 128}, with a workspace: two launches per
+ *     segment of the sequence (per-chunk records of the state-independent
+ *     work, then the scan over chunks).  The segment length is what the
+ *     workspace holds: workspace_bytes / (B * H * record bytes) chunks per
+ *     sequence (at least one), so any workspace of at least
+ *     gdn_fwd_workspace_size() bytes runs the call; a longer sequence runs
+ *     as several segments, its state passing through final_state.
+ *   - C = 32 without a workspace (or GDN_FLAG_FUSED_KERNEL), bf16, or K = 256
+ *     / GDN_FLAG_PHASED_KERNEL: one fused kernel, no workspace.
+ *   - C = 64 with K in {32, 64, 128}: two launches (a per-chunk record, then
+ *     the scan over chunks; block_v is 16 there); needs params->workspace.
+ * The state stays on chip in every path: no chunk state is written. */
 int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
 
 /* Bytes of workspace gdn_fwd_launch needs for these params (0 for the fused
- * kernels; B = the number of sequences when cu_seqlens is set); -1 if the
- * shape is invalid.  No counterpart in the reference, whose Triton launch
- * needs none. */
+ * kernels; for 32-row chunks the records of a segment of at most 256 chunks
+ * per sequence; B = the number of sequences when cu_seqlens is set); -1 if
+ * the shape is invalid.  No counterpart in the reference, whose Triton
+ * launch needs none. */
 int64_t gdn_fwd_workspace_size(const GdnFwdParams* params);
 
 /* The block_v the launcher picks when params->block_v == 0 (for logging and

@@ -18,7 +18,10 @@ pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-5
 TOL_LOWP = 1e-3
 
-KERNELS = ["auto", "phased"]
+# "auto": for fp16 at C = 32 the per-chunk records and the scan (two
+# launches), for bf16 the fused pipelined kernel; "fused": the pipelined
+# kernel for both; "phased": the phase-by-phase kernel.
+KERNELS = ["auto", "fused", "phased"]
 
 
 def _run(pkg, dev, q, k, v, g, beta, h0=None, **kw):
@@ -284,3 +287,36 @@ def test_c64_degenerate_and_agrees_with_phased(pkg, cuda):
     _report("c64 degenerate bf16", eo, eh)
     assert eo <= TOL_LOWP and eh <= TOL_LOWP
     assert ref.rel_err(o2, o) <= TOL_LOWP and ref.rel_err(fs2, fs) <= TOL_LOWP
+
+
+@pytest.mark.parametrize("T,seg", [(1000, 3), (4096, 1), (77, 2)])
+def test_segments_equal_one_pass(pkg, cuda, T, seg):
+    """The two-launch path with records for only `seg` chunks per sequence
+    runs a sequence as consecutive segments, the state passing through
+    final_state (fp32, exact): outputs are bit-equal to the one-segment run,
+    with and without h0, batched and packed."""
+    B, H, K, V = 2, 3, 128, 32
+    q, k, v, g, beta, h0 = ref.make_inputs_baseline(B, T, H, K, V, seed=7, with_h0=True)
+    d = lambda t: t.to(cuda)
+    print(f"[segments] T={T} seg={seg}", flush=True)
+    for h in (None, h0):
+        o1, f1 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h))
+        o2, f2 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h),
+                             max_segment_chunks=seg)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.cpu(), o2.cpu()) and torch.equal(f1.cpu(), f2.cpu())
+    o_ref, h_ref = _recurrent(q, k, v, g, beta, h0)
+    eo, eh = ref.rel_err(o_ref, o2.cpu().float()), ref.rel_err(h_ref, f2.cpu())
+    _report(f"segments T={T} seg={seg}", eo, eh)
+    assert eh <= TOL_LOWP and eo <= TOL_LOWP + 2.0 ** -11
+    # packed sequences of unequal lengths: sequences end in different segments
+    lens = [T // 3, 0, T - T // 3]
+    cu = torch.tensor([0, lens[0], lens[0], T], dtype=torch.int64)
+    qp, kp, vp, gp, bp = (t[:1] for t in (q, k, v, g, beta))
+    hp = 0.1 * torch.randn(3, H, K, V, generator=torch.Generator().manual_seed(8))
+    o1, f1 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu))
+    o2, f2 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu),
+                         max_segment_chunks=seg)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.cpu(), o2.cpu()) and torch.equal(f1.cpu(), f2.cpu())
+    assert torch.equal(f2[1].cpu(), hp[1])     # the empty sequence keeps its h0

@@ -27,6 +27,7 @@ GDN_ERR_WORKSPACE = 1006
 
 # enum GdnFlags
 FLAG_PHASED_KERNEL = 1
+FLAG_FUSED_KERNEL = 2
 
 # Every symbol the header declares; tests check the library exports them.
 EXPORTED_SYMBOLS = (

@@ -19,7 +19,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 # One translation unit per q/k/v dtype, the host API, the input
 # preparation and the backward, compiled in parallel.
 SOURCES = ["gdn_fwd_api.hip", "gdn_fwd_f16.hip", "gdn_fwd_bf16.hip", "gdn_fwd_f32.hip",
-           "gdn_fwd_c64.hip", "gdn_prep.hip", "gdn_bwd.hip"]
+           "gdn_fwd_c64.hip", "gdn_fwd_scan32.hip", "gdn_prep.hip", "gdn_bwd.hip"]
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
@@ -37,6 +37,14 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+
+
+# Per-source flags.  The scan kernels keep their MFMA accumulators (the
+# carried state) in arch VGPRs: with the AGPR form every iteration would copy
+# the state through v_accvgpr_read / write on its serial path.
+SOURCE_FLAGS = {
+    "gdn_fwd_scan32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:
@@ -62,8 +70,8 @@ def build(verbose: bool = True, extra_flags=None) -> str:
     objs = []
     for src in SOURCES:
         obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-        cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", "-c",
-               os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *(extra_flags or []),
+               f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print("[build]", " ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,

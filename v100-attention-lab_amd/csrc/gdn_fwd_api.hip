@@ -75,13 +75,31 @@ static bool uses_c64(const GdnFwdParams& P) {
   return !(P.flags & GDN_FLAG_PHASED_KERNEL) && c64_supported(P.K, P.chunk_size, P.V);
 }
 
+// Records of at most this many chunks per sequence are what
+// gdn_fwd_workspace_size asks for on the 32-row two-launch path.
+constexpr int64_t kSegChunks = 256;
+
+// The 32-row two-launch path (records, then the scan) for this BV, unless
+// another kernel is asked for.
+static bool uses_scan32(const GdnFwdParams& P, int bv) {
+  return !(P.flags & (GDN_FLAG_PHASED_KERNEL | GDN_FLAG_FUSED_KERNEL)) &&
+         scan32_supported(P.qkv_dtype, P.K, P.chunk_size, bv) && pipe_offsets_fit(P);
+}
+
 int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
   if (prm == nullptr) return -1;
   const GdnFwdParams& P = *prm;
   if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0) return -1;
   if (!valid_dtype(P.qkv_dtype)) return -1;
-  if (!uses_c64(P)) return 0;
-  return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
+  if (uses_c64(P)) return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
+  const int bv = P.block_v ? P.block_v : auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
+  if (bv > 0 && P.V % bv == 0 && uses_scan32(P, bv)) {
+    const int64_t nch = (P.T + 31) / 32;
+    const int64_t L = nch < kSegChunks ? nch : kSegChunks;
+    const int64_t bytes = (int64_t)P.B * P.H * L * scan32_record_bytes();
+    return (bytes + 255) / 256 * 256;
+  }
+  return 0;
 }
 
 int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
@@ -138,6 +156,13 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
 
   const int grid = (int)units;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (P.workspace != nullptr && uses_scan32(P, bv)) {
+    // segment length: as many chunks per sequence as the workspace holds
+    const int64_t per_chunk = (int64_t)P.B * P.H * scan32_record_bytes();
+    const int64_t L = P.workspace_bytes / per_chunk;
+    if (reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 || L < 1) return GDN_ERR_WORKSPACE;
+    return scan32_launch(P, bv, (int)(L < 0x7fffffff ? L : 0x7fffffff), s);
+  }
   if (!(P.flags & GDN_FLAG_PHASED_KERNEL) && pipe_supported(P.qkv_dtype, P.K, P.chunk_size, bv) &&
       pipe_offsets_fit(P)) {
     if (P.qkv_dtype == GDN_DTYPE_F16) return launch_pipe_f16(a, P.K, bv, grid, s);

@@ -776,5 +776,11 @@ int launch_pipe_bf16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
 bool c64_supported(int K, int C, int V);
 int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype);
 int c64_launch(const GdnFwdParams& P, hipStream_t stream);
+// 32-row chunks, fp16, K in {64, 128}, BV in {16, 32}: per-chunk records
+// then the scan (gdn_fwd_scan32.hip), in segments of at most seg_chunks
+// chunks per sequence whose records fit the caller's workspace.
+bool scan32_supported(int dtype, int K, int C, int BV);
+int64_t scan32_record_bytes();
+int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t stream);
 
 }  // namespace gdn

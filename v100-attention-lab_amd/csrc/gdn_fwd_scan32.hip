@@ -1,0 +1,664 @@
+// The forward for 32-row chunks as two launches: a per-chunk record of the
+// state-independent work, then a scan over the chunks that keeps the state
+// on chip (the default path for fp16 inputs, C = 32, K in {64, 128}).
+//
+// Per chunk (C = 32 rows, b = in-chunk cumsum of g, as in gdn_ref.py:51-99):
+//   A  = tril_-1(beta_t e^{b_t - b_j} K K^T),   T = (I + A)^-1,
+//   Tu = T diag(beta),
+//   u  = Tu (V - diag(e^b) K S)             (= U - W h^T, gdn_triton.py:87)
+//   o  = scale (P u + diag(e^b) Q S),  P = tril_0(e^{b_t - b_j} Q K^T)
+//   S' = e^{bC} S + K^T diag(e^{bC - b}) u  (the reference's h(e^{bC} I -
+//        Wbar^T K) + Ubar^T K, gdn_ref.py:93-98, without the K x K temporary)
+// Only u, o and S' involve the carried state.  A V-slice workgroup of the
+// fused kernel would rebuild A and rerun the 32-row substitution for T once
+// per slice; here they run once per (chunk, head):
+//
+//   1. rec32_kernel, one wave per two (chunk, head) records: K K^T on the
+//      matrix cores, A, then T by forward substitution on the VALU (one lane
+//      per row of T, rows of A^T broadcast from LDS), written with the gates
+//      to a 3 KB record: Tu as MFMA operand fragments, b, e^b, e^{bC - b},
+//      e^{bC}.
+//   2. scan32_kernel, one workgroup per (sequence, head, BV-column slice),
+//      walks the chunks with the fp32 K x BV state in accumulator registers
+//      (no chunk state is written).  Waves have fixed roles and pass one
+//      barrier per iteration:
+//        SCAN x BV/16  chunk it: K S, Y = V - diag(e^b) K S, u = Tu Y,
+//                      S <- e^{bC} S + K^T diag(e^{bC-b}) u (16 columns each)
+//        OUT  x BV/16  chunk it: Q S with the chunk-start state;
+//                      chunk it-1: o = scale (P u + diag(e^b) Q S)
+//        PQK           chunk it: P = e^{b_t-b_j} Q K^T (t >= j) as hi + lo
+//                      fp16 operand fragments
+//        LOAD          chunk it+D: q, k, the v slice and the record, copied
+//                      global -> LDS by the asynchronous LDS-DMA loads
+//                      (global_load_lds_dwordx4), D chunks ahead.
+//
+// The records of a segment of L chunks per (sequence, head) live in the
+// caller's workspace; a sequence longer than L chunks runs as several
+// (rec32, scan32) pairs, the state passing from one segment to the next
+// through final_state.  The workspace is therefore bounded by B * H * L
+// records, independent of T.
+//
+// MFMA operand layouts, the state's key order and the transposing LDS reads
+// are those of gdn_fwd_pipe.h (v_mfma_f32_16x16x32_f16; pi(g, s) pairing
+// of accumulator rows and contraction slots).
+
+#include "gdn_fwd_pipe.h"
+
+namespace gdn {
+namespace s32 {
+
+using namespace pipe;
+
+constexpr int C = 32;
+constexpr int D = 4;  // chunks loaded ahead by the LOAD wave
+constexpr int REC_BYTES = 3072;
+// record layout (byte offsets)
+constexpr int R_TU = 0;     // f16x8 [2][64]: Tu rows 16 mt + (lane & 15), columns pi(lane >> 4, s)
+constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b (flat past the sequence end)
+constexpr int R_EB = 2176;  // float [32]: e^b
+constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
+constexpr int R_EBC = 2432; // float: e^{bC}
+
+struct SArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;
+  void* o;
+  float* fs;
+  char* rec;
+  int64_t sq[3], sk[3], sv[3], sg[3], sb[3], so[3];
+  int64_t sh0[4], sfs[4];
+  int B, T, H, V, nv;  // B: sequences (units of row_span)
+  int c0, L;           // this segment: chunks [c0, c0 + L) of every sequence
+  int first;           // initial state from h0 (or zero) rather than final_state
+  int nrec;            // B * H * L
+  float scale;
+  int g_dtype, beta_dtype, o_dtype;
+  const int64_t* cu;
+  int xcd_remap;
+};
+
+// One barrier of the workgroup.  Written out (rather than __syncthreads)
+// so that the LOAD wave's LDS-DMA copies in flight are not drained at every
+// barrier: LDS writes of the issuing wave are complete (lgkmcnt), and the
+// LOAD wave waits for the DMA copies it publishes itself.  The "memory"
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// 16 bytes per lane from global memory into LDS at base + 16 * lane.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_ptr)lds_base, 16, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// 1. records
+// ---------------------------------------------------------------------------
+
+// Record r of a segment is (sequence bi, head hi, chunk c0 + lc) with
+// r = (bi * H + hi) * L + lc.
+__device__ __forceinline__ void rec_coords(const SArgs& p, int r, int& bi, int& hi, int& lc) {
+  lc = r % p.L;
+  const int bh = r / p.L;
+  hi = bh % p.H;
+  bi = bh / p.H;
+}
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
+  constexpr int KB = K / 32;
+  constexpr uint32_t EB = sizeof(TIn);
+  // per wave and record: A^T row-major (at[j][t] = A[t][j]), beta and b
+  __shared__ __attribute__((aligned(16))) float s_at[4][2][C * C];
+  __shared__ __attribute__((aligned(16))) float s_beta[4][2][C];
+  __shared__ __attribute__((aligned(16))) float s_b[4][2][C];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, gq = lane >> 4;
+  const int half = lane >> 5, c = lane & 31;
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+  // the two records of this wave: geometry (wave-uniform)
+  int nval[2];
+  const char* kh[2];
+  char* rp[2];
+  uint32_t skb[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int r = (blockIdx.x * 4 + wave) * 2 + e;
+    nval[e] = 0;
+    kh[e] = nullptr;
+    rp[e] = nullptr;
+    skb[e] = 0;
+    if (r < p.nrec) {
+      int bi, hi, lc;
+      rec_coords(p, r, bi, hi, lc);
+      const RowSpan rs = row_span(p.cu, p.T, bi);
+      const int t0 = (p.c0 + lc) * C;
+      if (t0 < rs.T) {
+        nval[e] = min(C, rs.T - t0);
+        kh[e] = static_cast<const char*>(p.k) + (head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1]) * EB;
+        skb[e] = (uint32_t)p.sk[1] * EB;
+        rp[e] = p.rec + (int64_t)r * REC_BYTES;
+      }
+    }
+  }
+  // k rows (rows past the end re-read the last row: finite values whose
+  // beta is zero), then the gates of row c of record `half`
+  uint4 kr[2][2][KB];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (nval[e] > 0) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int rr = min(16 * mt + n, nval[e] - 1);
+          kr[e][mt][kb] = ld16(kh[e], (uint32_t)rr * skb[e] + (32 * kb + 8 * gq) * EB);
+        }
+    }
+  }
+  float gv = 0.f, bv = 0.f;
+  {
+    const int e = half;
+    const int r = (blockIdx.x * 4 + wave) * 2 + e;
+    if (r < p.nrec && c < nval[e]) {
+      int bi, hi, lc;
+      rec_coords(p, r, bi, hi, lc);
+      const RowSpan rs = row_span(p.cu, p.T, bi);
+      const int64_t t = (int64_t)(p.c0 + lc) * C + c;
+      gv = load_scalar(p.g, head_base(rs, hi, p.sg) + t * p.sg[1], p.g_dtype);
+      bv = load_scalar(p.beta, head_base(rs, hi, p.sb) + t * p.sb[1], p.beta_dtype);
+    }
+  }
+  // gates (lanes 0-31: record 0, lanes 32-63: record 1)
+  const float b = scan32(gv);
+  const float bC0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), 31));
+  const float bC1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), 63));
+  const float bC = half ? bC1 : bC0;
+  s_beta[wave][half][c] = bv;
+  s_b[wave][half][c] = b;
+  if (nval[half] > 0) {
+    char* rr = rp[half];
+    reinterpret_cast<float*>(rr + R_B)[c] = b;
+    reinterpret_cast<float*>(rr + R_EB)[c] = fexp(b);
+    reinterpret_cast<float*>(rr + R_EC)[c] = fexp(bC - b);
+    if (c == 0) *reinterpret_cast<float*>(rr + R_EBC) = fexp(bC);
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // A = beta_t e^{b_t - b_j} K K^T (t > j), stored as A^T
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (nval[e] > 0) {
+      f16x8 kf[2][KB];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) kf[mt][kb] = to_f16x8<TIn>(kr[e][mt][kb]);
+      float* sa = s_at[wave][e];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt <= mt; ++nt) {
+          f32x4 acc = z4;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) acc = Mma<f16>::mma(kf[mt][kb], kf[nt][kb], acc);
+          const int jj = 16 * nt + n;
+          const float bj = s_b[wave][e][jj];
+          const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&s_b[wave][e][16 * mt + 4 * gq]);
+          const f32x4 be4 = *reinterpret_cast<const f32x4*>(&s_beta[wave][e][16 * mt + 4 * gq]);
+          f32x4 av;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 16 * mt + 4 * gq + i;
+            const float x = t > jj ? bt4[i] - bj : -__builtin_inff();
+            av[i] = acc[i] * fexp(x) * be4[i];
+          }
+          *reinterpret_cast<f32x4*>(sa + jj * C + 16 * mt + 4 * gq) = av;
+        }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // T by substitution: lane c of half h holds row c of T of record h
+  float xc[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) xc[i] = 0.f;
+  const float* at = s_at[wave][half];
+  solve_rows<19, 32>(at, c, xc);
+  solve_rows<13, 19>(at, c, xc);
+  solve_rows<9, 13>(at, c, xc);
+  solve_rows1<6, 9>(at, c, xc);
+  solve_rows1<3, 6>(at, c, xc);
+  solve_rows1<0, 3>(at, c, xc);
+  if (nval[half] > 0) {
+    // row c of Tu = T diag(beta): operand tile c / 16, lane (c % 16, g4)
+    const float* bt = s_beta[wave][half];
+    f16x8* tu = reinterpret_cast<f16x8*>(rp[half] + R_TU);
+    const int mt = c >> 4, nl = c & 15;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 u0 = *reinterpret_cast<const f32x4*>(&bt[4 * g4]);
+      const f32x4 u1 = *reinterpret_cast<const f32x4*>(&bt[16 + 4 * g4]);
+      f16x8 fu;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        fu[e] = (f16)(xc[4 * g4 + e] * u0[e]);
+        fu[4 + e] = (f16)(xc[16 + 4 * g4 + e] * u1[e]);
+      }
+      tu[mt * 64 + 16 * g4 + nl] = fu;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. the scan
+// ---------------------------------------------------------------------------
+
+template <int K, int BV>
+struct alignas(16) ScanSmem {
+  static constexpr int NSW = BV / 16;
+  static constexpr int R = D + 1;   // q, k, v slots: read in the chunk's own iteration
+  static constexpr int RR = D + 2;  // record slots: e^b is read once more by OUT
+  f16x8 rq[R][C][K / 8];            // q rows, 16-byte piece c of row r at swz(r, c)
+  f16x8 rk[R][C][K / 8];            // k rows, likewise
+  f16x8 rv[R][C][BV / 8];           // v slice rows (plain)
+  char rec[RR][REC_BYTES];
+  f16x8 p[2][2][64];                // P operand fragments, hi
+  f16x8 plo[2][2][64];              // and the fp16 residual
+  f16x8 so[2][NSW][K / 32][64];     // chunk-start state as B operand fragments
+  f16x8 uo[2][NSW][2][64];          // u as hi + lo
+};
+
+template <int BV>
+constexpr int scan_waves() {
+  return 2 * (BV / 16) + 2;
+}
+
+enum ScanRole { SR_SCAN, SR_OUT, SR_PQK, SR_LOAD };
+
+// DMA copies per chunk: q and k (1 KB each), the v slice, the record.
+template <int K, int BV>
+constexpr int dma_per_chunk() {
+  return 2 * (C * K * 2 / 1024) + (C * BV * 2 + 1023) / 1024 + REC_BYTES / 1024;
+}
+
+template <typename TIn, int K, int BV>
+__global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SArgs p) {
+  using M = Mma<f16>;
+  using S = ScanSmem<K, BV>;
+  constexpr int NSW = BV / 16;
+  constexpr int KB = K / 32, KT = K / 16;
+  constexpr int R = S::R, RR = S::RR;
+  constexpr int ND = dma_per_chunk<K, BV>();
+  static_assert(sizeof(TIn) == 2, "16-bit inputs");
+  static_assert((D - 1) * ND < 64, "outstanding DMA copies fit vmcnt");
+  static_assert(C * BV * 2 % 1024 == 0, "v slice rows fill whole DMA copies");
+
+  __shared__ S s;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n = lane & 15;
+  const int gq = lane >> 4;
+
+  int unit = blockIdx.x;
+  if (p.xcd_remap) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int vs = unit % p.nv;
+  const int bh = unit / p.nv;
+  const int bi = bh / p.H;
+  const int hi = bh % p.H;
+  const int v0 = vs * BV;
+  const RowSpan rs = row_span(p.cu, p.T, bi);
+  const int T = rs.T;
+  const int nch_all = (T + C - 1) / C;
+  const int nloc = max(0, min(p.L, nch_all - p.c0));  // chunks of this segment
+  if (nloc == 0 && !p.first) return;                  // state unchanged
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+  constexpr uint32_t EB = sizeof(TIn);
+  const uint32_t sqb = (uint32_t)p.sq[1] * EB, skb = (uint32_t)p.sk[1] * EB;
+  const uint32_t svb = (uint32_t)p.sv[1] * EB;
+  const char* qh = static_cast<const char*>(p.q) + head_base(rs, hi, p.sq) * EB;
+  const char* kh = static_cast<const char*>(p.k) + head_base(rs, hi, p.sk) * EB;
+  const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
+  const char* rech = p.rec + (int64_t)(bi * p.H + hi) * p.L * REC_BYTES;
+
+  auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int cc) { return tile[r][swz<K>(r, cc)]; };
+
+  int role, ridx;
+  if (wave < NSW) {
+    role = SR_SCAN;
+    ridx = wave;
+  } else if (wave < 2 * NSW) {
+    role = SR_OUT;
+    ridx = wave - NSW;
+  } else if (wave == 2 * NSW) {
+    role = SR_PQK;
+    ridx = 0;
+  } else {
+    role = SR_LOAD;
+    ridx = 0;
+  }
+
+  if (role == SR_SCAN) {
+    // ================================================================ SCAN
+    const int cb = ridx;
+    const int vcol = 16 * cb + n;
+    // accumulator element (r, i) is state row rho = 16 r + 4 gq + i
+    auto key_of = [&](int r, int i) { return 32 * (r >> 1) + 8 * gq + 4 * (r & 1) + i; };
+    f32x4 st[KT];
+    {
+      const float* src = p.first ? p.h0 : p.fs;
+      const int64_t* sd = p.first ? p.sh0 : p.sfs;
+#pragma unroll
+      for (int r = 0; r < KT; ++r) st[r] = z4;
+      if (src != nullptr) {
+        const float* s0 = src + bi * sd[0] + hi * sd[1] + (v0 + vcol) * sd[3];
+#pragma unroll
+        for (int r = 0; r < KT; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[r][i] = s0[key_of(r, i) * sd[2]];
+      }
+    }
+    f16x8 sB[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
+      s.so[0][cb][kb][lane] = sB[kb];
+    }
+    if (nloc > 0) wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      const int sl = it % R;
+      const char* rc = s.rec[it % RR];
+      f16x8 kR[2][KB], kA[KT];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+      const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
+      const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
+#pragma unroll
+      for (int r = 0; r < KT; ++r) {
+        const int piece = 4 * (r >> 1) + (n & 3);
+        const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
+        const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
+        kA[r] = cat8(lo, hi4);
+      }
+      // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
+      const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
+      const int vc = (16 * cb + 4 * (n & 3)) * 2;
+      const f16x4 va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+      const f16x4 vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+      const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
+      const f16x8 tu0 = tu[lane], tu1 = tu[64 + lane];
+      const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
+      const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
+      const f32x4 eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+      const f32x4 eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+      const f32x4 ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+      const f32x4 ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+      const float ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+      // K S: rows t, so its two row tiles form a B operand over t
+      f32x4 ks[2] = {z4, z4};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(kR[mt][kb], sB[kb], ks[mt]);
+      f32x4 y0, y1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y0[i] = (float)va[i] - eb_lo[i] * ks[0][i];
+        y1[i] = (float)vb[i] - eb_hi[i] * ks[1][i];
+      }
+      const f16x8 yB = M::from_acc(y0, y1);
+      f32x4 u[2];
+      u[0] = M::mma(tu0, yB, z4);
+      u[1] = M::mma(tu1, yB, z4);
+      const f16x8 utB = M::from_acc(u[0] * ec_lo, u[1] * ec_hi);
+#pragma unroll
+      for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * ebC);
+      {
+        const f16x8 uh = M::from_acc(u[0], u[1]);
+        s.uo[it & 1][cb][0][lane] = uh;
+        s.uo[it & 1][cb][1][lane] = split_lo(u[0], u[1], uh);
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
+        s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
+      }
+      wg_barrier();
+    }
+    float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
+#pragma unroll
+    for (int r = 0; r < KT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i];
+  } else if (nloc == 0) {
+    return;
+  } else if (role == SR_OUT) {
+    // ================================================================ OUT
+    const int c2 = ridx;
+    f32x4 oq[2] = {z4, z4};
+    auto store_chunk = [&](int it) {
+      const f16x8 uh = s.uo[it & 1][c2][0][lane];
+      const f16x8 ul = s.uo[it & 1][c2][1][lane];
+      const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
+      const f32x4 ebv[2] = {*reinterpret_cast<const f32x4*>(ebr + 4 * gq),
+                            *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq)};
+      f32x4 ov[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f16x8 pA = s.p[it & 1][mt][lane], pL = s.plo[it & 1][mt][lane];
+        f32x4 pu = M::mma(pA, ul, z4);
+        pu = M::mma(pL, uh, pu);
+        pu = M::mma(pA, uh, pu);
+        ov[mt] = (pu + ebv[mt] * oq[mt]) * p.scale;
+      }
+      const int j = p.c0 + it;
+      const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2 + n;
+      if (p.o_dtype == GDN_DTYPE_F16)
+        store_o<f16>(p.o, o_col, p.so[1], j * C, T, gq, ov);
+      else if (p.o_dtype == GDN_DTYPE_BF16)
+        store_o<bf16_t>(p.o, o_col, p.so[1], j * C, T, gq, ov);
+      else
+        store_o<float>(p.o, o_col, p.so[1], j * C, T, gq, ov);
+    };
+    wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      if (it >= 1) store_chunk(it - 1);
+      const int sl = it % R;
+      f16x8 qA[2][KB];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) qA[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x4 acc = z4;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc = M::mma(qA[mt][kb], s.so[it & 1][c2][kb][lane], acc);
+        oq[mt] = acc;
+      }
+      wg_barrier();
+    }
+    store_chunk(nloc - 1);
+  } else if (role == SR_PQK) {
+    // ================================================================ PQK
+    wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      const int sl = it % R;
+      const float* bb = reinterpret_cast<const float*>(s.rec[it % RR] + R_B);
+      f16x8 qf[2][KB], kf[2][KB];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          qf[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+          kf[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+        }
+      // P^T tiles (rows j, columns t) = K Q^T: the tiles of rows j in
+      // [0,16) and [16,32) of one column tile form one P operand
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int t = 16 * mt + n;
+        const float bt = bb[t];
+        f32x4 pt[2] = {z4, z4};
+#pragma unroll
+        for (int a = 0; a <= mt; ++a) {
+          f32x4 acc = z4;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) acc = M::mma(kf[a][kb], qf[mt][kb], acc);
+          const f32x4 bj4 = *reinterpret_cast<const f32x4*>(bb + 16 * a + 4 * gq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // mask folded into the exponent: 2^-inf = 0
+            const float x = t >= 16 * a + 4 * gq + i ? bt - bj4[i] : -__builtin_inff();
+            pt[a][i] = pin(acc[i] * fexp(x));
+          }
+        }
+        const f16x8 ph = M::from_acc(pt[0], pt[1]);
+        s.p[it & 1][mt][lane] = ph;
+        s.plo[it & 1][mt][lane] = split_lo(pt[0], pt[1], ph);
+      }
+      wg_barrier();
+    }
+  } else {
+    // =============================================================== LOAD
+    // chunk j -> slots j % R (q, k, v) and j % RR (record).  Rows past the
+    // end re-read the last row (finite values that the record's zero beta
+    // and the masks cancel).
+    constexpr int RCH = K / 8;               // 16-byte pieces per q / k row
+    constexpr int NQ = C * RCH / 64;         // DMA copies per q / k tile
+    constexpr int VCH = BV / 8;              // pieces per v row
+    constexpr int NV = C * VCH / 64;         // DMA copies per v tile
+    auto issue = [&](int it) {
+      const int j = p.c0 + it;
+      const int row0 = j * C;
+      const int last = T - 1 - row0;          // rows > last re-read row last
+      const char* qb = qh + (int64_t)row0 * sqb;
+      const char* kb = kh + (int64_t)row0 * skb;
+      const char* vb = vh + (int64_t)row0 * svb;
+      const int sl = it % R;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
+        const uint32_t rr = (uint32_t)min(r, last);
+        dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
+        dma16(kb + rr * skb + cc * 16, &s.rk[sl][0][0] + 64 * i);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int pc = 64 * i + lane, r = pc / VCH, cc = pc % VCH;
+        const uint32_t rr = (uint32_t)min(r, last);
+        dma16(vb + rr * svb + cc * 16, &s.rv[sl][0][0] + 64 * i);
+      }
+      const char* rsrc = rech + (int64_t)it * REC_BYTES;
+#pragma unroll
+      for (int i = 0; i < REC_BYTES / 1024; ++i) dma16(rsrc + 1024 * i + 16 * lane, s.rec[it % RR] + 1024 * i);
+    };
+    for (int it = 0; it < D; ++it)
+      if (it < nloc) issue(it);
+    if (nloc >= D)
+      wait_vm<(D - 1) * ND>();
+    else
+      wait_vm<0>();
+    wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      // chunk it + 1 must be in LDS at this iteration's barrier
+      if (it + D < nloc) {
+        issue(it + D);
+        wait_vm<(D - 1) * ND>();
+      } else {
+        wait_vm<0>();
+      }
+      wg_barrier();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+template <typename TIn, int K, int BV>
+int launch_kb(const SArgs& a, int units, hipStream_t s) {
+  static_assert(sizeof(ScanSmem<K, BV>) <= kLdsLimit, "LDS budget");
+  if (a.nrec > 0) hipLaunchKernelGGL((rec32_kernel<TIn, K>), dim3((a.nrec + 7) / 8), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((scan32_kernel<TIn, K, BV>), dim3(units), dim3(64 * scan_waves<BV>()), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn>
+int launch_t(const SArgs& a, int K, int bv, int units, hipStream_t s) {
+  if (K == 64 && bv == 16) return launch_kb<TIn, 64, 16>(a, units, s);
+  if (K == 64 && bv == 32) return launch_kb<TIn, 64, 32>(a, units, s);
+  if (K == 128 && bv == 16) return launch_kb<TIn, 128, 16>(a, units, s);
+  if (K == 128 && bv == 32) return launch_kb<TIn, 128, 32>(a, units, s);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+}  // namespace s32
+
+bool scan32_supported(int dtype, int K, int C, int BV) {
+  return dtype == GDN_DTYPE_F16 && C == s32::C && (K == 64 || K == 128) && (BV == 16 || BV == 32);
+}
+
+int64_t scan32_record_bytes() { return s32::REC_BYTES; }
+
+// Enqueues the segments of one call: for each, the records then the scan
+// (arguments checked by the caller; seg_chunks >= 1).
+int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t stream) {
+  s32::SArgs a = {};
+  a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
+  a.o = P.o; a.fs = P.final_state;
+  a.rec = static_cast<char*>(P.workspace);
+  for (int d = 0; d < 3; ++d) {
+    a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
+    a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.so[d] = P.o_stride[d];
+  }
+  for (int d = 0; d < 4; ++d) { a.sh0[d] = P.h0_stride[d]; a.sfs[d] = P.fs_stride[d]; }
+  a.B = P.B; a.T = P.T; a.H = P.H; a.V = P.V; a.nv = P.V / bv;
+  a.scale = P.scale;
+  a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.o_dtype = P.o_dtype;
+  a.cu = P.cu_seqlens;
+  const int64_t units = (int64_t)P.B * P.H * a.nv;
+  a.xcd_remap = (units % 8 == 0) ? 1 : 0;
+  // every sequence has at most ceil(T / C) chunks (the offsets are not read here)
+  const int nchmax = (P.T + s32::C - 1) / s32::C;
+  const int L = nchmax > 0 ? (seg_chunks < nchmax ? seg_chunks : nchmax) : 1;
+  const int nseg = nchmax > 0 ? (nchmax + L - 1) / L : 1;
+  a.L = L;
+  a.nrec = (int)((int64_t)P.B * P.H * L);
+  for (int sg = 0; sg < nseg; ++sg) {
+    a.c0 = sg * L;
+    a.first = sg == 0;
+    if (nchmax == 0) a.nrec = 0;
+    int st;
+    if (P.qkv_dtype == GDN_DTYPE_F16)
+      st = s32::launch_t<f16>(a, P.K, bv, (int)units, stream);
+    else
+      st = GDN_ERR_UNSUPPORTED;
+    if (st != 0) return st;
+  }
+  return GDN_OK;
+}
+
+}  // namespace gdn

@@ -110,7 +110,7 @@ def _check_devices(q, *others):
         raise ValueError("all inputs must be on the same device")
 
 
-_KERNELS = {"auto": 0, "phased": _lib.FLAG_PHASED_KERNEL}
+_KERNELS = {"auto": 0, "phased": _lib.FLAG_PHASED_KERNEL, "fused": _lib.FLAG_FUSED_KERNEL}
 
 # Launch plans keyed by everything but the data pointers: shapes, strides,
 # dtypes, devices and options.  A call whose signature was seen before skips
@@ -126,16 +126,16 @@ class _Plan:
 
 
 def _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
-               n_seq, o_hf):
+               n_seq, o_hf, seg_chunks=None):
     hs = None if h0 is None else (h0.shape, h0.stride(), h0.dtype, h0.device)
     return (q.shape, q.stride(), q.dtype, q.device, k.shape, k.stride(), k.dtype, k.device,
             v.shape, v.stride(), v.dtype, v.device, g.shape, g.stride(), g.dtype, g.device,
             beta.shape, beta.stride(), beta.dtype, beta.device, hs, float(scale), chunk_size,
-            block_v, output_dtype, kernel, fs_vk, n_seq, o_hf)
+            block_v, output_dtype, kernel, fs_vk, n_seq, o_hf, seg_chunks)
 
 
 def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
-               n_seq, o_hf):
+               n_seq, o_hf, seg_chunks=None):
     B, T, H, K, V = _validate(q, k, v, g, beta, h0, chunk_size, block_v, n_seq)
     if kernel not in _KERNELS:
         raise ValueError(f"kernel={kernel!r} must be one of {sorted(_KERNELS)}")
@@ -176,10 +176,20 @@ def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, k
     # workspace bytes for these shapes (only whether cu_seqlens is set
     # matters to the size, not where it points)
     P.cu_seqlens = 1 if n_seq is not None else None
-    ws = _lib.load_library().gdn_fwd_workspace_size(ctypes.byref(P))
-    P.cu_seqlens = None
+    lib = _lib.load_library()
+    ws = lib.gdn_fwd_workspace_size(ctypes.byref(P))
     if ws < 0:
         raise ValueError(f"unsupported forward shape B={B} T={T} H={H} K={K} V={V}")
+    if seg_chunks is not None and ws > 0 and chunk_size == 32:
+        # the records of seg_chunks chunks per sequence (what a call of
+        # seg_chunks * 32 rows takes): the call then runs in segments of that
+        # many chunks (fewer records, more launches)
+        if int(seg_chunks) < 1:
+            raise ValueError(f"max_segment_chunks must be >= 1, got {seg_chunks}")
+        P.T = min(T, 32 * int(seg_chunks))
+        ws = lib.gdn_fwd_workspace_size(ctypes.byref(P))
+        P.T = T
+    P.cu_seqlens = None
     plan.ws_bytes = int(ws)
     plan.params = bytes(P)
     return plan
@@ -204,7 +214,7 @@ def _check_cu_seqlens(cu, T, dev):
 
 
 def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, fs_vk,
-         cu_seqlens=None, o_hf=False):
+         cu_seqlens=None, o_hf=False, seg_chunks=None):
     n_seq = None
     if cu_seqlens is not None:
         if not isinstance(q, torch.Tensor) or q.dim() != 4:
@@ -212,13 +222,13 @@ def _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
         cu_seqlens, n_seq = _check_cu_seqlens(cu_seqlens, q.shape[1], q.device)
     try:
         key = _signature(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
-                         kernel, fs_vk, n_seq, o_hf)
+                         kernel, fs_vk, n_seq, o_hf, seg_chunks)
         plan = _PLANS.get(key)
     except (AttributeError, TypeError):   # not tensors: _validate says which
         key, plan = None, None
     if plan is None:
         plan = _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
-                          kernel, fs_vk, n_seq, o_hf)
+                          kernel, fs_vk, n_seq, o_hf, seg_chunks)
         if key is not None:
             if len(_PLANS) >= _PLANS_MAX:
                 _PLANS.clear()
@@ -256,7 +266,8 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
             chunk_size: int = 32, *, block_v: Optional[int] = None,
             output_dtype: Optional[torch.dtype] = None,
             kernel: str = "auto",
-            cu_seqlens: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+            cu_seqlens: Optional[torch.Tensor] = None,
+            max_segment_chunks: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Fused chunked Gated DeltaNet forward on an MI355X.
 
     Args:
@@ -271,13 +282,19 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
       block_v: V columns per workgroup (16, 32, 64); None picks one.
       output_dtype: dtype of ``o``; defaults to ``q.dtype`` (as the
         reference, gdn_triton.py:126).
-      kernel: ``"auto"`` runs the software-pipelined kernel where it applies
-        (fp16/bf16, chunk 32, K in {64, 128}, block_v 16/32) and the
-        phase-by-phase kernel elsewhere; ``"phased"`` forces the latter.
+      kernel: ``"auto"`` picks per shape: for fp16 with chunk 32 and K in
+        {64, 128}, per-chunk records then the scan (two launches per
+        segment, a workspace of records); for bf16 there, the single fused
+        pipelined kernel; the phase-by-phase kernel elsewhere.  ``"fused"``
+        forces the fused pipelined kernel (no workspace) where it applies,
+        ``"phased"`` the phase-by-phase kernel.
       cu_seqlens: optional int64 ``[N + 1]`` row offsets: N sequences
         packed along t of a batch of one (B = 1); sequence i is rows
         ``cu_seqlens[i]:cu_seqlens[i+1]`` with its own ``h0[i]`` and
         ``final_state[i]`` (h0 and final_state are then ``[N, H, K, V]``).
+      max_segment_chunks: for the two-launch 32-row path, the records of at
+        most this many chunks per sequence are held at once; a longer
+        sequence runs as several segments (default: 256 chunks).
 
     Returns:
       ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.  When an
@@ -291,7 +308,7 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         return _GdnFunction.apply(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
                                   kernel, False, cu_seqlens, False)
     return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False,
-                cu_seqlens)
+                cu_seqlens, False, max_segment_chunks)
 
 
 def gdn_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
