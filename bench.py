@@ -1,13 +1,15 @@
 """Benchmark of the MI355X fused chunked GDN forward (BASELINE.json metric).
 
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` times K back-to-back
-forwards of the headline workload (configs[2]: fp16, B=2, H=16, T=4096,
+forwards (after W untimed ones, preceded by 0.3 s of untimed calls that bring
+the GPU out of its idle clock) of the headline workload (configs[2]: fp16, B=2, H=16, T=4096,
 K=V=128, C=32) with inputs already resident in HBM, and prints ONE JSON line
 with tokens/s, ms per step, the roofline position of the kernel and a CPU
 baseline (the oracle's chunked-UT restatement of gdn_ref.py:48-99 on this
 host's cores).
 
-A "step" is one ``gdn_fwd`` call over the whole batch (one kernel launch).
+A "step" is one ``gdn_fwd`` call over the whole batch: one ``gdn_fwd_launch``
+(for fp16 at C=32, two kernels: the per-chunk records, then the scan).
 Extra fields report the C=64 variant, a cold-cache timing (caches flushed
 with a 512 MiB write between launches, each launch timed with its own
 events) and the fused input preparation (``gdn_prep``: L2-norm of q and k,
@@ -140,9 +142,31 @@ def time_bwd(pkg, q, k, v, g, beta, h0, steps, warmup):
             "bytes_per_launch": nb, "achieved_gbs": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 6)}
 
 
+PREWARM_S = 0.3
+
+
+def prewarm(fn, seconds=PREWARM_S):
+    """Runs ``fn`` back to back, untimed, for ``seconds`` of wall time.  An
+    idle MI355X raises its clock only after tens of milliseconds of sustained
+    work: five warmup steps of ~0.1 ms leave the timed steps of a short run
+    about 10 % slower than the same steps after this.  Returns the calls
+    made."""
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 64 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
 def time_steps(fn, steps, warmup):
-    """Warm up, then time exactly ``steps`` back-to-back calls between two
-    events on the current stream (the stream the kernel is launched on)."""
+    """Warm up (the clock pre-warm, then ``warmup`` calls), then time exactly
+    ``steps`` back-to-back calls between two events on the current stream
+    (the stream the kernel is launched on)."""
+    prewarm(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -308,6 +332,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_s": PREWARM_S,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
