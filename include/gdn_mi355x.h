@@ -65,7 +65,10 @@ enum GdnStatus {
   GDN_ERR_UNSUPPORTED = 1003,
   GDN_ERR_MISALIGNED = 1004,
   GDN_ERR_BAD_DTYPE = 1005,
-  GDN_ERR_WORKSPACE = 1006
+  GDN_ERR_WORKSPACE = 1006,
+  /* gdn_fwd_launch_noalloc: the call needs more workspace than the static
+   * scratch array holds (gdn_fwd_scratch_bytes()) */
+  GDN_ERR_SCRATCH_LIMIT = 1007
 };
 
 /* Launch options (bit flags). */
@@ -132,6 +135,30 @@ typedef struct GdnFwdParams {
  *     the scan over chunks; block_v is 16 there); needs params->workspace.
  * The state stays on chip in every path: no chunk state is written. */
 int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
+
+/* gdn_fwd_launch without a caller workspace and without any allocation.
+ * No counterpart in the reference (its Triton launch needs no workspace);
+ * it is for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same arguments, semantics and statuses as gdn_fwd_launch, except that
+ * params->workspace / workspace_bytes are ignored: the paths that take a
+ * workspace (32-row records, 64-row records) use a static device array of
+ * gdn_fwd_scratch_bytes() bytes (32 MiB) held by each device from the
+ * library's load to the end of the process.
+ *   - 32-row chunks (fp16): the sequence runs in segments of as many chunks
+ *     as the array holds (B * H records of 3 KB per chunk); the call fails
+ *     with GDN_ERR_SCRATCH_LIMIT only if one chunk per sequence does not
+ *     fit (B * H > 10922).
+ *   - 64-row chunks: GDN_ERR_SCRATCH_LIMIT when gdn_fwd_workspace_size()
+ *     exceeds the array.
+ *   - Nothing is enqueued when a status other than GDN_OK is returned.
+ * Every call on a device shares that device's array: calls that overlap
+ * on one device (on different streams, or from different host threads)
+ * race and must be serialised by the caller. */
+int gdn_fwd_launch_noalloc(const GdnFwdParams* params, void* stream);
+
+/* Size in bytes of the static scratch array of gdn_fwd_launch_noalloc. */
+int64_t gdn_fwd_scratch_bytes(void);
 
 /* Bytes of workspace gdn_fwd_launch needs for these params (0 for the fused
  * kernels; for 32-row chunks the records of a segment of at most 256 chunks

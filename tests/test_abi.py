@@ -392,3 +392,26 @@ def test_bwd_python_validation(pkg):
     with pytest.raises(ValueError, match="dfinal"):
         pkg.gdn_bwd(q, k, v, g, b, None, torch.zeros(1, 64, 2, 32, dtype=torch.float16),
                     torch.zeros(1, 2, 64, 32, dtype=torch.float16))
+
+
+# --------------------------------------------------------------------------
+# gdn_fwd_launch_noalloc: argument and size checks come before any HIP call
+# --------------------------------------------------------------------------
+
+def test_noalloc_scratch_size(lib):
+    assert lib.gdn_fwd_scratch_bytes() == 32 << 20
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=0), 1002), (dict(V=24), 1002), (dict(K=96), 1003), (dict(qkv_dtype=7), 1005),
+    (dict(q=0x1008), 1004), (dict(final_state=None), 1001),
+    # 64-row records of B2 H16 T4096 (69 MB) exceed the 32 MiB array
+    (dict(chunk_size=64), 1007),
+    # one 3 KB record per (sequence, head) must fit: 11000 > 10922 heads
+    (dict(B=11000, H=1, T=64), 1007),
+])
+def test_noalloc_rejects_before_launch(lib, pkg, kw, code):
+    P = _params(pkg._lib, **kw)
+    assert lib.gdn_fwd_launch_noalloc(ctypes.byref(P), None) == code
+    assert lib.gdn_fwd_launch_noalloc(None, None) == 1001
+    assert "scratch" in lib.gdn_fwd_status_string(1007).decode()

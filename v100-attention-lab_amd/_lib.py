@@ -24,6 +24,7 @@ GDN_ERR_UNSUPPORTED = 1003
 GDN_ERR_MISALIGNED = 1004
 GDN_ERR_BAD_DTYPE = 1005
 GDN_ERR_WORKSPACE = 1006
+GDN_ERR_SCRATCH_LIMIT = 1007
 
 # enum GdnFlags
 FLAG_PHASED_KERNEL = 1
@@ -39,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "gdn_prep_launch",
     "gdn_bwd_workspace_size",
     "gdn_bwd_launch",
+    "gdn_fwd_launch_noalloc",
+    "gdn_fwd_scratch_bytes",
 )
 
 _I64x3 = ctypes.c_int64 * 3
@@ -154,6 +157,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         lib = ctypes.CDLL(path)
         lib.gdn_fwd_launch.argtypes = [ctypes.POINTER(GdnFwdParams), ctypes.c_void_p]
         lib.gdn_fwd_launch.restype = ctypes.c_int
+        lib.gdn_fwd_launch_noalloc.argtypes = [ctypes.POINTER(GdnFwdParams), ctypes.c_void_p]
+        lib.gdn_fwd_launch_noalloc.restype = ctypes.c_int
+        lib.gdn_fwd_scratch_bytes.argtypes = []
+        lib.gdn_fwd_scratch_bytes.restype = ctypes.c_int64
         lib.gdn_fwd_workspace_size.argtypes = [ctypes.POINTER(GdnFwdParams)]
         lib.gdn_fwd_workspace_size.restype = ctypes.c_int64
         lib.gdn_fwd_auto_block_v.argtypes = [ctypes.c_int] * 6

@@ -1,6 +1,8 @@
 // Host side of the C ABI declared in include/gdn_mi355x.h: argument checks,
 // BV choice and dispatch to the per-dtype launchers.
 
+#include <mutex>
+
 #include "gdn_fwd_kernel.h"
 
 namespace gdn {
@@ -39,37 +41,6 @@ static bool pipe_offsets_fit(const GdnFwdParams& P) {
   return true;
 }
 
-}  // namespace gdn
-
-using namespace gdn;
-
-extern "C" {
-
-int gdn_fwd_abi_version(void) { return GDN_MI355X_ABI_VERSION; }
-
-int gdn_fwd_auto_block_v(int B, int H, int K, int V, int chunk_size, int qkv_dtype) {
-  if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || V % 16 != 0) return -1;
-  return auto_block_v(B, H, K, V, chunk_size, qkv_dtype);
-}
-
-const char* gdn_fwd_status_string(int status) {
-  switch (status) {
-    case GDN_OK: return "success";
-    case GDN_ERR_NULL_POINTER: return "gdn_fwd: a required pointer is NULL";
-    case GDN_ERR_BAD_SHAPE: return "gdn_fwd: invalid shape (B, H, K, V must be > 0, T >= 0, V % 16 == 0)";
-    case GDN_ERR_UNSUPPORTED:
-      return "gdn_fwd: unsupported configuration (K in {32,64,128,256}, chunk_size in {32,64}, "
-             "block_v in {16,32,64} dividing V, within the 160 KB LDS budget)";
-    case GDN_ERR_MISALIGNED:
-      return "gdn_fwd: q/k/v rows must be 16-byte aligned with a contiguous last dimension";
-    case GDN_ERR_BAD_DTYPE: return "gdn_fwd: unknown dtype code";
-    case GDN_ERR_WORKSPACE:
-      return "gdn: workspace missing, misaligned or smaller than gdn_fwd_workspace_size() / "
-             "gdn_bwd_workspace_size()";
-    default: return hipGetErrorString((hipError_t)status);
-  }
-}
-
 // The two-launch path for 64-row chunks, unless the phased kernel is asked for.
 static bool uses_c64(const GdnFwdParams& P) {
   return !(P.flags & GDN_FLAG_PHASED_KERNEL) && c64_supported(P.K, P.chunk_size, P.V);
@@ -86,25 +57,49 @@ static bool uses_scan32(const GdnFwdParams& P, int bv) {
          scan32_supported(P.qkv_dtype, P.K, P.chunk_size, bv) && pipe_offsets_fit(P);
 }
 
-int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
-  if (prm == nullptr) return -1;
-  const GdnFwdParams& P = *prm;
-  if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0) return -1;
-  if (!valid_dtype(P.qkv_dtype)) return -1;
-  if (uses_c64(P)) return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
-  const int bv = P.block_v ? P.block_v : auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
-  if (bv > 0 && P.V % bv == 0 && uses_scan32(P, bv)) {
-    const int64_t nch = (P.T + 31) / 32;
-    const int64_t L = nch < kSegChunks ? nch : kSegChunks;
-    const int64_t bytes = (int64_t)P.B * P.H * L * scan32_record_bytes();
-    return (bytes + 255) / 256 * 256;
+// ---------------------------------------------------------------------------
+// Static scratch of gdn_fwd_launch_noalloc: the record workspace for callers
+// that cannot allocate.  Each device holds its own copy from module load to
+// process end; host code uses only the per-device address fetched with
+// hipGetSymbolAddress (the array's name is a host-side stand-in).  Every
+// call on a device shares that device's copy, so calls that overlap on one
+// device race.  The records a call reads are written by the same call first,
+// so nothing needs clearing between calls.
+constexpr int64_t kScratchBytes = 32ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch copy (fetched once per
+// device, with that device current).
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return GDN_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (ptr == nullptr || reinterpret_cast<uintptr_t>(ptr) % 256 != 0) return GDN_ERR_WORKSPACE;
+    g_scratch_ptr[dev] = ptr;
   }
+  *out = g_scratch_ptr[dev];
   return 0;
 }
 
-int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
-  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
-  const GdnFwdParams& P = *prm;
+}  // namespace gdn
+
+using namespace gdn;
+
+// The launch of gdn_fwd_launch and gdn_fwd_launch_noalloc.  With
+// `scratch_bytes` > 0 the record workspace is the library's static scratch
+// array (its device address fetched only after every argument check passed)
+// and params->workspace is ignored.
+static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_bytes) {
   if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0)
     return GDN_ERR_BAD_SHAPE;
   if (!valid_dtype(P.qkv_dtype) || !valid_dtype(P.g_dtype) || !valid_dtype(P.beta_dtype) ||
@@ -132,12 +127,33 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   }
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
+  const bool scan32 = uses_scan32(P, bv) && (scratch_bytes > 0 || P.workspace != nullptr);
+  // workspace: the caller's, or the static scratch array when it holds
+  // what the path needs
+  GdnFwdParams W = P;
+  if (scratch_bytes > 0 && (c64 || scan32) && P.T > 0) {
+    const int64_t need = c64 ? c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype)
+                             : (int64_t)P.B * P.H * scan32_record_bytes();  // one chunk per sequence
+    if (need > scratch_bytes) return GDN_ERR_SCRATCH_LIMIT;
+    void* ptr = nullptr;
+    const int st = scratch_address(&ptr);
+    if (st != 0) return st;
+    W.workspace = ptr;
+    W.workspace_bytes = scratch_bytes;
+  }
   if (c64) {
     const int64_t need = c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
-    if (P.T > 0 && (P.workspace == nullptr || reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 ||
-                    P.workspace_bytes < need))
+    if (P.T > 0 && (W.workspace == nullptr || reinterpret_cast<uintptr_t>(W.workspace) % 256 != 0 ||
+                    W.workspace_bytes < need))
       return GDN_ERR_WORKSPACE;
-    return c64_launch(P, static_cast<hipStream_t>(stream));
+    return c64_launch(W, s);
+  }
+  if (scan32) {
+    // segment length: as many chunks per sequence as the workspace holds
+    const int64_t per_chunk = (int64_t)P.B * P.H * scan32_record_bytes();
+    const int64_t L = W.workspace_bytes / per_chunk;
+    if (P.T > 0 && (reinterpret_cast<uintptr_t>(W.workspace) % 256 != 0 || L < 1)) return GDN_ERR_WORKSPACE;
+    return scan32_launch(W, bv, (int)(L < 1 ? 1 : L < 0x7fffffff ? L : 0x7fffffff), s);
   }
 
   KArgs a = {};
@@ -155,14 +171,6 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
   a.cu = P.cu_seqlens;
 
   const int grid = (int)units;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (P.workspace != nullptr && uses_scan32(P, bv)) {
-    // segment length: as many chunks per sequence as the workspace holds
-    const int64_t per_chunk = (int64_t)P.B * P.H * scan32_record_bytes();
-    const int64_t L = P.workspace_bytes / per_chunk;
-    if (reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0 || L < 1) return GDN_ERR_WORKSPACE;
-    return scan32_launch(P, bv, (int)(L < 0x7fffffff ? L : 0x7fffffff), s);
-  }
   if (!(P.flags & GDN_FLAG_PHASED_KERNEL) && pipe_supported(P.qkv_dtype, P.K, P.chunk_size, bv) &&
       pipe_offsets_fit(P)) {
     if (P.qkv_dtype == GDN_DTYPE_F16) return launch_pipe_f16(a, P.K, bv, grid, s);
@@ -175,5 +183,63 @@ int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
     default: return GDN_ERR_BAD_DTYPE;
   }
 }
+
+extern "C" {
+
+int gdn_fwd_abi_version(void) { return GDN_MI355X_ABI_VERSION; }
+
+int gdn_fwd_auto_block_v(int B, int H, int K, int V, int chunk_size, int qkv_dtype) {
+  if (B <= 0 || H <= 0 || K <= 0 || V <= 0 || V % 16 != 0) return -1;
+  return auto_block_v(B, H, K, V, chunk_size, qkv_dtype);
+}
+
+const char* gdn_fwd_status_string(int status) {
+  switch (status) {
+    case GDN_OK: return "success";
+    case GDN_ERR_NULL_POINTER: return "gdn_fwd: a required pointer is NULL";
+    case GDN_ERR_BAD_SHAPE: return "gdn_fwd: invalid shape (B, H, K, V must be > 0, T >= 0, V % 16 == 0)";
+    case GDN_ERR_UNSUPPORTED:
+      return "gdn_fwd: unsupported configuration (K in {32,64,128,256}, chunk_size in {32,64}, "
+             "block_v in {16,32,64} dividing V, within the 160 KB LDS budget)";
+    case GDN_ERR_MISALIGNED:
+      return "gdn_fwd: q/k/v rows must be 16-byte aligned with a contiguous last dimension";
+    case GDN_ERR_BAD_DTYPE: return "gdn_fwd: unknown dtype code";
+    case GDN_ERR_WORKSPACE:
+      return "gdn: workspace missing, misaligned or smaller than gdn_fwd_workspace_size() / "
+             "gdn_bwd_workspace_size()";
+    case GDN_ERR_SCRATCH_LIMIT:
+      return "gdn_fwd_launch_noalloc: the call needs more workspace than the static scratch array "
+             "(gdn_fwd_scratch_bytes()) holds";
+    default: return hipGetErrorString((hipError_t)status);
+  }
+}
+
+int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
+  if (prm == nullptr) return -1;
+  const GdnFwdParams& P = *prm;
+  if (P.B <= 0 || P.H <= 0 || P.K <= 0 || P.V <= 0 || P.T < 0 || P.V % 16 != 0) return -1;
+  if (!valid_dtype(P.qkv_dtype)) return -1;
+  if (uses_c64(P)) return c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
+  const int bv = P.block_v ? P.block_v : auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
+  if (bv > 0 && P.V % bv == 0 && uses_scan32(P, bv)) {
+    const int64_t nch = (P.T + 31) / 32;
+    const int64_t L = nch < kSegChunks ? nch : kSegChunks;
+    const int64_t bytes = (int64_t)P.B * P.H * L * scan32_record_bytes();
+    return (bytes + 255) / 256 * 256;
+  }
+  return 0;
+}
+
+int gdn_fwd_launch(const GdnFwdParams* prm, void* stream) {
+  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
+  return launch_impl(*prm, static_cast<hipStream_t>(stream), 0);
+}
+
+int gdn_fwd_launch_noalloc(const GdnFwdParams* prm, void* stream) {
+  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
+  return launch_impl(*prm, static_cast<hipStream_t>(stream), kScratchBytes);
+}
+
+int64_t gdn_fwd_scratch_bytes(void) { return kScratchBytes; }
 
 }  // extern "C"
