@@ -146,9 +146,9 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  * gdn_fwd_scratch_bytes() bytes (32 MiB) held by each device from the
  * library's load to the end of the process.
  *   - 32-row chunks (fp16): the sequence runs in segments of as many chunks
- *     as the array holds (B * H records of 7 KB per chunk); the call fails
+ *     as the array holds (B * H records of 3 KB per chunk); the call fails
  *     with GDN_ERR_SCRATCH_LIMIT only if one chunk per sequence does not
- *     fit (B * H > 4681).
+ *     fit (B * H > 10922).
  *   - 64-row chunks: GDN_ERR_SCRATCH_LIMIT when gdn_fwd_workspace_size()
  *     exceeds the array.
  *   - Nothing is enqueued when a status other than GDN_OK is returned.
@@ -161,7 +161,7 @@ int gdn_fwd_launch_noalloc(const GdnFwdParams* params, void* stream);
 int64_t gdn_fwd_scratch_bytes(void);
 
 /* Bytes of workspace gdn_fwd_launch needs for these params (0 for the fused
- * kernels; for 32-row chunks the records of a segment of at most 128 chunks
+ * kernels; for 32-row chunks the records of a segment of at most 256 chunks
  * per sequence; B = the number of sequences when cu_seqlens is set); -1 if
  * the shape is invalid.  No counterpart in the reference, whose Triton
  * launch needs none. */

@@ -97,19 +97,19 @@ def _params(L, **kw):
 
 def test_fwd_workspace_size(lib, pkg):
     """Fused kernels need no workspace.  32-row chunks with fp16 q/k/v and
-    K in {64, 128} take one 7 KB record per (sequence, head, chunk) of a
-    segment of at most 128 chunks.  64-row chunks with K <= 128 take one
+    K in {64, 128} take one 3 KB record per (sequence, head, chunk) of a
+    segment of at most 256 chunks.  64-row chunks with K <= 128 take one
     record per (chunk slot, head).  fp32 inputs: T and P (C x C), W (C x K)
     in fp32, then three gate rows.  16-bit inputs: T diag(beta) and P (C x C)
     as fp16 hi/lo pairs, then four fp32 gate rows."""
     L = pkg._lib
     size = lambda **kw: lib.gdn_fwd_workspace_size(ctypes.byref(_params(L, **kw)))
     H = 16
-    assert size() == 2 * H * 128 * 7168                  # C = 32 fp16: records of 128 chunks
-    assert size(T=16384) == 2 * H * 128 * 7168           # segments of at most 128 chunks
-    assert size(T=100, K=64) == 2 * H * 4 * 7168         # partial last chunk included
+    assert size() == 2 * H * 128 * 3072                  # C = 32 fp16: records of 128 chunks
+    assert size(T=16384) == 2 * H * 256 * 3072           # segments of at most 256 chunks
+    assert size(T=100, K=64) == 2 * H * 4 * 3072         # partial last chunk included
     assert size(T=0) == 0
-    assert size(B=3, T=100, cu_seqlens=0x2000) == 3 * H * 4 * 7168
+    assert size(B=3, T=100, cu_seqlens=0x2000) == 3 * H * 4 * 3072
     assert size(flags=2) == 0                            # fused kernel forced: none
     assert size(qkv_dtype=2) == 0                        # bf16: fused kernel, none
     assert size(qkv_dtype=0) == 0                        # fp32: phased kernel, none
@@ -407,8 +407,8 @@ def test_noalloc_scratch_size(lib):
     (dict(q=0x1008), 1004), (dict(final_state=None), 1001),
     # 64-row records of B2 H16 T4096 (69 MB) exceed the 32 MiB array
     (dict(chunk_size=64), 1007),
-    # one 7 KB record per (sequence, head) must fit: 5000 > 4681 heads
-    (dict(B=5000, H=1, T=64), 1007),
+    # one 3 KB record per (sequence, head) must fit: 11000 > 10922 heads
+    (dict(B=11000, H=1, T=64), 1007),
 ])
 def test_noalloc_rejects_before_launch(lib, pkg, kw, code):
     P = _params(pkg._lib, **kw)

@@ -41,7 +41,7 @@ def test_cfg2_headline(pkg, cuda, C):
 
 def test_cfg3_long_sequence_and_footprint(pkg, cuda):
     """fp16 B2 H16 T16384.  Besides o and final_state only the
-    per-chunk records of one segment (at most 128 chunks per (b, h): 29 MB,
+    per-chunk records of one segment (at most 256 chunks per (b, h): 25 MB,
     independent of T) are allocated; no chunk state is materialised."""
     B, T, H, K, V = 2, 16384, 16, 128, 128
     q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=0)
@@ -53,10 +53,10 @@ def test_cfg3_long_sequence_and_footprint(pkg, cuda):
     torch.cuda.synchronize()
     delta = torch.cuda.max_memory_allocated() - base
     outputs = o.numel() * o.element_size() + fs.numel() * fs.element_size()
-    records = B * H * 128 * 7168
+    records = B * H * 256 * 3072
     print(f"[cfg3] peak HBM delta {delta} B, outputs {outputs} B, records {records} B", flush=True)
     assert delta == outputs + records  # no per-chunk state; records of one segment
-    assert records < 0.25 * outputs
+    assert records < 0.2 * outputs
     o_ref, h_ref = ref.recurrent(q, k, v, beta, g, dtype=torch.float32)
     eo = ref.rel_err(o_ref, o.cpu())
     eh = ref.rel_err(ref.to_kv(h_ref), fs.cpu())

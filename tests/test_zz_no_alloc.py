@@ -83,7 +83,7 @@ def _both(pkg, cuda, B, T, H, K, V, dtype, chunk, seed):
 
 
 # (B, T, H, K, V, dtype, chunk): the first call runs 3 segments in the
-# scratch (1024 heads x 7 KB per chunk: 4 chunks of 22 fit) against one
+# scratch (1024 heads x 3 KB per chunk: 10 chunks of 22 fit) against one
 # segment with a caller workspace; the second is smaller and runs in one.
 CASES = [
     (2, 700, 512, 128, 64, torch.float16, 32),
@@ -104,7 +104,7 @@ def test_noalloc_matches_launch(pkg, cuda, case):
 
 
 def test_noalloc_two_calls_in_a_row(pkg, cuda):
-    """A large call (320 heads: 9 segments of 14 chunks in the scratch), then a
+    """A large call (320 heads: 4 segments of 34 chunks in the scratch), then a
     smaller one (one segment), each against gdn_fwd_launch."""
     for seed, (B, T, H) in enumerate(((8, 4000, 40), (1, 700, 3))):
         (o1, fs1), (o2, fs2) = _both(pkg, cuda, B, T, H, 128, 128, torch.float16, 32, seed=60 + seed)

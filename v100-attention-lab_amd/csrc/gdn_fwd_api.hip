@@ -48,7 +48,7 @@ static bool uses_c64(const GdnFwdParams& P) {
 
 // Records of at most this many chunks per sequence are what
 // gdn_fwd_workspace_size asks for on the 32-row two-launch path.
-constexpr int64_t kSegChunks = 128;
+constexpr int64_t kSegChunks = 256;
 
 // The 32-row two-launch path (records, then the scan) for this BV, unless
 // another kernel is asked for.

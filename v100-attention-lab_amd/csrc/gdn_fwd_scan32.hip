@@ -10,28 +10,29 @@
 //   S' = e^{bC} S + K^T diag(e^{bC - b}) u  (the reference's h(e^{bC} I -
 //        Wbar^T K) + Ubar^T K, gdn_ref.py:93-98, without the K x K temporary)
 // Only u, o and S' involve the carried state.  A V-slice workgroup of the
-// fused kernel would rebuild A and P and rerun the 32-row substitution for T
-// once per slice; here they run once per (chunk, head):
+// fused kernel would rebuild A and rerun the 32-row substitution for T once
+// per slice; here they run once per (chunk, head):
 //
 //   1. rec32_kernel, one wave per two (chunk, head) records: K K^T on the
 //      matrix cores, A, then T by forward substitution on the VALU (one lane
-//      per row of T, rows of A^T broadcast from LDS); Q K^T on the matrix
-//      cores for P.  Written with the gates to a 7 KB record: Tu and P (hi +
-//      lo) as MFMA operand fragments, b, e^b, e^{bC - b}, e^{bC}.
+//      per row of T, rows of A^T broadcast from LDS), written with the gates
+//      to a 3 KB record: Tu as MFMA operand fragments, b, e^b, e^{bC - b},
+//      e^{bC}.
 //   2. scan32_kernel, one workgroup per (sequence, head, BV-column slice),
 //      walks the chunks with the fp32 K x BV state in accumulator registers
 //      (no chunk state is written).  Waves have fixed roles and pass one
-//      barrier per iteration; SCAN and OUT read the next chunk's operands
-//      from LDS while they work on the current one:
+//      barrier per iteration:
 //        SCAN x BV/16  chunk it: K S, Y = V - diag(e^b) K S, u = Tu Y,
 //                      S <- e^{bC} S + K^T diag(e^{bC-b}) u (16 columns each)
 //        OUT  x BV/16  chunk it: Q S with the chunk-start state;
 //                      chunk it-1: o = scale (P u + diag(e^b) Q S), staged
 //                      through LDS so that each lane stores 8 elements of
 //                      one row
-//        LQK, LVR      chunk it+D: q and k (LQK), the v slice and the record
-//                      (LVR), copied global -> LDS by the asynchronous LDS-DMA
-//                      loads (global_load_lds_dwordx4), D chunks ahead.
+//        PQK           chunk it: P = e^{b_t-b_j} Q K^T (t >= j) as hi + lo
+//                      fp16 operand fragments
+//        LOAD          chunk it+D: q, k, the v slice and the record, copied
+//                      global -> LDS by the asynchronous LDS-DMA loads
+//                      (global_load_lds_dwordx4), D chunks ahead.
 //
 // The records of a segment of L chunks per (sequence, head) live in the
 // caller's workspace; a sequence longer than L chunks runs as several
@@ -51,15 +52,14 @@ namespace s32 {
 using namespace pipe;
 
 constexpr int C = 32;
-constexpr int D = 4;  // chunks loaded ahead by the loader waves
-constexpr int REC_BYTES = 7168;
+constexpr int D = 4;  // chunks loaded ahead by the LOAD wave
+constexpr int REC_BYTES = 3072;
 // record layout (byte offsets)
 constexpr int R_TU = 0;     // f16x8 [2][64]: Tu rows 16 mt + (lane & 15), columns pi(lane >> 4, s)
-constexpr int R_P = 2048;   // f16x8 [2 (hi, lo)][2][64]: P operand fragments (rows t of tile mt)
-constexpr int R_B = 6144;   // float [32]: in-chunk cumsum b (flat past the sequence end)
-constexpr int R_EB = 6272;  // float [32]: e^b
-constexpr int R_EC = 6400;  // float [32]: e^{bC - b}
-constexpr int R_EBC = 6528; // float: e^{bC}
+constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b (flat past the sequence end)
+constexpr int R_EB = 2176;  // float [32]: e^b
+constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
+constexpr int R_EBC = 2432; // float: e^{bC}
 
 struct SArgs {
   const void* q;
@@ -136,16 +136,15 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   // the two records of this wave: geometry (wave-uniform)
   int nval[2];
   const char* kh[2];
-  const char* qh[2];
   char* rp[2];
-  uint32_t skb[2], sqb[2];
+  uint32_t skb[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int r = (blockIdx.x * 4 + wave) * 2 + e;
     nval[e] = 0;
-    kh[e] = qh[e] = nullptr;
+    kh[e] = nullptr;
     rp[e] = nullptr;
-    skb[e] = sqb[e] = 0;
+    skb[e] = 0;
     if (r < p.nrec) {
       int bi, hi, lc;
       rec_coords(p, r, bi, hi, lc);
@@ -154,17 +153,14 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
       if (t0 < rs.T) {
         nval[e] = min(C, rs.T - t0);
         kh[e] = static_cast<const char*>(p.k) + (head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1]) * EB;
-        qh[e] = static_cast<const char*>(p.q) + (head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1]) * EB;
         skb[e] = (uint32_t)p.sk[1] * EB;
-        sqb[e] = (uint32_t)p.sq[1] * EB;
         rp[e] = p.rec + (int64_t)r * REC_BYTES;
       }
     }
   }
-  // k and q rows (rows past the end re-read the last row: finite values
-  // whose beta is zero and whose o rows are not stored), then the gates of
-  // row c of record `half`
-  uint4 kr[2][2][KB], qr[2][2][KB];
+  // k rows (rows past the end re-read the last row: finite values whose
+  // beta is zero), then the gates of row c of record `half`
+  uint4 kr[2][2][KB];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (nval[e] > 0) {
@@ -174,7 +170,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
         for (int kb = 0; kb < KB; ++kb) {
           const int rr = min(16 * mt + n, nval[e] - 1);
           kr[e][mt][kb] = ld16(kh[e], (uint32_t)rr * skb[e] + (32 * kb + 8 * gq) * EB);
-          qr[e][mt][kb] = ld16(qh[e], (uint32_t)rr * sqb[e] + (32 * kb + 8 * gq) * EB);
         }
     }
   }
@@ -238,37 +233,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
           }
           *reinterpret_cast<f32x4*>(sa + jj * C + 16 * mt + 4 * gq) = av;
         }
-      // P = e^{b_t - b_j} Q K^T (t >= j) as fp16 hi + lo operand fragments:
-      // the P^T tiles K Q^T of rows j in [0, 16) and [16, 32) of column
-      // tile mt form the operand of rows t of tile mt.
-      f16x8 qf[2][KB];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) qf[mt][kb] = to_f16x8<TIn>(qr[e][mt][kb]);
-      f16x8* pr = reinterpret_cast<f16x8*>(rp[e] + R_P);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int t = 16 * mt + n;
-        const float bt = s_b[wave][e][t];
-        f32x4 pt[2] = {z4, z4};
-#pragma unroll
-        for (int a = 0; a <= mt; ++a) {
-          f32x4 acc = z4;
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb) acc = Mma<f16>::mma(kf[a][kb], qf[mt][kb], acc);
-          const f32x4 bj4 = *reinterpret_cast<const f32x4*>(&s_b[wave][e][16 * a + 4 * gq]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            // mask folded into the exponent: 2^-inf = 0
-            const float x = t >= 16 * a + 4 * gq + i ? bt - bj4[i] : -__builtin_inff();
-            pt[a][i] = pin(acc[i] * fexp(x));
-          }
-        }
-        const f16x8 ph = Mma<f16>::from_acc(pt[0], pt[1]);
-        pr[mt * 64 + lane] = ph;
-        pr[128 + mt * 64 + lane] = split_lo(pt[0], pt[1], ph);
-      }
     }
   }
   __builtin_amdgcn_wave_barrier();
@@ -314,37 +278,18 @@ constexpr int OT_PITCH = 20;  // floats per row of an o staging tile (16 + 4: ro
 template <int K, int BV>
 struct alignas(16) ScanSmem {
   static constexpr int NSW = BV / 16;
-  // q, k, v and record slots.  Chunk c is complete in LDS at barrier c - 2
-  // and read during iterations c - 1 (SCAN's and OUT's prefetch) and c
-  // (OUT's P and e^b); its slot is refilled by the copy of chunk c + R,
-  // issued in iteration c + R - D = c + 1, after barrier c.
-  static constexpr int R = D + 1;
+  static constexpr int R = D + 1;   // q, k, v slots: read in the chunk's own iteration
+  static constexpr int RR = D + 2;  // record slots: e^b is read once more by OUT
   f16x8 rq[R][C][K / 8];            // q rows, 16-byte piece c of row r at swz(r, c)
   f16x8 rk[R][C][K / 8];            // k rows, likewise
   f16x8 rv[R][C][BV / 8];           // v slice rows (plain)
-  char rec[R][REC_BYTES];
+  char rec[RR][REC_BYTES];
+  f16x8 p[2][2][64];                // P operand fragments, hi
+  f16x8 plo[2][2][64];              // and the fp16 residual
   f16x8 so[2][NSW][K / 32][64];     // chunk-start state as B operand fragments
   f16x8 uo[2][NSW][2][64];          // u as hi + lo
   float ot[NSW][C][OT_PITCH];       // o tile of each OUT wave, for row-contiguous stores
 };
-
-template <int BV>
-constexpr int scan_waves() {
-  return 2 * (BV / 16) + 2;
-}
-
-enum ScanRole { SR_SCAN, SR_OUT, SR_LQK, SR_LVR };
-
-// LDS-DMA copies per chunk of the two loader waves: q and k (1 KB each);
-// the v slice and the record.
-template <int K>
-constexpr int dma_qk() {
-  return 2 * (C * K * 2 / 1024);
-}
-template <int BV>
-constexpr int dma_vr() {
-  return (C * BV * 2 + 1023) / 1024 + REC_BYTES / 1024;
-}
 
 // 8 consecutive o elements (two f32x4) at o + off, aligned for a 16-byte
 // (16-bit o) or two 16-byte (fp32 o) stores.
@@ -363,25 +308,18 @@ __device__ __forceinline__ void store_o8(void* o, int64_t off, const f32x4& w0, 
   }
 }
 
-// Operands of one chunk for a SCAN wave, read from LDS one iteration ahead
-// (K^T, needed last, is read in the chunk's own iteration).
-template <int K>
-struct ScanOps {
-  f16x8 kR[2][K / 32];  // K rows (A operand of K S)
-  f16x4 va, vb;         // v rows 4 gq + i and 16 + 4 gq + i of this lane's column
-  f16x8 tu0, tu1;       // Tu operand fragments
-  f32x4 eb_lo, eb_hi, ec_lo, ec_hi;
-  float ebC;
-};
+template <int BV>
+constexpr int scan_waves() {
+  return 2 * (BV / 16) + 2;
+}
 
-// Operands of an OUT wave for iteration it: q rows of chunk it, P and e^b
-// of chunk it - 1.
-template <int K>
-struct OutOps {
-  f16x8 qA[2][K / 32];
-  f16x8 pH[2], pL[2];
-  f32x4 eb[2];
-};
+enum ScanRole { SR_SCAN, SR_OUT, SR_PQK, SR_LOAD };
+
+// DMA copies per chunk: q and k (1 KB each), the v slice, the record.
+template <int K, int BV>
+constexpr int dma_per_chunk() {
+  return 2 * (C * K * 2 / 1024) + (C * BV * 2 + 1023) / 1024 + REC_BYTES / 1024;
+}
 
 template <typename TIn, int K, int BV>
 __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SArgs p) {
@@ -389,11 +327,11 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   using S = ScanSmem<K, BV>;
   constexpr int NSW = BV / 16;
   constexpr int KB = K / 32, KT = K / 16;
-  constexpr int R = S::R;
-  constexpr int NQK = dma_qk<K>(), NVR = dma_vr<BV>();
+  constexpr int R = S::R, RR = S::RR;
+  constexpr int ND = dma_per_chunk<K, BV>();
   static_assert(sizeof(TIn) == 2, "16-bit inputs");
-  static_assert((D - 1) * NQK < 64 && (D - 1) * NVR < 64, "outstanding DMA copies fit vmcnt");
-  static_assert(C * BV * 2 % 1024 == 0 && REC_BYTES % 1024 == 0, "whole DMA copies");
+  static_assert((D - 1) * ND < 64, "outstanding DMA copies fit vmcnt");
+  static_assert(C * BV * 2 % 1024 == 0, "v slice rows fill whole DMA copies");
 
   __shared__ S s;
 
@@ -435,10 +373,10 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     role = SR_OUT;
     ridx = wave - NSW;
   } else if (wave == 2 * NSW) {
-    role = SR_LQK;
+    role = SR_PQK;
     ridx = 0;
   } else {
-    role = SR_LVR;
+    role = SR_LOAD;
     ridx = 0;
   }
 
@@ -468,36 +406,17 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
       s.so[0][cb][kb][lane] = sB[kb];
     }
-    const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
-    // operands of chunk it (slot it % R), read from LDS
-    auto load_ops = [&](ScanOps<K>& o, int it) {
+    if (nloc > 0) wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
       const int sl = it % R;
-      const char* rc = s.rec[sl];
+      const char* rc = s.rec[it % RR];
+      f16x8 kR[2][KB], kA[KT];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) o.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
-      // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
-      const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
-      const int vc = (16 * cb + 4 * (n & 3)) * 2;
-      o.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
-      o.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
-      const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
-      o.tu0 = tu[lane];
-      o.tu1 = tu[64 + lane];
-      const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
-      const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
-      o.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
-      o.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
-      o.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
-      o.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
-      o.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
-    };
-    // chunk it with its operands (read during iteration it - 1)
-    auto step = [&](const ScanOps<K>& o, int it) {
-      // K^T of chunk it by transposing reads: row rho of the state, rows t
-      const char* kbase = reinterpret_cast<const char*>(s.rk[it % R]);
-      f16x8 kA[KT];
+        for (int kb = 0; kb < KB; ++kb) kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+      const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
+      const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
 #pragma unroll
       for (int r = 0; r < KT; ++r) {
         const int piece = 4 * (r >> 1) + (n & 3);
@@ -505,25 +424,39 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
         kA[r] = cat8(lo, hi4);
       }
+      // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
+      const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
+      const int vc = (16 * cb + 4 * (n & 3)) * 2;
+      const f16x4 va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+      const f16x4 vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+      const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
+      const f16x8 tu0 = tu[lane], tu1 = tu[64 + lane];
+      const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
+      const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
+      const f32x4 eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+      const f32x4 eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+      const f32x4 ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+      const f32x4 ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+      const float ebC = *reinterpret_cast<const float*>(rc + R_EBC);
       // K S: rows t, so its two row tiles form a B operand over t
       f32x4 ks[2] = {z4, z4};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(o.kR[mt][kb], sB[kb], ks[mt]);
+        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(kR[mt][kb], sB[kb], ks[mt]);
       f32x4 y0, y1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
-        y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
+        y0[i] = (float)va[i] - eb_lo[i] * ks[0][i];
+        y1[i] = (float)vb[i] - eb_hi[i] * ks[1][i];
       }
       const f16x8 yB = M::from_acc(y0, y1);
       f32x4 u[2];
-      u[0] = M::mma(o.tu0, yB, z4);
-      u[1] = M::mma(o.tu1, yB, z4);
-      const f16x8 utB = M::from_acc(u[0] * o.ec_lo, u[1] * o.ec_hi);
+      u[0] = M::mma(tu0, yB, z4);
+      u[1] = M::mma(tu1, yB, z4);
+      const f16x8 utB = M::from_acc(u[0] * ec_lo, u[1] * ec_hi);
 #pragma unroll
-      for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * o.ebC);
+      for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * ebC);
       {
         const f16x8 uh = M::from_acc(u[0], u[1]);
         s.uo[it & 1][cb][0][lane] = uh;
@@ -535,18 +468,6 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
       }
       wg_barrier();
-    };
-    if (nloc > 0) {
-      wg_barrier();  // chunks 0 and 1 are in LDS
-      ScanOps<K> opA, opB;
-      load_ops(opA, 0);
-      for (int it = 0; it < nloc; it += 2) {
-        if (it + 1 < nloc) load_ops(opB, it + 1);
-        step(opA, it);
-        if (it + 1 >= nloc) break;
-        if (it + 2 < nloc) load_ops(opA, it + 2);
-        step(opB, it + 1);
-      }
     }
     float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
 #pragma unroll
@@ -558,10 +479,24 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   } else if (role == SR_OUT) {
     // ================================================================ OUT
     const int c2 = ridx;
-    const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2;
-    // o of chunk c (rows past T are not stored)
-    auto emit = [&](const f32x4 (&ov)[2], int c) {
-      const int t0 = (p.c0 + c) * C;
+    f32x4 oq[2] = {z4, z4};
+    auto store_chunk = [&](int it) {
+      const f16x8 uh = s.uo[it & 1][c2][0][lane];
+      const f16x8 ul = s.uo[it & 1][c2][1][lane];
+      const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
+      const f32x4 ebv[2] = {*reinterpret_cast<const f32x4*>(ebr + 4 * gq),
+                            *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq)};
+      f32x4 ov[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const f16x8 pA = s.p[it & 1][mt][lane], pL = s.plo[it & 1][mt][lane];
+        f32x4 pu = M::mma(pA, ul, z4);
+        pu = M::mma(pL, uh, pu);
+        pu = M::mma(pA, uh, pu);
+        ov[mt] = (pu + ebv[mt] * oq[mt]) * p.scale;
+      }
+      const int t0 = (p.c0 + it) * C;
+      const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2;
       if (p.o_vec) {
         // through this wave's LDS tile: lane -> row lane / 2, 8 columns
         float(*const ot)[OT_PITCH] = s.ot[c2];
@@ -581,151 +516,122 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
           else
             store_o8<float>(p.o, off, w0, w1);
         }
+      } else if (p.o_dtype == GDN_DTYPE_F16) {
+        store_o<f16>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
+      } else if (p.o_dtype == GDN_DTYPE_BF16) {
+        store_o<bf16_t>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
       } else {
-        if (p.o_dtype == GDN_DTYPE_F16)
-          store_o<f16>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
-        else if (p.o_dtype == GDN_DTYPE_BF16)
-          store_o<bf16_t>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
-        else
-          store_o<float>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
+        store_o<float>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
       }
     };
-    // q rows of chunk c into o.qA
-    auto load_q = [&](OutOps<K>& o, int c) {
-      const int sl = c % R;
+    wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      if (it >= 1) store_chunk(it - 1);
+      const int sl = it % R;
+      f16x8 qA[2][KB];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) o.qA[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
-    };
-    // P and e^b of chunk c into o
-    auto load_pe = [&](OutOps<K>& o, int c) {
-      const char* rc = s.rec[c % R];
-      const f16x8* pr = reinterpret_cast<const f16x8*>(rc + R_P);
-      const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        o.pH[mt] = pr[mt * 64 + lane];
-        o.pL[mt] = pr[128 + mt * 64 + lane];
-        o.eb[mt] = *reinterpret_cast<const f32x4*>(ebr + 16 * mt + 4 * gq);
-      }
-    };
-    f32x4 oq[2] = {z4, z4};  // Q S of the previous chunk
-    // o of chunk c - 1 from u (written by SCAN in iteration c - 1), P and
-    // e^b of chunk c - 1 (in o) and its Q S (oq)
-    auto finish = [&](const OutOps<K>& o, int c) {
-      const f16x8 uh = s.uo[c & 1][c2][0][lane];
-      const f16x8 ul = s.uo[c & 1][c2][1][lane];
-      f32x4 ov[2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        f32x4 pu = M::mma(o.pH[mt], ul, z4);
-        pu = M::mma(o.pL[mt], uh, pu);
-        pu = M::mma(o.pH[mt], uh, pu);
-        ov[mt] = (pu + o.eb[mt] * oq[mt]) * p.scale;
-      }
-      emit(ov, c);
-    };
-    // iteration it: Q S of chunk it (state written by SCAN in it - 1), o of
-    // chunk it - 1; prefetch q of chunk it + 1 and P, e^b of chunk it
-    auto step = [&](const OutOps<K>& cur, OutOps<K>& nxt, int it) {
-      f16x8 sOp[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sOp[kb] = s.so[it & 1][c2][kb][lane];
-      if (it + 1 < nloc) load_q(nxt, it + 1);
-      load_pe(nxt, it);
-      f32x4 oqn[2];
+        for (int kb = 0; kb < KB; ++kb) qA[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         f32x4 acc = z4;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) acc = M::mma(cur.qA[mt][kb], sOp[kb], acc);
-        oqn[mt] = acc;
+        for (int kb = 0; kb < KB; ++kb) acc = M::mma(qA[mt][kb], s.so[it & 1][c2][kb][lane], acc);
+        oq[mt] = acc;
       }
-      if (it >= 1) finish(cur, it - 1);
-      oq[0] = oqn[0];
-      oq[1] = oqn[1];
       wg_barrier();
-    };
-    wg_barrier();  // chunks 0 and 1 are in LDS
-    OutOps<K> opA, opB;
-    load_q(opA, 0);
-    for (int it = 0; it < nloc; it += 2) {
-      step(opA, opB, it);
-      if (it + 1 >= nloc) {
-        finish(opB, it);
-        break;
+    }
+    store_chunk(nloc - 1);
+  } else if (role == SR_PQK) {
+    // ================================================================ PQK
+    wg_barrier();
+    for (int it = 0; it < nloc; ++it) {
+      const int sl = it % R;
+      const float* bb = reinterpret_cast<const float*>(s.rec[it % RR] + R_B);
+      f16x8 qf[2][KB], kf[2][KB];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          qf[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+          kf[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+        }
+      // P^T tiles (rows j, columns t) = K Q^T: the tiles of rows j in
+      // [0,16) and [16,32) of one column tile form one P operand
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int t = 16 * mt + n;
+        const float bt = bb[t];
+        f32x4 pt[2] = {z4, z4};
+#pragma unroll
+        for (int a = 0; a <= mt; ++a) {
+          f32x4 acc = z4;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) acc = M::mma(kf[a][kb], qf[mt][kb], acc);
+          const f32x4 bj4 = *reinterpret_cast<const f32x4*>(bb + 16 * a + 4 * gq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // mask folded into the exponent: 2^-inf = 0
+            const float x = t >= 16 * a + 4 * gq + i ? bt - bj4[i] : -__builtin_inff();
+            pt[a][i] = pin(acc[i] * fexp(x));
+          }
+        }
+        const f16x8 ph = M::from_acc(pt[0], pt[1]);
+        s.p[it & 1][mt][lane] = ph;
+        s.plo[it & 1][mt][lane] = split_lo(pt[0], pt[1], ph);
       }
-      step(opB, opA, it + 1);
-      if (it + 2 >= nloc) finish(opA, it + 1);
+      wg_barrier();
     }
   } else {
-    // ====================================================== LQK and LVR
-    // chunk j -> slot j % R.  Rows past the end re-read the last row (finite
-    // values that the record's zero beta and the masks cancel).  LQK copies
-    // q and k, LVR the v slice and the record; each wave counts its own
-    // copies in vmcnt.
+    // =============================================================== LOAD
+    // chunk j -> slots j % R (q, k, v) and j % RR (record).  Rows past the
+    // end re-read the last row (finite values that the record's zero beta
+    // and the masks cancel).
     constexpr int RCH = K / 8;               // 16-byte pieces per q / k row
     constexpr int NQ = C * RCH / 64;         // DMA copies per q / k tile
     constexpr int VCH = BV / 8;              // pieces per v row
     constexpr int NV = C * VCH / 64;         // DMA copies per v tile
-    const bool qk = role == SR_LQK;
     auto issue = [&](int it) {
       const int j = p.c0 + it;
       const int row0 = j * C;
       const int last = T - 1 - row0;          // rows > last re-read row last
+      const char* qb = qh + (int64_t)row0 * sqb;
+      const char* kb = kh + (int64_t)row0 * skb;
+      const char* vb = vh + (int64_t)row0 * svb;
       const int sl = it % R;
-      if (qk) {
-        const char* qb = qh + (int64_t)row0 * sqb;
-        const char* kb = kh + (int64_t)row0 * skb;
 #pragma unroll
-        for (int i = 0; i < NQ; ++i) {
-          const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
-          const uint32_t rr = (uint32_t)min(r, last);
-          dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
-          dma16(kb + rr * skb + cc * 16, &s.rk[sl][0][0] + 64 * i);
-        }
-      } else {
-        const char* vb = vh + (int64_t)row0 * svb;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int pc = 64 * i + lane, r = pc / VCH, cc = pc % VCH;
-          const uint32_t rr = (uint32_t)min(r, last);
-          dma16(vb + rr * svb + cc * 16, &s.rv[sl][0][0] + 64 * i);
-        }
-        const char* rsrc = rech + (int64_t)it * REC_BYTES;
-#pragma unroll
-        for (int i = 0; i < REC_BYTES / 1024; ++i) dma16(rsrc + 1024 * i + 16 * lane, s.rec[sl] + 1024 * i);
+      for (int i = 0; i < NQ; ++i) {
+        const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
+        const uint32_t rr = (uint32_t)min(r, last);
+        dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
+        dma16(kb + rr * skb + cc * 16, &s.rk[sl][0][0] + 64 * i);
       }
-    };
-    // wait until at most `ahead` chunks of this wave's copies are in flight
-    auto wait_ahead = [&](int ahead) {
-      if (qk) {
-        if (ahead >= 2)
-          wait_vm<2 * NQK>();
-        else if (ahead == 1)
-          wait_vm<NQK>();
-        else
-          wait_vm<0>();
-      } else {
-        if (ahead >= 2)
-          wait_vm<2 * NVR>();
-        else if (ahead == 1)
-          wait_vm<NVR>();
-        else
-          wait_vm<0>();
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int pc = 64 * i + lane, r = pc / VCH, cc = pc % VCH;
+        const uint32_t rr = (uint32_t)min(r, last);
+        dma16(vb + rr * svb + cc * 16, &s.rv[sl][0][0] + 64 * i);
       }
+      const char* rsrc = rech + (int64_t)it * REC_BYTES;
+#pragma unroll
+      for (int i = 0; i < REC_BYTES / 1024; ++i) dma16(rsrc + 1024 * i + 16 * lane, s.rec[it % RR] + 1024 * i);
     };
-    static_assert(D == 4, "wait_ahead covers at most two chunks beyond the one waited for");
     for (int it = 0; it < D; ++it)
       if (it < nloc) issue(it);
-    // chunks 0 and 1 complete at the first barrier
-    wait_ahead(min(D, nloc) - 2);
+    if (nloc >= D)
+      wait_vm<(D - 1) * ND>();
+    else
+      wait_vm<0>();
     wg_barrier();
     for (int it = 0; it < nloc; ++it) {
-      // chunk it + 2 must be in LDS at this iteration's barrier
-      if (it + D < nloc) issue(it + D);
-      wait_ahead(min(it + D, nloc - 1) - (it + 2));
+      // chunk it + 1 must be in LDS at this iteration's barrier
+      if (it + D < nloc) {
+        issue(it + D);
+        wait_vm<(D - 1) * ND>();
+      } else {
+        wait_vm<0>();
+      }
       wg_barrier();
     }
   }

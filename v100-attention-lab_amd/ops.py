@@ -294,7 +294,7 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         ``final_state[i]`` (h0 and final_state are then ``[N, H, K, V]``).
       max_segment_chunks: for the two-launch 32-row path, the records of at
         most this many chunks per sequence are held at once; a longer
-        sequence runs as several segments (default: 128 chunks).
+        sequence runs as several segments (default: 256 chunks).
 
     Returns:
       ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.  When an
