@@ -247,6 +247,79 @@ def load_traffic(config):
         return None
 
 
+def phase_stamps(pkg, config):
+    """MFMA utilisation of the contraction phases, from the measurement build
+    (``build.py --phase-stamps``: the same kernels with s_memtime stamps around
+    each MFMA phase, summed per wave).  Per phase: MFMA count x the cycles one
+    MFMA keeps a SIMD busy (measured by the build's probe: 256 workgroups of
+    four waves, four independent accumulators each) / the phase's stamped
+    cycles, on the SIMDs that run it.  The scan's phases are K S -> u -> state
+    update (SCAN), Q S and P u (OUT), Q K^T with the decay mask (P); the record
+    kernel's is K K^T with A's gates and mask."""
+    import ctypes
+    import numpy as np
+    bmod = importlib.import_module("v100-attention-lab_amd.build")
+    lib = pkg.load_library(bmod.STAMPS_LIB_PATH)  # first load of this process
+    lib.gdn_phase_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.gdn_phase_mfma_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = torch.empty(256 * 256, device=dev)
+    cyc = torch.zeros(1024, dtype=torch.int64, device=dev)
+    for _ in range(3):
+        assert lib.gdn_phase_mfma_probe(out.data_ptr(), cyc.data_ptr(), 256, 2000, stream) == 0
+    torch.cuda.synchronize()
+    cyc_mfma = float(cyc.double().median()) / (4 * 2000)
+
+    B, T, H, K, V, dtype, C, with_h0 = CONFIGS[config]
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
+    step = lambda: pkg.gdn_fwd(q, k, v, g, beta, h0, scale=1.0, chunk_size=C)
+    ms = time_steps(step, 20, 5)
+    assert lib.gdn_phase_clear() == 0
+    step()
+    torch.cuda.synchronize()
+    scan = np.zeros(1024 * 8 * 8, dtype=np.uint64)
+    rec = np.zeros(16384 * 4, dtype=np.uint64)
+    assert lib.gdn_phase_read(scan.ctypes.data, rec.ctypes.data) == 0
+    scan = scan.reshape(1024, 8, 8).astype(np.float64)
+    rec = rec.reshape(16384, 4).astype(np.float64)
+    if not (scan[:, :, 0] > 0).any():
+        raise RuntimeError(f"{config}: no stamps recorded (the two-launch 32-row path did not run)")
+    phases = {}
+    for role, names in ((1, ("SCAN: K S, u, state update", None)), (2, ("OUT: Q S", "OUT: P u")),
+                        (3, ("P: Q K^T, decay, mask", None))):
+        d = scan[scan[:, :, 0] == role]
+        for col, name in enumerate(names):
+            if name is None:
+                continue
+            window = float(d[:, 2 + col].sum())
+            mfma = float((d[:, 4 + col] * d[:, 1]).sum())
+            phases[name] = {"waves": int(len(d)), "mfma": int(mfma), "busy_cycles": mfma * cyc_mfma,
+                            "window_cycles": window}
+    r = rec[rec[:, 0] > 0]
+    phases["records: K K^T, A"] = {"waves": int(len(r)), "mfma": int(r[:, 2].sum()),
+                                   "busy_cycles": float(r[:, 2].sum()) * cyc_mfma,
+                                   "window_cycles": float(r[:, 1].sum())}
+    for ph in phases.values():
+        ph["util"] = round(ph["busy_cycles"] / ph["window_cycles"], 4)
+    scan_names = [n for n in phases if not n.startswith("records")]
+    busy = sum(phases[n]["busy_cycles"] for n in scan_names)
+    win = sum(phases[n]["window_cycles"] for n in scan_names)
+    busy_all = busy + phases["records: K K^T, A"]["busy_cycles"]
+    win_all = win + phases["records: K K^T, A"]["window_cycles"]
+    for ph in phases.values():
+        ph["busy_cycles"] = round(ph["busy_cycles"])
+        ph["window_cycles"] = round(ph["window_cycles"])
+    print(json.dumps({"metric": "MFMA utilisation of the contraction phases (s_memtime phase windows)",
+                      "config": config, "B": B, "T": T, "H": H, "K": K, "V": V, "chunk_size": C,
+                      "mfma_cycles_per_instruction": round(cyc_mfma, 3),
+                      "stamped_ms_per_step": round(ms, 5),
+                      "scan_contraction_util": round(busy / win, 4),
+                      "all_contraction_util": round(busy_all / win_all, 4),
+                      "phases": phases}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +332,9 @@ def main():
                          "preparation; bwd: only the backward (gdn_bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="MFMA utilisation of the contraction phases from the stamps build "
+                         "(lib/libgdn_mi355x_stamps.so, built by build.py --phase-stamps)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (scale for rocprof byte counters)")
     args = ap.parse_args()
@@ -285,6 +361,9 @@ def main():
         return
 
     pkg = importlib.import_module("v100-attention-lab_amd")
+    if args.phase_stamps:
+        phase_stamps(pkg, args.config)
+        return
     dev = torch.device("cuda:0")
     B, T, H, K, V, dtype, C, with_h0 = CONFIGS[args.config]
     if args.workload == "prep":

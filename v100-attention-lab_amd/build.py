@@ -25,6 +25,10 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+# The same sources with -DGDN_PHASE_STAMPS: the 32-row scan and record kernels
+# sum s_memtime windows of their MFMA phases (bench.py --phase-stamps reads
+# them).  A measurement build only; the product never loads it.
+STAMPS_LIB_PATH = os.path.join(LIB_DIR, "libgdn_mi355x_stamps.so")
 
 ARCH = "gfx950"
 
@@ -61,15 +65,20 @@ def _filtered(stderr: str) -> str:
     return "\n".join(l for l in stderr.splitlines() if noise not in l)
 
 
-def build(verbose: bool = True, extra_flags=None) -> str:
-    """Compile the HIP sources into ``lib/libgdn_mi355x.so``; returns its path."""
+def build(verbose: bool = True, extra_flags=None, phase_stamps: bool = False) -> str:
+    """Compile the HIP sources into ``lib/libgdn_mi355x.so`` (or, with
+    ``phase_stamps``, the measurement build ``lib/libgdn_mi355x_stamps.so``);
+    returns its path."""
+    obj_dir = OBJ_DIR + ("_stamps" if phase_stamps else "")
+    lib_path = STAMPS_LIB_PATH if phase_stamps else LIB_PATH
+    extra_flags = list(extra_flags or []) + (["-DGDN_PHASE_STAMPS"] if phase_stamps else [])
     os.makedirs(LIB_DIR, exist_ok=True)
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(obj_dir, exist_ok=True)
     t0 = time.time()
     procs = []
     objs = []
     for src in SOURCES:
-        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
         cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *(extra_flags or []),
                f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
@@ -87,16 +96,16 @@ def build(verbose: bool = True, extra_flags=None) -> str:
             print(err, file=sys.stderr)
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
-    tmp = LIB_PATH + ".tmp"
+    tmp = lib_path + ".tmp"
     link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed ({res.returncode}):\n{_filtered(res.stderr)}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"[build] {LIB_PATH} ({time.time() - t0:.1f} s)", flush=True)
-    return LIB_PATH
+        print(f"[build] {lib_path} ({time.time() - t0:.1f} s)", flush=True)
+    return lib_path
 
 
 if __name__ == "__main__":
-    build()
+    build(phase_stamps="--phase-stamps" in sys.argv[1:])

@@ -106,6 +106,73 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
 }
 
 // ---------------------------------------------------------------------------
+// Phase stamps.  Built only with -DGDN_PHASE_STAMPS (build.py --phase-stamps,
+// a separate library used by bench.py --phase-stamps): each MFMA phase is
+// bracketed by s_memtime stamps, the first taken once the phase's operands
+// are in registers (the stamp waits for outstanding LDS loads), the second
+// once its results are, and the windows are summed per wave.  Dividing the
+// phase's MFMA count times the measured cycles of one MFMA by the window
+// gives the MFMA utilisation of the contraction phases on the SIMDs that
+// run them.  The product library compiles none of this.
+// ---------------------------------------------------------------------------
+
+#ifdef GDN_PHASE_STAMPS
+constexpr int PS_SLOTS = 8;                // counters per (workgroup, wave)
+constexpr int PS_WG = 1024, PS_WAVES = 8;  // scan workgroups and waves recorded
+constexpr int PS_REC = 16384;              // record-kernel waves recorded
+__device__ unsigned long long g_phase_scan[PS_WG * PS_WAVES * PS_SLOTS];
+__device__ unsigned long long g_phase_rec[PS_REC * 4];
+
+// s_memtime once the given registers hold their values; the asm also
+// "modifies" them, so no consumer is moved above the stamp.
+template <typename A>
+__device__ __forceinline__ unsigned long long ps_stamp(A& a) {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(a) :: "memory");
+  return t;
+}
+template <typename A, typename B>
+__device__ __forceinline__ unsigned long long ps_stamp(A& a, B& b) {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(a), "+v"(b) :: "memory");
+  return t;
+}
+template <typename A, typename B, typename Cc>
+__device__ __forceinline__ unsigned long long ps_stamp(A& a, B& b, Cc& c) {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(a), "+v"(b), "+v"(c) :: "memory");
+  return t;
+}
+template <typename A, typename B, typename Cc, typename Dd>
+__device__ __forceinline__ unsigned long long ps_stamp(A& a, B& b, Cc& c, Dd& d) {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
+  return t;
+}
+// slots of (workgroup, wave): role, chunks, window A, window B, MFMAs per
+// window A, per window B
+__device__ __forceinline__ void ps_record(int wave, int lane, unsigned long long role, unsigned long long n,
+                                          unsigned long long wa, unsigned long long wb, unsigned long long ma,
+                                          unsigned long long mb) {
+  if (lane == 0 && blockIdx.x < PS_WG && wave < PS_WAVES) {
+    unsigned long long* d = g_phase_scan + ((int64_t)blockIdx.x * PS_WAVES + wave) * PS_SLOTS;
+    d[0] = role; d[1] = n; d[2] = wa; d[3] = wb; d[4] = ma; d[5] = mb;
+  }
+}
+#define PS_DECL unsigned long long ps_a = 0, ps_b = 0, ps_t0 = 0
+#define PS_BEGIN(...) ps_t0 = ps_stamp(__VA_ARGS__)
+#define PS_END_A(...) ps_a += ps_stamp(__VA_ARGS__) - ps_t0
+#define PS_END_B(...) ps_b += ps_stamp(__VA_ARGS__) - ps_t0
+#define PS_RECORD(role, n, ma, mb) ps_record(wave, lane, role, n, ps_a, ps_b, ma, mb)
+#else
+#define PS_DECL
+#define PS_BEGIN(...)
+#define PS_END_A(...)
+#define PS_END_B(...)
+#define PS_RECORD(role, n, ma, mb)
+#endif
+
+// ---------------------------------------------------------------------------
 // 1. records
 // ---------------------------------------------------------------------------
 
@@ -204,9 +271,16 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   // A = beta_t e^{b_t - b_j} K K^T (t > j), stored as A^T
+#ifdef GDN_PHASE_STAMPS
+  unsigned long long ps_r0 = ps_stamp(kr[0][0][0].x, kr[1][0][0].x);
+  int ps_n = 0;
+#endif
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (nval[e] > 0) {
+#ifdef GDN_PHASE_STAMPS
+      ps_n += 3 * KB;
+#endif
       f16x8 kf[2][KB];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -237,6 +311,18 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#ifdef GDN_PHASE_STAMPS
+  {
+    unsigned long long ps_r1;
+    asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(ps_r1) :: "memory");
+    const int w = blockIdx.x * 4 + wave;
+    if (lane == 0 && w < PS_REC) {
+      g_phase_rec[4 * w] = 1;
+      g_phase_rec[4 * w + 1] = ps_r1 - ps_r0;
+      g_phase_rec[4 * w + 2] = ps_n;
+    }
+  }
+#endif
 
   // T by substitution: lane c of half h holds row c of T of record h
   float xc[C];
@@ -406,6 +492,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
       s.so[0][cb][kb][lane] = sB[kb];
     }
+    PS_DECL;
     if (nloc > 0) wg_barrier();
     for (int it = 0; it < nloc; ++it) {
       const int sl = it % R;
@@ -440,6 +527,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       const float ebC = *reinterpret_cast<const float*>(rc + R_EBC);
       // K S: rows t, so its two row tiles form a B operand over t
       f32x4 ks[2] = {z4, z4};
+      PS_BEGIN(kR[0][0], kR[1][0], sB[0], kA[0]);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -463,12 +551,13 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         s.uo[it & 1][cb][1][lane] = split_lo(u[0], u[1], uh);
       }
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
-        s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
-      }
+      for (int kb = 0; kb < KB; ++kb) sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
+      PS_END_A(sB[0], sB[KB - 1]);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
       wg_barrier();
     }
+    PS_RECORD(1, nloc, 2 * KB + 2 + KT, 0);
     float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
 #pragma unroll
     for (int r = 0; r < KT; ++r)
@@ -480,21 +569,29 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     // ================================================================ OUT
     const int c2 = ridx;
     f32x4 oq[2] = {z4, z4};
+    PS_DECL;
     auto store_chunk = [&](int it) {
-      const f16x8 uh = s.uo[it & 1][c2][0][lane];
-      const f16x8 ul = s.uo[it & 1][c2][1][lane];
+      f16x8 uh = s.uo[it & 1][c2][0][lane];
+      f16x8 ul = s.uo[it & 1][c2][1][lane];
       const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
       const f32x4 ebv[2] = {*reinterpret_cast<const f32x4*>(ebr + 4 * gq),
                             *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq)};
       f32x4 ov[2];
+      f16x8 pAs[2], pLs[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const f16x8 pA = s.p[it & 1][mt][lane], pL = s.plo[it & 1][mt][lane];
-        f32x4 pu = M::mma(pA, ul, z4);
-        pu = M::mma(pL, uh, pu);
-        pu = M::mma(pA, uh, pu);
+        pAs[mt] = s.p[it & 1][mt][lane];
+        pLs[mt] = s.plo[it & 1][mt][lane];
+      }
+      PS_BEGIN(uh, ul, pAs[1], pLs[1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x4 pu = M::mma(pAs[mt], ul, z4);
+        pu = M::mma(pLs[mt], uh, pu);
+        pu = M::mma(pAs[mt], uh, pu);
         ov[mt] = (pu + ebv[mt] * oq[mt]) * p.scale;
       }
+      PS_END_B(ov[0], ov[1]);
       const int t0 = (p.c0 + it) * C;
       const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2;
       if (p.o_vec) {
@@ -533,18 +630,25 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) qA[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+      f16x8 sOp[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sOp[kb] = s.so[it & 1][c2][kb][lane];
+      PS_BEGIN(qA[0][0], qA[1][0], sOp[0], sOp[KB - 1]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         f32x4 acc = z4;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) acc = M::mma(qA[mt][kb], s.so[it & 1][c2][kb][lane], acc);
+        for (int kb = 0; kb < KB; ++kb) acc = M::mma(qA[mt][kb], sOp[kb], acc);
         oq[mt] = acc;
       }
+      PS_END_A(oq[0], oq[1]);
       wg_barrier();
     }
     store_chunk(nloc - 1);
+    PS_RECORD(2, nloc, 2 * KB, 6);
   } else if (role == SR_PQK) {
     // ================================================================ PQK
+    PS_DECL;
     wg_barrier();
     for (int it = 0; it < nloc; ++it) {
       const int sl = it % R;
@@ -559,6 +663,8 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         }
       // P^T tiles (rows j, columns t) = K Q^T: the tiles of rows j in
       // [0,16) and [16,32) of one column tile form one P operand
+      PS_BEGIN(qf[0][0], qf[1][0], kf[0][0], kf[1][0]);
+      f16x8 phs[2], pls[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         const int t = 16 * mt + n;
@@ -577,12 +683,18 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
             pt[a][i] = pin(acc[i] * fexp(x));
           }
         }
-        const f16x8 ph = M::from_acc(pt[0], pt[1]);
-        s.p[it & 1][mt][lane] = ph;
-        s.plo[it & 1][mt][lane] = split_lo(pt[0], pt[1], ph);
+        phs[mt] = M::from_acc(pt[0], pt[1]);
+        pls[mt] = split_lo(pt[0], pt[1], phs[mt]);
+      }
+      PS_END_A(phs[0], phs[1], pls[0], pls[1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        s.p[it & 1][mt][lane] = phs[mt];
+        s.plo[it & 1][mt][lane] = pls[mt];
       }
       wg_barrier();
     }
+    PS_RECORD(3, nloc, 3 * KB, 0);
   } else {
     // =============================================================== LOAD
     // chunk j -> slots j % R (q, k, v) and j % RR (record).  Rows past the
@@ -710,3 +822,57 @@ int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t str
 }
 
 }  // namespace gdn
+
+#ifdef GDN_PHASE_STAMPS
+// ---------------------------------------------------------------------------
+// MFMA rate probe of the stamps build: every wave issues `n` groups of four
+// v_mfma_f32_16x16x32_f16 on independent accumulators between two stamps,
+// so (stamped cycles) / (4 n) is the cycles one MFMA keeps a SIMD busy.
+// ---------------------------------------------------------------------------
+namespace gdn {
+__global__ __launch_bounds__(256) void phase_mfma_probe_kernel(float* out, unsigned long long* cyc, int n) {
+  using M = Mma<f16>;
+  const int lane = threadIdx.x & 63;
+  f16x8 a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (f16)(0.001f * (lane + i));
+    b[i] = (f16)(0.002f * (i - lane));
+  }
+  f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0;
+  const unsigned long long t0 = s32::ps_stamp(a, b);
+  for (int i = 0; i < n; ++i) {
+    c0 = M::mma(a, b, c0);
+    c1 = M::mma(a, b, c1);
+    c2 = M::mma(a, b, c2);
+    c3 = M::mma(a, b, c3);
+  }
+  const unsigned long long t1 = s32::ps_stamp(c0, c1, c2, c3);
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  out[w * 64 + lane] = c0[0] + c1[1] + c2[2] + c3[3];
+  if (lane == 0) cyc[w] = t1 - t0;
+}
+}  // namespace gdn
+
+extern "C" int gdn_phase_mfma_probe(float* out, unsigned long long* cyc, int blocks, int n, void* stream) {
+  hipLaunchKernelGGL(gdn::phase_mfma_probe_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, cyc, n);
+  return (int)hipGetLastError();
+}
+
+// Copies the stamp sums of the last call out: scan [1024][8][8], records [16384][4].
+extern "C" int gdn_phase_read(void* scan, void* rec) {
+  hipError_t e = hipMemcpyFromSymbol(scan, HIP_SYMBOL(gdn::s32::g_phase_scan), sizeof(gdn::s32::g_phase_scan), 0,
+                                     hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return (int)e;
+  return (int)hipMemcpyFromSymbol(rec, HIP_SYMBOL(gdn::s32::g_phase_rec), sizeof(gdn::s32::g_phase_rec), 0,
+                                  hipMemcpyDeviceToHost);
+}
+
+// Clears the stamp sums (so that waves of an earlier, larger call do not remain).
+extern "C" int gdn_phase_clear(void) {
+  static unsigned long long zs[gdn::s32::PS_WG * gdn::s32::PS_WAVES * gdn::s32::PS_SLOTS];
+  static unsigned long long zr[gdn::s32::PS_REC * 4];
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(gdn::s32::g_phase_scan), zs, sizeof(zs), 0, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return (int)e;
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(gdn::s32::g_phase_rec), zr, sizeof(zr), 0, hipMemcpyHostToDevice);
+}
+#endif
