@@ -1,0 +1,92 @@
+"""bf16 inputs outside fp16's range.
+
+bf16 q, k, v reach the matrix cores as fp16 operands.  Each workgroup scales
+its V-slice of v and h0 by a power of two chosen from their largest
+magnitude and scales o and final_state back, which is exact because o and
+the state are jointly linear in (v, h0) and every state column evolves on
+its own.  These cases would overflow fp16 (|v| up to 1e5 > 65504) or sink
+into its subnormals (|v| ~ 1e-6) without it.  Every forward kernel that
+takes bf16 is covered (the fused pipelined kernel at C = 32, the record +
+scan launches at C = 64, the phase-by-phase kernel), against the fp64 step
+recurrence at the north star's 1e-3 (max-norm relative error,
+bench_gdn.py:89-94), with fp32-stored outputs.
+"""
+
+import pytest
+import torch
+
+from oracle import gdn_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+CASES = [  # (name, chunk, kernel, K)
+    ("pipelined C=32", 32, "auto", 128),
+    ("two-launch C=64", 64, "auto", 64),
+    ("phased C=32", 32, "phased", 64),
+]
+
+
+def _inputs(B, T, H, K, V, seed, v_scale, h0_scale):
+    q, k, v, g, beta, h0 = ref.make_inputs_baseline(B, T, H, K, V, seed=seed, dtype=torch.float32,
+                                                    with_h0=True)
+    v = v * v_scale.view(1, 1, -1, 1) if torch.is_tensor(v_scale) else v * v_scale
+    h0 = h0 * h0_scale.view(1, -1, 1, 1) if torch.is_tensor(h0_scale) else h0 * h0_scale
+    bf = lambda t: t.to(torch.bfloat16)
+    return bf(q), bf(k), bf(v), g, beta, h0
+
+
+def _check(pkg, cuda, name, q, k, v, g, beta, h0, chunk, kernel, per_head=False):
+    d = lambda t: t.to(cuda)
+    print(f"[bf16 range] {name}", flush=True)
+    o, fs = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), chunk_size=chunk, kernel=kernel,
+                        output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o, fs = o.cpu(), fs.cpu()
+    assert torch.isfinite(o).all() and torch.isfinite(fs).all()
+    o_ref, h_ref = ref.recurrent(q, k, v, beta, g, ref.to_vk(h0), dtype=torch.float64)
+    h_ref = ref.to_kv(h_ref)
+    if per_head:  # each head against its own magnitude
+        for h in range(q.shape[2]):
+            eo = ref.rel_err(o_ref[:, :, h], o[:, :, h])
+            eh = ref.rel_err(h_ref[:, h], fs[:, h])
+            assert eo <= TOL and eh <= TOL, (h, eo, eh)
+    eo, eh = ref.rel_err(o_ref, o), ref.rel_err(h_ref, fs)
+    print(f"[bf16 range] {name}: o rel={eo:.3e} state rel={eh:.3e}", flush=True)
+    assert eo <= TOL and eh <= TOL
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("v_scale,h0_scale", [(1e5, 1e4), (1e-6, 1e-7), (3e4, 1e-6)])
+def test_bf16_extreme_scales(pkg, cuda, case, v_scale, h0_scale):
+    """v and h0 far outside fp16's comfortable range, one scale for all."""
+    name, chunk, kernel, K = CASES[case]
+    q, k, v, g, beta, h0 = _inputs(1, 150, 3, K, 32, 90 + case, v_scale, h0_scale)
+    _check(pkg, cuda, f"{name} v*{v_scale:g} h0*{h0_scale:g}", q, k, v, g, beta, h0, chunk, kernel)
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_bf16_per_head_scales(pkg, cuda, case):
+    """Heads whose v and h0 span 1e-6 .. 1e5: each head is checked against its
+    own magnitude (a single shift for all heads could not serve them all)."""
+    name, chunk, kernel, K = CASES[case]
+    H = 6
+    sv = torch.logspace(-6, 5, H)
+    q, k, v, g, beta, h0 = _inputs(2, 100, H, K, 32, 95 + case, sv, sv * 0.5)
+    _check(pkg, cuda, f"{name} heads 1e-6..1e5", q, k, v, g, beta, h0, chunk, kernel, per_head=True)
+
+
+def test_bf16_in_range_unchanged(pkg, cuda):
+    """Inside [2^-6, 2^10] the shift is zero, and bf16 values are exact in
+    fp16: the fused kernel on bf16 inputs then gives the bits it gives on the
+    same values in fp16."""
+    q, k, v, g, beta, h0 = _inputs(1, 200, 2, 128, 32, 97, 1.0, 1.0)
+    d = lambda t: t.to(cuda)
+    o_b, f_b = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), kernel="fused",
+                           output_dtype=torch.float32)
+    h = lambda t: d(t.to(torch.float16))
+    o_h, f_h = pkg.gdn_fwd(h(q), h(k), h(v), d(g), d(beta), d(h0), kernel="fused",
+                           output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(o_b.cpu(), o_h.cpu()) and torch.equal(f_b.cpu(), f_h.cpu())

@@ -569,14 +569,14 @@ struct Next16 {
     v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
     gate = rec[Rec16::GF + (tid & (4 * C - 1))];
   }
-  __device__ __forceinline__ void store(S16mem<K>& s, int tid) const {
+  __device__ __forceinline__ void store(S16mem<K>& s, int tid, float vsc) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
     ph.store(tid, s.ph);
     pl.store(tid, s.pl);
     q.store(tid, s.q);
     k.store(tid, s.k);
-    v.store(tid, s.vt);
+    v.store(tid, s.vt, vsc);
     s.gv[tid / C][tid % C] = gate;
   }
 };
@@ -603,11 +603,16 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   const RowSpan rs = row_span(p.cu, p.T, bi);
   const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
   const int nch = (rs.T + C - 1) / C;
-  const float scale = p.scale;
   const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
   const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
   const int64_t ob = head_base(rs, hi, p.so) + v0;
+  // bf16: this slice's v and h0 scaled into fp16's range, o and the final
+  // state scaled back (identity for fp16)
+  const RangeScale rsc = slice_range_scale<TIn>(
+      reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), rs.T, BV,
+      p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, p.scale);
+  const float scale = rsc.o;
 
   constexpr int NST = (K / 16 + 3) / 4;
   const bool upper = wave < 4;
@@ -631,7 +636,7 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         st[j][i] = (p.h0 && m0 < K)
-                       ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + (m0 + 4 * kq + i) * p.sh0[2] + (v0 + r) * p.sh0[3]]
+                       ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + (m0 + 4 * kq + i) * p.sh0[2] + (v0 + r) * p.sh0[3]] * rsc.v
                        : 0.f;
     }
     put_state();
@@ -639,7 +644,7 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   Next16<TIn, K> nx;
   if (nch > 0) {
     nx.load(p, tid, slot0 * p.H + hi, qg, kg, vg, 0, min(C, rs.T));
-    nx.store(s, tid);
+    nx.store(s, tid, rsc.v);
   }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
@@ -743,7 +748,7 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       }
     }
     __syncthreads();
-    nx.store(s, tid);
+    nx.store(s, tid, rsc.v);
     __syncthreads();
   }
   if (upper) {
@@ -753,7 +758,7 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       if (m0 < K) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          p.fs[bi * p.sfs[0] + hi * p.sfs[1] + (m0 + 4 * kq + i) * p.sfs[2] + (v0 + r) * p.sfs[3]] = st[j][i];
+          p.fs[bi * p.sfs[0] + hi * p.sfs[1] + (m0 + 4 * kq + i) * p.sfs[2] + (v0 + r) * p.sfs[3]] = st[j][i] * rsc.fs;
       }
     }
   }

@@ -131,6 +131,15 @@ struct InTraits<bf16_t> {
       out[2 * e + 1] = (f16)bf16_bits_to_float(w[e] >> 16);
     }
   }
+  // times sc (a power of two: exact) before the conversion
+  __device__ static __forceinline__ void to_op_sc(const uint4& r, f16* out, float sc) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out[2 * e] = (f16)(bf16_bits_to_float(w[e] & 0xffffu) * sc);
+      out[2 * e + 1] = (f16)(bf16_bits_to_float(w[e] >> 16) * sc);
+    }
+  }
 };
 
 template <>
@@ -143,6 +152,91 @@ struct InTraits<float> {
     out[3] = __uint_as_float(r.w);
   }
 };
+
+// ---------------------------------------------------------------------------
+// Range of bf16 inputs.  bf16 q, k, v reach the matrix cores as fp16
+// operands, and so do quantities derived from v (u, the state): fp16 holds
+// |x| <= 65504 and is subnormal below 2^-14, far less than bf16.  o and the
+// state are jointly linear in (v, h0), and each column of the state evolves
+// on its own, so a workgroup that owns a slice of V columns runs on v and h0
+// scaled by a power of two 2^s chosen from the slice's largest magnitude and
+// scales o and final_state by 2^-s.  Powers of two are exact in fp32 and
+// carry over fp16 rounding unchanged, and s = 0 (nothing changes) whenever
+// that magnitude lies in [2^-6, 2^10].  (q and k are not rescaled: the delta
+// rule needs |k| of order one, and q is normalised in every caller here.)
+// ---------------------------------------------------------------------------
+
+// Largest |x| of a pair of bf16 values as an fp32 bit pattern (patterns of
+// non-negative floats order like their values; NaN patterns lie above inf).
+__device__ __forceinline__ uint32_t bf16x2_absmax_bits(uint32_t w) {
+  return max((w & 0x7fffu) << 16, w & 0x7fff0000u);
+}
+
+// Largest magnitude of v[rows x cols] (bf16, rows `rstride` bytes apart,
+// cols a multiple of 8, 16-byte aligned rows) and of h0[K x cols] (fp32,
+// element strides sk and sc; nullable), over the whole workgroup: every
+// thread of the workgroup calls it (one barrier).  NaN if either holds one.
+__device__ __forceinline__ float slice_absmax_bf16(const char* v, int64_t rstride, int rows, int cols,
+                                                   const float* h0, int64_t sk, int64_t sc, int K) {
+  __shared__ uint32_t red[16];
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  uint32_t m = 0;
+  const int pieces = cols >> 3;
+  const int64_t nv = (int64_t)rows * pieces;
+  for (int64_t i = tid; i < nv; i += nthr) {
+    const int64_t r = i / pieces;
+    const int c = (int)(i - r * pieces);
+    const uint4 x = *reinterpret_cast<const uint4*>(v + r * rstride + c * 16);
+    m = max(m, max(max(bf16x2_absmax_bits(x.x), bf16x2_absmax_bits(x.y)),
+                   max(bf16x2_absmax_bits(x.z), bf16x2_absmax_bits(x.w))));
+  }
+  if (h0 != nullptr) {
+    const int64_t nh = (int64_t)K * cols;
+    for (int64_t i = tid; i < nh; i += nthr) {
+      const int64_t kk = i / cols;
+      const int c = (int)(i - kk * cols);
+      m = max(m, __float_as_uint(h0[kk * sk + c * sc]) & 0x7fffffffu);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = 0;
+  for (int w = 0; w < (nthr + 63) / 64; ++w) m = max(m, red[w]);
+  return __uint_as_float(m);
+}
+
+// The shift s for a slice whose largest magnitude is m: 0 when m is zero,
+// not finite or in [2^-6, 2^10]; else m 2^s lies in [1, 2).
+__device__ __forceinline__ int range_shift(float m) {
+  if (!(m > 0.f) || !(m < __builtin_inff())) return 0;
+  if (m >= 0x1p-6f && m <= 0x1p10f) return 0;
+  int e;
+  (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+  return min(max(1 - e, -126), 126);
+}
+
+// Scale factors of a slice: v and h0 by 2^s, o (with the caller's scale)
+// and final_state by 2^-s.
+struct RangeScale {
+  float v = 1.f, o = 1.f, fs = 1.f;
+};
+
+template <typename TIn>
+__device__ __forceinline__ RangeScale slice_range_scale(const char* v, int64_t rstride, int rows, int cols,
+                                                        const float* h0, int64_t sk, int64_t sc, int K,
+                                                        float scale) {
+  RangeScale r;
+  r.o = scale;
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    const int sh = range_shift(slice_absmax_bf16(v, rstride, rows, cols, h0, sk, sc, K));
+    r.v = ldexpf(1.f, sh);
+    r.fs = ldexpf(1.f, -sh);
+    r.o = scale * r.fs;
+  }
+  return r;
+}
 
 template <typename TIn>
 struct OpOf {
@@ -357,6 +451,11 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
   const TIn* vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
   const int64_t g_base = head_base(rs, hi, p.sg);
   const int64_t b_base = head_base(rs, hi, p.sb);
+  // bf16: this slice's v and h0 scaled into fp16's range, o and the final
+  // state scaled back (identity for fp16 and fp32)
+  const RangeScale rsc = slice_range_scale<TIn>(
+      reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), T, BV,
+      p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, p.scale);
 
   // State slice S[:, v0 + 16*wave + n] in D layout: tile r holds rows
   // 16r + 4gq + i.
@@ -369,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
 #pragma unroll
     for (int r = 0; r < KT; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st[r][i] = h0[(16 * r + 4 * gq + i) * p.sh0[2]];
+      for (int i = 0; i < 4; ++i) st[r][i] = h0[(16 * r + 4 * gq + i) * p.sh0[2]] * rsc.v;
   }
 
   for (int t0 = 0; t0 < T; t0 += C) {
@@ -402,7 +501,10 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         uint4 rv = {0u, 0u, 0u, 0u};
         if (t0 + t < T) rv = *reinterpret_cast<const uint4*>(vg + (int64_t)(t0 + t) * p.sv[1] + c);
         TOp xv[VEC];
-        InTraits<TIn>::to_op(rv, xv);
+        if constexpr (std::is_same<TIn, bf16_t>::value)
+          InTraits<TIn>::to_op_sc(rv, xv, rsc.v);
+        else
+          InTraits<TIn>::to_op(rv, xv);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) s.vt[(c + e) * SC + t] = xv[e];
       }
@@ -640,7 +742,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * mt + 4 * gq + i;
           if (t0 + t < T) {
-            const float val = p.scale * (acc[i] + s.eb[t] * oq[mt][i]);
+            const float val = rsc.o * (acc[i] + s.eb[t] * oq[mt][i]);
             store_scalar(p.o, o_col + (int64_t)(t0 + t) * p.so[1], p.o_dtype, val);
           }
         }
@@ -664,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
 #pragma unroll
     for (int r = 0; r < KT; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fs[(16 * r + 4 * gq + i) * p.sfs[2]] = st[r][i];
+      for (int i = 0; i < 4; ++i) fs[(16 * r + 4 * gq + i) * p.sfs[2]] = st[r][i] * rsc.fs;
   }
 }
 

@@ -121,6 +121,18 @@ __device__ __forceinline__ f16x8 to_f16x8(const uint4& r) {
   return f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
 }
 
+// bf16 rows times sc (a power of two) before the conversion; fp16 as is.
+template <typename TIn>
+__device__ __forceinline__ f16x8 to_f16x8_sc(const uint4& r, float sc) {
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    f16 x[8];
+    InTraits<bf16_t>::to_op_sc(r, x, sc);
+    return f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  } else {
+    return to_f16x8<TIn>(r);
+  }
+}
+
 __device__ __forceinline__ uint4 cr_get4(const uint32_t* cr, int w) {
   return uint4{cr[w], cr[w + 1], cr[w + 2], cr[w + 3]};
 }
@@ -416,6 +428,11 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
   const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
   const char* gh = static_cast<const char*>(p.g) + head_base(rs, hi, p.sg) * geb;
   const char* betah = static_cast<const char*>(p.beta) + head_base(rs, hi, p.sb) * beb;
+  // bf16: this slice's v and h0 scaled into fp16's range, o and the final
+  // state scaled back (identity for fp16)
+  const RangeScale rsc = slice_range_scale<TIn>(
+      vh, (int64_t)p.sv[1] * EB, T, BV, p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr,
+      p.sh0[2], p.sh0[3], K, p.scale);
 
   // f(std::bool_constant<tail>) for chunk j: tail is set only for a last,
   // partial chunk.
@@ -465,7 +482,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
       for (int r = 0; r < KT; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[r][i] = h0[key_of(r, i) * p.sh0[2]];
+        for (int i = 0; i < 4; ++i) st[r][i] = h0[key_of(r, i) * p.sh0[2]] * rsc.v;
     }
     f16x8 sB[KB];
 #pragma unroll
@@ -526,7 +543,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
     for (int r = 0; r < KT; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i];
+      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i] * rsc.fs;
   } else if (role == R_OUT) {
     // ================================================================ OUT
     // chunk it: Q S (S from SCAN); chunk it-1: o = scale (P u + diag(e^b) Q S);
@@ -557,7 +574,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
           f32x4 pu = M::mma(pA[mt], ul, z4);
           pu = M::mma(pL[mt], uh, pu);
           pu = M::mma(pA[mt], uh, pu);
-          ov[mt] = (pu + ebv[mt] * oq[c2][mt]) * p.scale;
+          ov[mt] = (pu + ebv[mt] * oq[c2][mt]) * rsc.o;
         }
         const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2 + n;
         if (p.o_dtype == GDN_DTYPE_F16)
@@ -829,7 +846,7 @@ __global__ __launch_bounds__(64 * pipe_waves<BV>()) void gdn_fwd_pipe_kernel(con
 #pragma unroll
           for (int i = 0; i < NIV; ++i) {
             const int e = 64 * i + lane, r = e / VCH, c = e % VCH;
-            s.rv[j % NRV][r][c] = to_f16x8<TIn>(cr_get4(cr, 4 * NI + 4 * i));
+            s.rv[j % NRV][r][c] = to_f16x8_sc<TIn>(cr_get4(cr, 4 * NI + 4 * i), rsc.v);
           }
           if (lane < C) s.rg[j % NRG][lane] = gate_at(j, cr[4 * NI + 4 * NIV], p.g_dtype);
         }

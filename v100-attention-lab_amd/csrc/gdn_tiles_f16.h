@@ -138,8 +138,10 @@ struct SlicePairs {
     nv = nvalid;
     r = *reinterpret_cast<const uint32_t*>(src + min(tid / (COLS / 2), nvalid - 1) * ld + 2 * (tid % (COLS / 2)));
   }
+  // bf16 values are multiplied by sc (a power of two: exact) before the
+  // conversion; fp16 values are stored as they are.
   template <int LD>
-  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD]) const {
+  __device__ __forceinline__ void store(int tid, f16 (*dst)[LD], float sc = 1.f) const {
     const int t = tid / (COLS / 2), c = tid % (COLS / 2);
     const uint32_t v = t < nv ? r : 0u;
     const uint16_t l16 = (uint16_t)(v & 0xffffu), h16 = (uint16_t)(v >> 16);
@@ -147,8 +149,8 @@ struct SlicePairs {
       dst[2 * c][t] = __builtin_bit_cast(f16, l16);
       dst[2 * c + 1][t] = __builtin_bit_cast(f16, h16);
     } else {
-      dst[2 * c][t] = (f16)bf16_bits_to_float(l16);
-      dst[2 * c + 1][t] = (f16)bf16_bits_to_float(h16);
+      dst[2 * c][t] = (f16)(bf16_bits_to_float(l16) * sc);
+      dst[2 * c + 1][t] = (f16)(bf16_bits_to_float(h16) * sc);
     }
   }
 };
