@@ -250,3 +250,26 @@ def test_autograd_fp32_output(pkg, cuda, dtype):
     want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=0.9)
     got = [t.grad for t in leaves]
     _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, f"{dtype} fp32 o")
+
+
+@pytest.mark.parametrize("v_scale,d_scale", [(1.0, 1e-6), (1e5, 1.0), (1e-6, 1e-7), (3e4, 1e-6)])
+def test_bwd_bf16_extreme_scales(pkg, cuda, v_scale, d_scale):
+    """bf16 v / h0 and dO / d_final_state far from fp16's range (|v| up to
+    1e5, gradients of 1e-6 as in bf16 training without loss scaling): the
+    16-bit state walks run on power-of-two-shifted values and shift their
+    outputs back (exact), so every gradient stays within the 16-bit bar of
+    the fp64 recurrence's, relative to its own magnitude."""
+    B, T, H, K, V = 1, 150, 2, 64, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, torch.float32, seed=41)
+    v, h0, do, dfin = v * v_scale, h0 * v_scale, do * d_scale, dfin * d_scale
+    bf = lambda t: t.to(torch.bfloat16)
+    q, k, v, do = bf(q), bf(k), bf(v), bf(do)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] bf16 v*{v_scale:g} dO*{d_scale:g}", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=1.0)
+    torch.cuda.synchronize()
+    for t in got:
+        assert t is None or torch.isfinite(t.float()).all()
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=1.0)
+    got = (got[0], got[1], got[2], got[4], got[3], got[5])   # -> dq dk dv dbeta dg dh0
+    _compare(got, want, torch.bfloat16, f"bf16 v*{v_scale:g} dO*{d_scale:g}")

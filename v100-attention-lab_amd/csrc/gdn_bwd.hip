@@ -616,14 +616,16 @@ template <int K>
 struct State {
   static constexpr int NST = (K / 16 + 3) / 4;
   f32x4 st[NST];
+  // times sc (a power of two: exact)
   __device__ __forceinline__ void load(const float* src, const int64_t (&sd)[4], int bi, int hi, int v0, int wave,
-                                       int r, int kq) {
+                                       int r, int kq, float sc = 1.f) {
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        st[j][i] = (src && m0 < K) ? src[bi * sd[0] + hi * sd[1] + (m0 + 4 * kq + i) * sd[2] + (v0 + r) * sd[3]] : 0.f;
+        st[j][i] = (src && m0 < K) ? src[bi * sd[0] + hi * sd[1] + (m0 + 4 * kq + i) * sd[2] + (v0 + r) * sd[3]] * sc
+                                   : 0.f;
     }
   }
   // into the fp32 LDS copy (read back by copy_rows after a barrier)
@@ -651,16 +653,17 @@ struct State {
   }
 };
 
-// The K x BV fp32 state copy -> rows of a [K][V] array, 16 bytes per lane.
+// The K x BV fp32 state copy, times sc (a power of two), -> rows of a
+// [K][V] array, 16 bytes per lane.
 template <int K, int LD>
-__device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, int64_t ld, int tid) {
+__device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, int64_t ld, int tid, float sc) {
   constexpr int NV = K * BV / 4;
 #pragma unroll
   for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
     const int e = tid + i * NTP;
     if (NV % NTP == 0 || e < NV)
       *reinterpret_cast<f32x4*>(dst + (int64_t)(e / 4) * ld + 4 * (e % 4)) =
-          *reinterpret_cast<const f32x4*>(&s32[e / 4][4 * (e % 4)]);
+          *reinterpret_cast<const f32x4*>(&s32[e / 4][4 * (e % 4)]) * sc;
   }
 }
 
@@ -681,16 +684,18 @@ struct FNext16 {
     v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
   }
-  __device__ __forceinline__ void store(FMem<K>& s, int tid) const {
+  __device__ __forceinline__ void store(FMem<K>& s, int tid, float vsc) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
     k.store(tid, s.k);
-    v.store(tid, s.vt);
+    v.store(tid, s.vt, vsc);
     s.gv[tid / C][tid % C] = gate;
   }
 };
 
-// Forward walk: S at each chunk start -> ckS, u -> uu.
+// Forward walk: S at each chunk start -> ckS, u -> uu.  For bf16 inputs the
+// walk runs on v and h0 shifted into fp16's range (slice_range_scale: both
+// outputs are linear in them) and shifts ckS and u back.
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                int v0, int64_t slot0) {
@@ -700,14 +705,17 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
   const int nch = (rs.T + C - 1) / C;
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
   const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
+  const RangeScale rsc = slice_range_scale<TIn>(
+      reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), rs.T, BV,
+      p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, 1.f);
   State<K> S;
-  S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq);
+  S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq, rsc.v);
   S.put(s.sh, s.sl, wave, r, kq);
   S.put32(s.s32, wave, r, kq);
   FNext16<TIn, K> nx;
   if (nch > 0) {
     nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
-    nx.store(s, tid);
+    nx.store(s, tid, rsc.v);
   }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
@@ -716,7 +724,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     // is then consumed by the staging below, on every path)
     const int cn = min(c + 1, nch - 1);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
-    copy_rows<K>(s.s32, p.ckS + ri * (int64_t)K * p.V + v0, p.V, tid);
+    copy_rows<K>(s.s32, p.ckS + ri * (int64_t)K * p.V + v0, p.V, tid, rsc.fs);
     if (wave < 2) {
       // Y = V - diag(gam) K S for rows 16 w .. (k exact in fp16), as Y^T pairs
       const int um0 = 16 * wave;
@@ -748,7 +756,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         du[i] = s.gv[2][t + i] * au[i];
-        uo[(int64_t)(t + i) * p.V + r] = au[i];
+        uo[(int64_t)(t + i) * p.V + r] = au[i] * rsc.fs;
       }
       store_pair4(&s.dh[r][t], &s.dl[r][t], du);
     }
@@ -769,7 +777,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     S.put(s.sh, s.sl, wave, r, kq);
     S.put32(s.s32, wave, r, kq);
     __syncthreads();
-    nx.store(s, tid);
+    nx.store(s, tid, rsc.v);
     __syncthreads();
   }
 }
@@ -794,19 +802,22 @@ struct RNext16 {
     d.load(tid, dg + (int64_t)t0 * p.sdo[1], p.sdo[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
   }
-  __device__ __forceinline__ void store(RMem<K>& s, int tid) const {
+  __device__ __forceinline__ void store(RMem<K>& s, int tid, float dsc) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
     ph.store(tid, s.ph);
     pl.store(tid, s.pl);
     q.store(tid, s.q);
     k.store(tid, s.k);
-    d.store(tid, s.dot);
+    d.store(tid, s.dot, dsc);
     s.gv[tid / C][tid % C] = gate;
   }
 };
 
-// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.
+// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.  For
+// bf16 inputs the walk runs on dO and d_final_state shifted into fp16's
+// range (every output of the walk is linear in them) and shifts ckD, du and
+// dh0 back: small gradients keep their hi / lo precision.
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                 int v0, int64_t slot0) {
@@ -818,15 +829,18 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
   const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
   const TIn* const dg = static_cast<const TIn*>(p.d_o) + head_base(rs, hi, p.sdo) + v0;
+  const RangeScale rsd = slice_range_scale<TIn>(
+      reinterpret_cast<const char*>(dg), p.sdo[1] * (int64_t)sizeof(TIn), rs.T, BV,
+      p.dfs ? p.dfs + bi * p.sdfs[0] + hi * p.sdfs[1] + v0 * p.sdfs[3] : nullptr, p.sdfs[2], p.sdfs[3], K, 1.f);
   State<K> S;
-  S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq);
+  S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq, rsd.v);
   S.put(s.sh, s.sl, wave, r, kq);
   S.put32(s.s32, wave, r, kq);
   RNext16<TIn, K> nx;
   if (nch > 0) {
     const int t0 = (nch - 1) * C;
     nx.load(p, tid, (slot0 + nch - 1) * p.H + hi, qg, kg, dg, t0, rs.T - t0);
-    nx.store(s, tid);
+    nx.store(s, tid, rsd.v);
   }
   __syncthreads();
   for (int c = nch - 1; c >= 0; --c) {
@@ -834,7 +848,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     // the previous chunk's inputs (chunk 0's again at the end)
     const int cn = max(c - 1, 0);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
-    copy_rows<K>(s.s32, p.ckD + ri * (int64_t)K * p.V + v0, p.V, tid);
+    copy_rows<K>(s.s32, p.ckD + ri * (int64_t)K * p.V + v0, p.V, tid, rsd.fs);
     if (wave < 2) {
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
@@ -854,7 +868,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         du[i] = scale * a1[i] + s.gv[2][t + i] * a2[i];
-        duo[(int64_t)(t + i) * p.V + r] = du[i];
+        duo[(int64_t)(t + i) * p.V + r] = du[i] * rsd.fs;
       }
       store_pair4(&s.uh[r][t], &s.ul[r][t], du);
     } else {
@@ -915,7 +929,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     S.put(s.sh, s.sl, wave, r, kq);
     S.put32(s.s32, wave, r, kq);
     __syncthreads();
-    nx.store(s, tid);
+    nx.store(s, tid, rsd.v);
     __syncthreads();
   }
   if (p.dh0 != nullptr) {
@@ -925,7 +939,8 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       if (m0 < K) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          p.dh0[bi * p.sdh0[0] + hi * p.sdh0[1] + (m0 + 4 * kq + i) * p.sdh0[2] + (v0 + r) * p.sdh0[3]] = S.st[j][i];
+          p.dh0[bi * p.sdh0[0] + hi * p.sdh0[1] + (m0 + 4 * kq + i) * p.sdh0[2] + (v0 + r) * p.sdh0[3]] =
+              S.st[j][i] * rsd.fs;
       }
     }
   }
