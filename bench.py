@@ -45,6 +45,9 @@ CONFIGS = {
     "cfg2_c64": (2, 4096, 16, 128, 128, torch.float16, 64, False),
     "cfg3": (2, 16384, 16, 128, 128, torch.float16, 32, False),
     "cfg4": (4, 4096, 16, 128, 128, torch.bfloat16, 32, True),
+    # exploration only: the configs[4] shape in fp16 (64 heads on the
+    # two-launch path)
+    "cfg4_f16": (4, 4096, 16, 128, 128, torch.float16, 32, True),
 }
 
 DTYPE_NAME = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
@@ -320,6 +323,33 @@ def phase_stamps(pkg, config):
                       "phases": phases}), flush=True)
 
 
+# (C, BV) combinations of the sweep: 32-row chunks take BV 16 or 32 on the
+# two-launch path (fp16) or the fused kernel (bf16) and 64 on the phased
+# kernel; 64-row chunks run at BV 16.
+SWEEP = ((32, 16), (32, 32), (32, 64), (64, 16))
+
+
+def sweep(pkg, steps, warmup):
+    """Times every (C, BV) of SWEEP at every config (configs[2] with C = 64 is
+    configs[2] as well) and prints one JSON line per config with the times
+    and the launcher's automatic BV for 32-row chunks."""
+    dev = torch.device("cuda:0")
+    for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg4_f16"):
+        B, T, H, K, V, dtype, _, with_h0 = CONFIGS[name]
+        q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
+        res = {}
+        for C, bv in SWEEP:
+            fn = lambda: pkg.gdn_fwd(q, k, v, g, beta, h0, scale=1.0, chunk_size=C, block_v=bv)
+            res[f"C{C}_BV{bv}"] = round(time_steps(fn, steps, warmup), 5)
+        best = min((t, key) for key, t in res.items() if key.startswith("C32_"))[1]
+        print(json.dumps({"config": name, "B": B, "T": T, "H": H, "K": K, "V": V,
+                          "dtype": DTYPE_NAME[dtype], "ms_per_step": res,
+                          "auto_block_v_c32": pkg.auto_block_v(B, H, K, V, 32, dtype),
+                          "best_c32": best}), flush=True)
+        del q, k, v, g, beta, h0
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +362,8 @@ def main():
                          "preparation; bwd: only the backward (gdn_bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time every (chunk, block_v) at every config (one JSON line per config)")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="MFMA utilisation of the contraction phases from the stamps build "
                          "(lib/libgdn_mi355x_stamps.so, built by build.py --phase-stamps)")
@@ -363,6 +395,9 @@ def main():
     pkg = importlib.import_module("v100-attention-lab_amd")
     if args.phase_stamps:
         phase_stamps(pkg, args.config)
+        return
+    if args.sweep:
+        sweep(pkg, min(args.steps, 50), min(args.warmup, 10))
         return
     dev = torch.device("cuda:0")
     B, T, H, K, V, dtype, C, with_h0 = CONFIGS[args.config]
@@ -453,6 +488,10 @@ def main():
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(B, T, H, K, V, dtype, C)
+        if args.config == "cfg2":
+            # configs[2] times both chunk sizes; the reference's own default is
+            # C = 64 (gdn_ref.py:48)
+            line["cpu_baseline"]["c64"] = cpu_baseline(B, T, H, K, V, dtype, 64)
 
     print(json.dumps(line), flush=True)
 

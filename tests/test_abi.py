@@ -415,3 +415,16 @@ def test_noalloc_rejects_before_launch(lib, pkg, kw, code):
     assert lib.gdn_fwd_launch_noalloc(ctypes.byref(P), None) == code
     assert lib.gdn_fwd_launch_noalloc(None, None) == 1001
     assert "scratch" in lib.gdn_fwd_status_string(1007).decode()
+
+
+def test_auto_block_v_matches_sweep(pkg):
+    """The launcher's BV for 32-row chunks is the fastest one measured by
+    `bench.py --sweep` at every config (profiles/gdn_fwd_sweep_chunk_block_v.json)."""
+    import json
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16}
+    with open(os.path.join(REPO, "profiles", "gdn_fwd_sweep_chunk_block_v.json")) as f:
+        rows = json.load(f)["rows"]
+    assert len(rows) >= 4
+    for r in rows:
+        best = min((t, key) for key, t in r["ms_per_step"].items() if key.startswith("C32_"))[1]
+        assert pkg.auto_block_v(r["B"], r["H"], r["K"], r["V"], 32, dt[r["dtype"]]) == int(best.split("BV")[1]), r
