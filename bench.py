@@ -239,15 +239,85 @@ def cpu_baseline(B, T, H, K, V, dtype, C, budget_s=12.0):
     }
 
 
+def sources_digest():
+    """sha256 (first 16 hex digits) over the library's HIP sources, names and
+    bytes: it identifies the build a traffic profile was measured on, also on
+    a machine without the git history."""
+    import hashlib
+    d = os.path.join(REPO, "v100-attention-lab_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_path(config):
+    return os.path.join(REPO, "profiles", f"gdn_fwd_{config}_traffic.json")
+
+
 def load_traffic(config):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE
-    (profiles/gdn_fwd_<config>_traffic.json), or None."""
-    path = os.path.join(REPO, "profiles", f"gdn_fwd_{config}_traffic.json")
+    (profiles/gdn_fwd_<config>_traffic.json) and a note on where they come
+    from.  The bytes are None when no profile exists or when it was taken on
+    other kernel sources than the ones present (its ``sources`` digest differs
+    from ``sources_digest()``): a stale figure is not reported as this
+    build's."""
     try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+        with open(traffic_path(config)) as f:
+            rec = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, "no traffic profile for this config"
+    where = f"profiles/gdn_fwd_{config}_traffic.json, commit {rec.get('commit', '?')}"
+    if rec.get("sources") != sources_digest():
+        return None, f"stale: {where} measured other kernel sources"
+    return rec.get("hbm_bytes_per_launch"), where
+
+
+def write_traffic(config, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
+    """Writes profiles/gdn_fwd_<config>_traffic.json from four rocprofv3
+    ``--pmc`` CSVs: FETCH_SIZE and WRITE_SIZE of a ``bench.py --steps 5
+    --warmup 1 --no-extras --no-cpu-baseline`` run, and the same two counters
+    of ``bench.py --calibrate-copy`` (a 256 MiB copy, which gives each
+    counter's scale).  Every library kernel (``gdn::`` names) of the run is
+    one launch's share: per kernel the median KiB per dispatch, summed over
+    the kernels, scaled.  Run where the git history is, after the GPU run."""
+    import csv
+    import subprocess
+
+    def medians(path):
+        per = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                per.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {k: statistics.median(v) for k, v in per.items()}
+
+    def scale(path):
+        copy = [v for k, v in medians(path).items() if "copyBuffer" in k or "copy_kernel" in k]
+        return (256 << 10) / max(copy)  # the 256 MiB copy in KiB / the counter's KiB
+
+    fetch, write = medians(fetch_csv), medians(write_csv)
+    kernels = sorted(k for k in fetch if k.startswith("_ZN3gdn"))
+    fs, ws = scale(copy_fetch_csv), scale(copy_write_csv)
+    per_kernel = {k: {"fetch_kib": fetch[k], "write_kib": write.get(k)} for k in kernels}
+    rd = sum(fetch[k] for k in kernels) * 1024 * fs
+    wr = sum(write[k] for k in kernels) * 1024 * ws
+    B, T, H, K, V, dtype, C, with_h0 = CONFIGS[config]
+    alg = algorithmic_bytes(B, T, H, K, V, torch.finfo(dtype).bits // 8, with_h0)
+    git = lambda *a: subprocess.run(["git", *a], cwd=REPO, capture_output=True, text=True).stdout.strip()
+    rec = {"config": config, "commit": git("rev-parse", "--short", "HEAD"),
+           "uncommitted_changes": bool(git("status", "--porcelain", "--", "v100-attention-lab_amd/csrc")),
+           "sources": sources_digest(), "kernels": per_kernel,
+           "fetch_scale": round(fs, 6), "write_scale": round(ws, 6),
+           "bytes_read_per_launch": round(rd), "bytes_written_per_launch": round(wr),
+           "hbm_bytes_per_launch": round(rd + wr), "algorithmic_bytes_per_launch": alg,
+           "traffic_over_algorithmic": round((rd + wr) / alg, 4)}
+    with open(traffic_path(config), "w") as f:
+        json.dump(rec, f, indent=1)
+        f.write("\n")
+    print(json.dumps(rec, indent=1))
 
 
 def phase_stamps(pkg, config):
@@ -369,7 +439,15 @@ def main():
                          "(lib/libgdn_mi355x_stamps.so, built by build.py --phase-stamps)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (scale for rocprof byte counters)")
+    ap.add_argument("--write-traffic", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                                                          "COPY_WRITE_CSV"),
+                    help="no GPU: write profiles/gdn_fwd_<config>_traffic.json from rocprofv3 "
+                         "--pmc FETCH_SIZE / WRITE_SIZE CSVs of a bench run and of --calibrate-copy")
     args = ap.parse_args()
+
+    if args.write_traffic:
+        write_traffic(args.config, *args.write_traffic)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The GDN "
@@ -438,6 +516,7 @@ def main():
     achieved_gbs = alg_bytes / (ms / 1e3) / 1e9
     achieved_tflops = alg_flops / (ms / 1e3) / 1e12
     bv = args.block_v or pkg.auto_block_v(B, H, K, V, C, dtype)
+    traffic, traffic_note = load_traffic(args.config)
 
     line = {
         "metric": "GDN fwd tokens/sec at B2 H16 K=V=128 T=4096; % MFMA/HBM roofline",
@@ -463,7 +542,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 5),
-            "traffic": load_traffic(args.config),
+            "traffic": traffic,
+            "traffic_profile": traffic_note,
         },
         "head_tokens_per_s": round(B * T * H / (ms / 1e3), 1),
         "mfma": {"algorithmic_tflops": round(achieved_tflops, 3), "peak_tflops": MFMA_F16_PEAK_TFLOPS,

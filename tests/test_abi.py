@@ -10,6 +10,7 @@
 """
 
 import ctypes
+import json
 import os
 import re
 import subprocess
@@ -428,3 +429,25 @@ def test_auto_block_v_matches_sweep(pkg):
     for r in rows:
         best = min((t, key) for key, t in r["ms_per_step"].items() if key.startswith("C32_"))[1]
         assert pkg.auto_block_v(r["B"], r["H"], r["K"], r["V"], 32, dt[r["dtype"]]) == int(best.split("BV")[1]), r
+
+
+def test_traffic_profile_tracks_sources(monkeypatch):
+    """bench.py reports roofline.traffic from the committed rocprofv3 profile
+    only while the kernel sources hash to the digest recorded in it; a stale
+    profile gives null and says so."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_bench", os.path.join(REPO, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    with open(bench.traffic_path("cfg2")) as f:
+        rec = json.load(f)
+    assert rec["sources"] and rec["commit"] and rec["kernels"]
+    assert all(k.startswith("_ZN3gdn") for k in rec["kernels"])
+    nbytes, note = bench.load_traffic("cfg2")
+    if rec["sources"] == bench.sources_digest():
+        assert nbytes == rec["hbm_bytes_per_launch"] and rec["commit"] in note
+    else:
+        assert nbytes is None and note.startswith("stale")
+    monkeypatch.setattr(bench, "sources_digest", lambda: "0" * 16)
+    nbytes, note = bench.load_traffic("cfg2")
+    assert nbytes is None and note.startswith("stale")
