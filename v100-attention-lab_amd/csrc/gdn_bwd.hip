@@ -36,7 +36,10 @@
 //      on hi + lo pairs), one workgroup per (sequence, head, 16-column V
 //      slice) and direction, both directions in one launch: the forward
 //      walk stores each chunk's start state S and u; the backward walk
-//      stores each chunk's dS' and du and finally dh0;
+//      stores each chunk's dS' and du and finally dh0.  The 16-bit walks
+//      store S and dS' in fp16 (half the bytes of the largest arrays of
+//      the backward), in their range-shifted units with one scale per
+//      walk;
 //   3. grad_kernel, one workgroup per (chunk, head) over all of V: every
 //      gradient of the chunk from the stored S, dS', u, du and the record,
 //      written directly in the output dtypes (V is walked in 32-column steps,
@@ -74,11 +77,16 @@ struct BArgs {
   void* dbeta;
   float* dh0;
   float* rec;  // per (slot, head): the prep kernel's record
-  float* ckS;  // per (slot, head): S at the chunk start, [K][V]
-  float* ckD;  // per (slot, head): dS', the gradient of the state after the chunk, [K][V]
+  // per (slot, head): S at the chunk start and dS', the gradient of the
+  // state after the chunk, [K][V]; fp32, or fp16 from the 16-bit walks (in
+  // each walk's range-shifted units: scl below scales them back)
+  float* ckS;
+  float* ckD;
   float* uu;   // per (slot, head): u, [C][V]
   float* du;   // per (slot, head): du, [C][V]
   f16* r16;    // per (slot, head): T diag(beta) and P as fp16 pairs (16-bit walks)
+  float* scl;  // per walk unit (sequence, head, V-slice): the power of two that
+               // takes the fp16 ckS (units first) and ckD (then) back to true units
   int w16;     // the recurrences run on fp16 pairs (16-bit q, k, v and dO)
   int64_t sq[3], sk[3], sv[3], sg[3], sb[3], sdo[3], sdq[3], sdk[3], sdv[3], sdg[3], sdb[3];
   int64_t sh0[4], sdfs[4], sdh0[4];
@@ -667,6 +675,23 @@ __device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, in
   }
 }
 
+// The K x BV fp32 state copy -> fp16 rows of a [K][V] array, 16 bytes per
+// lane (rounded to nearest: the same value as the walk's hi part).
+template <int K, int LD>
+__device__ __forceinline__ void copy_rows16(const float (*s32)[LD], f16* dst, int64_t ld, int tid) {
+  constexpr int NV = K * BV / 8;
+#pragma unroll
+  for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
+    const int e = tid + i * NTP;
+    if (NV % NTP == 0 || e < NV) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&s32[e / 2][8 * (e % 2)]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&s32[e / 2][8 * (e % 2) + 4]);
+      *reinterpret_cast<f16x8*>(dst + (int64_t)(e / 2) * ld + 8 * (e % 2)) =
+          f16x8{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3], (f16)b[0], (f16)b[1], (f16)b[2], (f16)b[3]};
+    }
+  }
+}
+
 // Next chunk's inputs of the forward walk, in registers.
 template <typename TIn, int K>
 struct FNext16 {
@@ -693,9 +718,11 @@ struct FNext16 {
   }
 };
 
-// Forward walk: S at each chunk start -> ckS, u -> uu.  For bf16 inputs the
-// walk runs on v and h0 shifted into fp16's range (slice_range_scale: both
-// outputs are linear in them) and shifts ckS and u back.
+// Forward walk: S at each chunk start -> ckS (fp16), u -> uu.  For bf16
+// inputs the walk runs on v and h0 shifted into fp16's range
+// (slice_range_scale: both outputs are linear in them) and shifts u back;
+// ckS stays in the shifted units, and the factor that takes it back goes to
+// scl[unit].
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                int v0, int64_t slot0) {
@@ -708,6 +735,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
   const RangeScale rsc = slice_range_scale<TIn>(
       reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), rs.T, BV,
       p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, 1.f);
+  if (tid == 0) p.scl[((int64_t)bi * p.H + hi) * p.nv + v0 / BV] = rsc.fs;
   State<K> S;
   S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq, rsc.v);
   S.put(s.sh, s.sl, wave, r, kq);
@@ -724,7 +752,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     // is then consumed by the staging below, on every path)
     const int cn = min(c + 1, nch - 1);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
-    copy_rows<K>(s.s32, p.ckS + ri * (int64_t)K * p.V + v0, p.V, tid, rsc.fs);
+    copy_rows16<K>(s.s32, reinterpret_cast<f16*>(p.ckS) + ri * (int64_t)K * p.V + v0, p.V, tid);
     if (wave < 2) {
       // Y = V - diag(gam) K S for rows 16 w .. (k exact in fp16), as Y^T pairs
       const int um0 = 16 * wave;
@@ -814,10 +842,11 @@ struct RNext16 {
   }
 };
 
-// Backward walk: dS' of each chunk -> ckD, du -> du, at the end dh0.  For
-// bf16 inputs the walk runs on dO and d_final_state shifted into fp16's
-// range (every output of the walk is linear in them) and shifts ckD, du and
-// dh0 back: small gradients keep their hi / lo precision.
+// Backward walk: dS' of each chunk -> ckD (fp16), du -> du, at the end dh0.
+// For bf16 inputs the walk runs on dO and d_final_state shifted into fp16's
+// range (every output of the walk is linear in them) and shifts du and dh0
+// back: small gradients keep their hi / lo precision.  ckD stays in the
+// shifted units; the factor that takes it back goes to scl[units + unit].
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                 int v0, int64_t slot0) {
@@ -832,6 +861,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
   const RangeScale rsd = slice_range_scale<TIn>(
       reinterpret_cast<const char*>(dg), p.sdo[1] * (int64_t)sizeof(TIn), rs.T, BV,
       p.dfs ? p.dfs + bi * p.sdfs[0] + hi * p.sdfs[1] + v0 * p.sdfs[3] : nullptr, p.sdfs[2], p.sdfs[3], K, 1.f);
+  if (tid == 0) p.scl[p.units + ((int64_t)bi * p.H + hi) * p.nv + v0 / BV] = rsd.fs;
   State<K> S;
   S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq, rsd.v);
   S.put(s.sh, s.sl, wave, r, kq);
@@ -848,7 +878,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     // the previous chunk's inputs (chunk 0's again at the end)
     const int cn = max(c - 1, 0);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
-    copy_rows<K>(s.s32, p.ckD + ri * (int64_t)K * p.V + v0, p.V, tid, rsd.fs);
+    copy_rows16<K>(s.s32, reinterpret_cast<f16*>(p.ckD) + ri * (int64_t)K * p.V + v0, p.V, tid);
     if (wave < 2) {
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
@@ -995,8 +1025,9 @@ struct alignas(16) GSmem {
 };
 
 // VS: V columns per step of the V walk (32, or 16 when V is an odd
-// multiple of 16).
-template <typename TIn, int K, int VS>
+// multiple of 16).  ST16: ckS and ckD hold fp16 in the walks' shifted units
+// (the 16-bit walks), scaled back per 16-column slice by scl when staged.
+template <typename TIn, int K, int VS, bool ST16>
 __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   using R = Rec<K>;
   constexpr int RL = NTG / C;
@@ -1007,14 +1038,18 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   const int64_t slot = blockIdx.x / p.H;
   const int hi = blockIdx.x % p.H;
   RowSpan rs;
-  int c;
-  if (!slot_chunk<C>(p, slot, rs, c)) return;
+  int c, seq;
+  if (!slot_chunk<C>(p, slot, rs, c, seq)) return;
   const int t0 = c * C, nval = min(C, rs.T - t0);
   const float scale = p.scale;
   const int64_t ri = slot * p.H + hi;
   const float* const rec = p.rec + ri * R::SIZE;
-  const float* const cks = p.ckS + ri * (int64_t)K * p.V;
-  const float* const ckd = p.ckD + ri * (int64_t)K * p.V;
+  using TS = typename std::conditional<ST16, f16, float>::type;
+  const TS* const cks = reinterpret_cast<const TS*>(p.ckS) + ri * (int64_t)K * p.V;
+  const TS* const ckd = reinterpret_cast<const TS*>(p.ckD) + ri * (int64_t)K * p.V;
+  // the state scales of this head's 16-column walk slices
+  const float* const sclS = ST16 ? p.scl + ((int64_t)seq * p.H + hi) * p.nv : nullptr;
+  const float* const sclD = ST16 ? sclS + p.units : nullptr;
   const float* const uu = p.uu + ri * (int64_t)C * p.V;
   const float* const dug = p.du + ri * (int64_t)C * p.V;
   const int64_t qb = head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1];
@@ -1070,7 +1105,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   const int nvs = p.V / VS;
   RowLoad<TIn, C, VS, NTG> lv;
   RowLoad<float, C, VS, NTG> lu, ldu;
-  RowLoad<float, K, VS, NTG> lS, ldS;
+  RowLoad<TS, K, VS, NTG> lS, ldS;
+  float scS[2] = {1.f, 1.f}, scD[2] = {1.f, 1.f};
   constexpr int NDO = C * VS / NTG;
   static_assert(C * VS % NTG == 0, "dO elements per thread");
   uint32_t rdo[NDO];
@@ -1081,6 +1117,13 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     ldu.load(tid, dug + v0, p.V, C);
     lS.load(tid, cks + v0, p.V, K);
     ldS.load(tid, ckd + v0, p.V, K);
+    if constexpr (ST16) {
+#pragma unroll
+      for (int j = 0; j < VS / 16; ++j) {
+        scS[j] = sclS[v0 / 16 + j];
+        scD[j] = sclD[v0 / 16 + j];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int e = tid + i * NTG, t = e / VS, c2 = e % VS;
@@ -1091,8 +1134,13 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     lv.store(tid, s.v);
     lu.store(tid, s.u);
     ldu.store(tid, s.du);
-    lS.store(tid, s.S);
-    ldS.store(tid, s.dS);
+    if constexpr (ST16) {
+      lS.store_scaled(tid, s.S, scS[0], scS[1]);
+      ldS.store_scaled(tid, s.dS, scD[0], scD[1]);
+    } else {
+      lS.store(tid, s.S);
+      ldS.store(tid, s.dS);
+    }
 #pragma unroll
     for (int i = 0; i < NDO; ++i) {
       const int e = tid + i * NTG;
@@ -1323,7 +1371,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 
 // Workspace layout (each part 256-byte aligned).
 struct Layout {
-  int64_t rec, ckS, ckD, uu, du, r16, total;  // offsets in bytes
+  int64_t rec, ckS, ckD, uu, du, r16, scl, total;  // offsets in bytes
   int64_t nslot;
 };
 
@@ -1347,6 +1395,8 @@ inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
   off = align256(off + nr * C * V * 4);
   L.r16 = off;
   off = align256(off + nr * rec16_size(K) * 2);
+  L.scl = off;  // two floats per walk unit (B sequences x H x V / BV)
+  off = align256(off + 2 * (int64_t)B * H * (V / BV) * 4);
   L.total = off;
   return L;
 }
@@ -1361,10 +1411,15 @@ int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
     hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
   }
   if (nrec > 0) {
-    if (a.V % 32 == 0)
-      hipLaunchKernelGGL((grad_kernel<TIn, K, 32>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
-    else
-      hipLaunchKernelGGL((grad_kernel<TIn, K, 16>), dim3((unsigned)nrec), dim3(NTG), 0, s, a);
+    const dim3 grid((unsigned)nrec);
+    const bool st16 = !std::is_same<TIn, float>::value && a.w16;
+    if (a.V % 32 == 0) {
+      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 32, true>), grid, dim3(NTG), 0, s, a);
+      else hipLaunchKernelGGL((grad_kernel<TIn, K, 32, false>), grid, dim3(NTG), 0, s, a);
+    } else {
+      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 16, true>), grid, dim3(NTG), 0, s, a);
+      else hipLaunchKernelGGL((grad_kernel<TIn, K, 16, false>), grid, dim3(NTG), 0, s, a);
+    }
   }
   return (int)hipGetLastError();
 }
@@ -1435,6 +1490,7 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   a.uu = reinterpret_cast<float*>(ws + L.uu);
   a.du = reinterpret_cast<float*>(ws + L.du);
   a.r16 = reinterpret_cast<f16*>(ws + L.r16);
+  a.scl = reinterpret_cast<float*>(ws + L.scl);
   for (int d = 0; d < 3; ++d) {
     a.sq[d] = P.q_stride[d]; a.sk[d] = P.k_stride[d]; a.sv[d] = P.v_stride[d];
     a.sg[d] = P.g_stride[d]; a.sb[d] = P.beta_stride[d]; a.sdo[d] = P.do_stride[d];

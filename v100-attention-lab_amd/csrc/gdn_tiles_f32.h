@@ -92,6 +92,24 @@ struct RowLoad {
       }
     }
   }
+  // 16-bit rows as floats, columns [0, 16) times sc0 and [16, 32) times sc1
+  // (powers of two: exact)
+  template <int LD>
+  __device__ __forceinline__ void store_scaled(int tid, float (*dst)[LD], float sc0, float sc1) const {
+    static_assert(sizeof(TIn) == 2 && LD % 4 == 0 && COLS <= 32, "16-bit rows of at most 32 columns");
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (e < ROWS * RV) {
+        float x[VEC];
+        unpack16<TIn>(r[i], x);
+        const float sc = col < 16 ? sc0 : sc1;
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4)
+          *reinterpret_cast<f32x4*>(&dst[t][col + j]) = f32x4{x[j], x[j + 1], x[j + 2], x[j + 3]} * sc;
+      }
+    }
+  }
 };
 
 // One term sum_{kk < KD} a(m, kk) b(kk, n) of a product.
@@ -213,13 +231,13 @@ __device__ __forceinline__ f32x4 ld4(const float (*x)[LD], int row, int col) {
   return *reinterpret_cast<const f32x4*>(&x[row][col]);
 }
 
-// Chunk slot -> (sequence rows, chunk).  False for a slot that holds no
-// chunk (the gaps between packed sequences).
+// Chunk slot -> (sequence, its rows, chunk).  False for a slot that holds
+// no chunk (the gaps between packed sequences).
 // p: B (sequences when cu is set), T, nchmax = ceil(T / C), cu.
 template <int C, typename Args>
-__device__ __forceinline__ bool slot_chunk(const Args& p, int64_t slot, RowSpan& rs, int& c) {
+__device__ __forceinline__ bool slot_chunk(const Args& p, int64_t slot, RowSpan& rs, int& c, int& seq) {
   if (p.cu == nullptr) {
-    const int seq = (int)(slot / p.nchmax);
+    seq = (int)(slot / p.nchmax);
     c = (int)(slot % p.nchmax);
     rs = row_span(nullptr, p.T, seq);
     return seq < p.B && (int64_t)c * C < rs.T;
@@ -232,9 +250,15 @@ __device__ __forceinline__ bool slot_chunk(const Args& p, int64_t slot, RowSpan&
     else hi = mid - 1;
   }
   rs = row_span(p.cu, p.T, lo);
+  seq = lo;
   const int64_t cc = slot - (rs.t0 / C + lo);
   c = (int)cc;
   return cc >= 0 && cc * C < rs.T;
+}
+template <int C, typename Args>
+__device__ __forceinline__ bool slot_chunk(const Args& p, int64_t slot, RowSpan& rs, int& c) {
+  int seq;
+  return slot_chunk<C>(p, slot, rs, c, seq);
 }
 
 }  // namespace tiles
