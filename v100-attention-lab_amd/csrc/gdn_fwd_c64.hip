@@ -10,10 +10,11 @@
 // Only u, o and S' involve the carried state S.  The 64 x 64 substitution
 // for T is the long serial step and does not depend on S; it runs first,
 // for every chunk at once:
-//   1. prep, one workgroup per (chunk, head): gates and T (two 32 x 32
-//      diagonal solves, one lane per column, then the off-diagonal block
-//      T21 = -T22 A21 T11 on the matrix cores), written to a per-chunk
-//      record in the caller's workspace;
+//   1. prep, one workgroup per (chunk, head): gates and T on the VALU, as
+//      block forward substitution (the two 32 x 32 diagonal blocks by
+//      substitution at once, one lane per column, then the lower-left block
+//      T21 = -T22 A21 T11 as dot products over LDS rows), written to a
+//      per-chunk record in the caller's workspace;
 //   2. scan, one workgroup per (sequence, head, 16-column V slice): walks
 //      the chunks with S on chip (no chunk state is written), loading the
 //      next chunk's record and rows while the current one computes.
@@ -104,17 +105,22 @@ __device__ __forceinline__ void chunk_gates(int tid, const float* gl, float* b, 
 }
 
 // T = (I + A)^-1 for a strictly lower 64 x 64 A, given as at = A^T (a
-// barrier passed since it was written): T11 = (I + A11)^-1 (lanes 0-31 of
-// wave 0) and T22 = (I + A22)^-1 (lanes 0-31 of wave 1), one column per lane
-// held in registers, T12 = 0; then X = A21 T11 (x: 32 x 32 scratch) and
-// T21 = -T22 X on the matrix cores.  Ends with a barrier.
+// barrier passed since it was written), all on the VALU, as the block form
+// of forward substitution:
+//   * T11 = (I + A11)^-1 and T22 = (I + A22)^-1 by forward substitution at
+//     the same time, lanes 0-31 of waves 0 and 1, one column per lane held
+//     in registers, the rows of A broadcast from LDS (right-looking: once
+//     v[j] is final it is subtracted from every row below; row i still sums
+//     its terms in the order j = 0, 1, .., but the dependent chain is 32
+//     steps long, not 496);
+//   * the second block row, (I + A22) T21 = -A21 T11: X = A21 T11 (x: 32 x
+//     32 scratch), then T21 = -T22 X, as VALU dot products over LDS rows
+//     (every thread two entries of each).
+// T12 = 0.  Ends with a barrier.
 template <int XLD>
 __device__ __forceinline__ void solve_t(int tid, float (*at)[C + PAD], float (*t)[C + PAD], float (*x)[XLD]) {
   if ((tid & 63) < 32 && tid < 128) {
     const int o = tid < 64 ? 0 : 32, cc = tid & 31;
-    // right-looking substitution: once v[j] is final it is subtracted from
-    // every row below (row i still sums its terms in the order j = 0, 1, ..,
-    // but the dependent chain is 32 steps long, not 496)
     float v[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) v[i] = (i == cc) ? 1.f : 0.f;
@@ -125,16 +131,27 @@ __device__ __forceinline__ void solve_t(int tid, float (*at)[C + PAD], float (*t
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       t[o + i][o + cc] = v[i];
-      t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21 overwritten below)
+      t[o + i][32 - o + cc] = 0.f;  // T12 = 0 (and T21, overwritten below)
     }
   }
   __syncthreads();
-  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { x[m][n] = v; },
-                       seg<32>([&](int m, int kk) { return at[kk][32 + m]; }, [&](int kk, int n) { return t[kk][n]; }));
+  // X = A21 T11 (T11's zeros above its diagonal are exact)
+  for (int e = tid; e < 32 * 32; e += NT) {
+    const int m = e / 32, n = e % 32;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) acc = __builtin_fmaf(at[kk][32 + m], t[kk][n], acc);
+    x[m][n] = acc;
+  }
   __syncthreads();
-  mmx<NT, 32, 32, UNR>(tid, [&](int m, int n, float v) { t[32 + m][n] = -v; },
-                       seg<32>([&](int m, int kk) { return t[32 + m][32 + kk]; },
-                               [&](int kk, int n) { return x[kk][n]; }));
+  // T21 = -T22 X
+  for (int e = tid; e < 32 * 32; e += NT) {
+    const int m = e / 32, n = e % 32;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) acc = __builtin_fmaf(t[32 + m][32 + kk], x[kk][n], acc);
+    t[32 + m][n] = -acc;
+  }
   __syncthreads();
 }
 

@@ -577,10 +577,12 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
 
     // ---------------- P3: T = (I + A)^{-1} by forward substitution ----------
     if constexpr (C == 64) {
-      // Blocked: T = [[T11, 0], [T21, T22]] with T11 = (I + A11)^{-1} and
-      // T22 = (I + A22)^{-1} solved at the same time by waves 0 and 1 (lane c
-      // owns column c of its block), then T21 = -T22 (A21 T11).  Every block
-      // lands in place in s.a (fp32); the unused upper block holds A21 T11.
+      // Block forward substitution on the VALU, T = [[T11, 0], [T21, T22]]:
+      // T11 = (I + A11)^{-1} and T22 = (I + A22)^{-1} by substitution at the
+      // same time (waves 0 and 1, lane c owns column c of its block, written
+      // over A11 / A22); then the second block row, (I + A22) T21 = -A21 T11,
+      // as X = A21 T11 (into the unused upper-right block) and T21 = -T22 X
+      // (over A21), dot products over LDS rows by every thread.
       constexpr int H2 = 32;
       if (wave < 2 && lane < H2) {
         const int o = H2 * wave;
@@ -602,36 +604,23 @@ __global__ __launch_bounds__(kThreads) void gdn_fwd_kernel(const KArgs p) {
         for (int i = 0; i < H2; ++i) s.a[(o + i) * C + o + lane] = tc[i];
       }
       __syncthreads();
-      // 32 x 32 x 32 products in fp32 on the matrix cores
-      // (v_mfma_f32_16x16x4_f32): wave w makes the 16 x 16 tile (w / 2, w % 2).
-      // Lane (n, gq) supplies row n of the left operand and column n of the
-      // right one at contraction index 4 k4 + gq, and receives rows 4 gq + i.
-      static_assert(kWaves == 4, "one 16 x 16 tile per wave");
-      const int tr = 16 * (wave >> 1), tcl = 16 * (wave & 1);
-      // X = A21 T11 -> upper block (rows 0..31, columns 32..63)
-      {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k4 = 0; k4 < H2 / 4; ++k4) {
-          const int kk = 4 * k4 + gq;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.a[(H2 + tr + n) * C + kk], s.a[kk * C + tcl + n],
-                                                     acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s.a[(tr + 4 * gq + i) * C + H2 + tcl + n] = acc[i];
+      // X = A21 T11 -> upper-right block (T11's zeros above its diagonal are
+      // exact)
+      for (int e = tid; e < H2 * H2; e += kThreads) {
+        const int m = e / H2, nn = e % H2;
+        float acc = 0.f;
+#pragma unroll 8
+        for (int kk = 0; kk < H2; ++kk) acc = fmaf(s.a[(H2 + m) * C + kk], s.a[kk * C + nn], acc);
+        s.a[m * C + H2 + nn] = acc;
       }
       __syncthreads();
       // T21 = -T22 X -> lower-left block (A21 is no longer needed)
-      {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k4 = 0; k4 < H2 / 4; ++k4) {
-          const int kk = 4 * k4 + gq;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s.a[(H2 + tr + n) * C + H2 + kk],
-                                                     s.a[kk * C + H2 + tcl + n], acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s.a[(H2 + tr + 4 * gq + i) * C + tcl + n] = -acc[i];
+      for (int e = tid; e < H2 * H2; e += kThreads) {
+        const int m = e / H2, nn = e % H2;
+        float acc = 0.f;
+#pragma unroll 8
+        for (int kk = 0; kk < H2; ++kk) acc = fmaf(s.a[(H2 + m) * C + H2 + kk], s.a[kk * C + H2 + nn], acc);
+        s.a[(H2 + m) * C + nn] = -acc;
       }
       __syncthreads();
       for (int e = tid; e < C * C; e += kThreads) {
