@@ -122,17 +122,17 @@ typedef struct GdnFwdParams {
 /* Enqueue one chunked GDN forward on `stream` (a hipStream_t; NULL = the
  * legacy default stream).  Returns a GdnStatus / hipError_t value.
  * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140).
- *   - C = 32, fp16 q/k/v, K in {64, 128}, with a workspace: two launches per
+ *   - C = 32, fp16 q/k/v, K in {64, 128}, with a workspace, and C = 64 with
+ *     K in {32, 64, 128} (any dtype; block_v is 16 there): two launches per
  *     segment of the sequence (per-chunk records of the state-independent
  *     work, then the scan over chunks).  The segment length is what the
  *     workspace holds: workspace_bytes / (B * H * record bytes) chunks per
  *     sequence (at least one), so any workspace of at least
  *     gdn_fwd_workspace_size() bytes runs the call; a longer sequence runs
- *     as several segments, its state passing through final_state.
+ *     as several segments, its state passing through final_state in fp32.
+ *     C = 64 needs params->workspace.
  *   - C = 32 without a workspace (or GDN_FLAG_FUSED_KERNEL), bf16, or K = 256
  *     / GDN_FLAG_PHASED_KERNEL: one fused kernel, no workspace.
- *   - C = 64 with K in {32, 64, 128}: two launches (a per-chunk record, then
- *     the scan over chunks; block_v is 16 there); needs params->workspace.
  * The state stays on chip in every path: no chunk state is written. */
 int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
 
@@ -149,8 +149,10 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  *     as the array holds (B * H records of 3 KB per chunk); the call fails
  *     with GDN_ERR_SCRATCH_LIMIT only if one chunk per sequence does not
  *     fit (B * H > 10922).
- *   - 64-row chunks: GDN_ERR_SCRATCH_LIMIT when gdn_fwd_workspace_size()
- *     exceeds the array.
+ *   - 64-row chunks: likewise in segments (records of 33 KB per chunk and
+ *     head for 16-bit inputs, 66 KB for fp32 at K = 128); GDN_ERR_SCRATCH_LIMIT
+ *     only if one chunk per sequence does not fit (B * H > 992 for 16-bit
+ *     inputs).
  *   - Nothing is enqueued when a status other than GDN_OK is returned.
  * Every call on a device shares that device's array: calls that overlap
  * on one device (on different streams, or from different host threads)
@@ -161,9 +163,9 @@ int gdn_fwd_launch_noalloc(const GdnFwdParams* params, void* stream);
 int64_t gdn_fwd_scratch_bytes(void);
 
 /* Bytes of workspace gdn_fwd_launch needs for these params (0 for the fused
- * kernels; for 32-row chunks the records of a segment of at most 256 chunks
- * per sequence; B = the number of sequences when cu_seqlens is set); -1 if
- * the shape is invalid.  No counterpart in the reference, whose Triton
+ * kernels; the records of a segment of at most 256 chunks per sequence for
+ * 32-row chunks, at most 64 chunks for 64-row chunks; B = the number of
+ * sequences when cu_seqlens is set); -1 if the shape is invalid.  No counterpart in the reference, whose Triton
  * launch needs none. */
 int64_t gdn_fwd_workspace_size(const GdnFwdParams* params);
 

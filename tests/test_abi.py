@@ -121,17 +121,19 @@ def test_fwd_workspace_size(lib, pkg):
     rec32 = 4 * (2 * C * C + C * K + 3 * C)
     rec16 = 2 * 4 * C * C + 4 * 4 * C
     for dt, rec in ((0, rec32), (1, rec16), (2, rec16)):
-        want = 2 * (4096 // C) * H * rec
+        want = 2 * (4096 // C) * H * rec                 # 64 chunks: one segment
         assert want <= size(chunk_size=64, qkv_dtype=dt) < want + 256
+        # T = 16384: segments of 64 chunks, the same workspace
+        assert want <= size(chunk_size=64, qkv_dtype=dt, T=16384) < want + 256
     # the 16-bit record does not depend on K, the fp32 one does (W is C x K)
     for k_ in (32, 64):
         want16 = 2 * (4096 // C) * H * rec16
         want32 = 2 * (4096 // C) * H * 4 * (2 * C * C + C * k_ + 3 * C)
         assert want16 <= size(chunk_size=64, K=k_) < want16 + 256
         assert want32 <= size(chunk_size=64, K=k_, qkv_dtype=0) < want32 + 256
-    # packed sequences: slots ceil(T / C) + N = 2 + 3
+    # packed sequences: ceil(T / C) = 2 chunks of records for each of 3
     got = size(chunk_size=64, B=3, T=100, cu_seqlens=0x2000)
-    assert 5 * H * rec16 <= got < 5 * H * rec16 + 256
+    assert 3 * 2 * H * rec16 <= got < 3 * 2 * H * rec16 + 256
     assert size(chunk_size=64, B=0) == -1
     assert size(chunk_size=64, qkv_dtype=9) == -1
     assert lib.gdn_fwd_workspace_size(None) == -1
@@ -409,8 +411,8 @@ def test_noalloc_scratch_size(lib):
 @pytest.mark.parametrize("kw,code", [
     (dict(B=0), 1002), (dict(V=24), 1002), (dict(K=96), 1003), (dict(qkv_dtype=7), 1005),
     (dict(q=0x1008), 1004), (dict(final_state=None), 1001),
-    # 64-row records of B2 H16 T4096 (69 MB) exceed the 32 MiB array
-    (dict(chunk_size=64), 1007),
+    # one 33 KB 64-row record per (sequence, head) must fit: 1000 > 992 heads
+    (dict(chunk_size=64, B=1000, H=1, T=64), 1007),
     # one 3 KB record per (sequence, head) must fit: 11000 > 10922 heads
     (dict(B=11000, H=1, T=64), 1007),
 ])

@@ -289,33 +289,42 @@ def test_c64_degenerate_and_agrees_with_phased(pkg, cuda):
     assert ref.rel_err(o2, o) <= TOL_LOWP and ref.rel_err(fs2, fs) <= TOL_LOWP
 
 
-@pytest.mark.parametrize("T,seg", [(1000, 3), (4096, 1), (77, 2)])
-def test_segments_equal_one_pass(pkg, cuda, T, seg):
-    """The two-launch path with records for only `seg` chunks per sequence
-    runs a sequence as consecutive segments, the state passing through
-    final_state (fp32, exact): outputs are bit-equal to the one-segment run,
-    with and without h0, batched and packed."""
+SEG_CASES = [(1000, 3, 32, torch.float16), (4096, 1, 32, torch.float16), (77, 2, 32, torch.float16),
+             (1000, 3, 64, torch.float16), (4096, 1, 64, torch.float16), (200, 2, 64, torch.bfloat16),
+             (300, 2, 64, torch.float32)]
+
+
+@pytest.mark.parametrize("T,seg,C,dtype", SEG_CASES)
+def test_segments_equal_one_pass(pkg, cuda, T, seg, C, dtype):
+    """The two-launch paths (32-row fp16, 64-row any dtype) with records for
+    only `seg` chunks per sequence run a sequence as consecutive segments,
+    the state passing through final_state (fp32, exact): outputs are
+    bit-equal to the one-segment run, with and without h0, batched and
+    packed."""
     B, H, K, V = 2, 3, 128, 32
     q, k, v, g, beta, h0 = ref.make_inputs_baseline(B, T, H, K, V, seed=7, with_h0=True)
+    q, k, v = (t.to(dtype) for t in (q, k, v))
     d = lambda t: t.to(cuda)
-    print(f"[segments] T={T} seg={seg}", flush=True)
+    print(f"[segments] T={T} seg={seg} C={C} {dtype}", flush=True)
     for h in (None, h0):
-        o1, f1 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h))
-        o2, f2 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h),
+        o1, f1 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h), chunk_size=C)
+        o2, f2 = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), None if h is None else d(h), chunk_size=C,
                              max_segment_chunks=seg)
         torch.cuda.synchronize()
         assert torch.equal(o1.cpu(), o2.cpu()) and torch.equal(f1.cpu(), f2.cpu())
     o_ref, h_ref = _recurrent(q, k, v, g, beta, h0)
     eo, eh = ref.rel_err(o_ref, o2.cpu().float()), ref.rel_err(h_ref, f2.cpu())
-    _report(f"segments T={T} seg={seg}", eo, eh)
-    assert eh <= TOL_LOWP and eo <= TOL_LOWP + 2.0 ** -11
+    _report(f"segments T={T} seg={seg} C={C} {dtype}", eo, eh)
+    # o is stored in the input dtype: one rounding of it on top of the bar
+    o_round = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}[dtype]
+    assert eh <= TOL_LOWP and eo <= TOL_LOWP + o_round
     # packed sequences of unequal lengths: sequences end in different segments
     lens = [T // 3, 0, T - T // 3]
     cu = torch.tensor([0, lens[0], lens[0], T], dtype=torch.int64)
     qp, kp, vp, gp, bp = (t[:1] for t in (q, k, v, g, beta))
     hp = 0.1 * torch.randn(3, H, K, V, generator=torch.Generator().manual_seed(8))
-    o1, f1 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu))
-    o2, f2 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu),
+    o1, f1 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu), chunk_size=C)
+    o2, f2 = pkg.gdn_fwd(d(qp), d(kp), d(vp), d(gp), d(bp), d(hp), cu_seqlens=d(cu), chunk_size=C,
                          max_segment_chunks=seg)
     torch.cuda.synchronize()
     assert torch.equal(o1.cpu(), o2.cpu()) and torch.equal(f1.cpu(), f2.cpu())

@@ -85,12 +85,15 @@ def _both(pkg, cuda, B, T, H, K, V, dtype, chunk, seed):
 # (B, T, H, K, V, dtype, chunk): the first call runs 3 segments in the
 # scratch (1024 heads x 3 KB per chunk: 10 chunks of 22 fit) against one
 # segment with a caller workspace; the second is smaller and runs in one.
+# The sixth runs 64-row chunks in 10 segments of one chunk in the scratch
+# (512 heads x 33 KB per chunk) against one segment.
 CASES = [
     (2, 700, 512, 128, 64, torch.float16, 32),
     (1, 300, 4, 128, 64, torch.float16, 32),
     (2, 1000, 3, 64, 32, torch.float16, 64),
     (1, 200, 2, 128, 48, torch.bfloat16, 64),
     (2, 333, 4, 128, 128, torch.bfloat16, 32),
+    (1, 600, 512, 64, 32, torch.float16, 64),
 ]
 
 

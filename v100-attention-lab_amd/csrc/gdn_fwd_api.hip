@@ -132,8 +132,8 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   // what the path needs
   GdnFwdParams W = P;
   if (scratch_bytes > 0 && (c64 || scan32) && P.T > 0) {
-    const int64_t need = c64 ? c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype)
-                             : (int64_t)P.B * P.H * scan32_record_bytes();  // one chunk per sequence
+    // one chunk per sequence and head (longer sequences run in segments)
+    const int64_t need = (int64_t)P.B * P.H * (c64 ? c64_record_bytes(P.K, P.qkv_dtype) : scan32_record_bytes());
     if (need > scratch_bytes) return GDN_ERR_SCRATCH_LIMIT;
     void* ptr = nullptr;
     const int st = scratch_address(&ptr);
@@ -142,11 +142,11 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
     W.workspace_bytes = scratch_bytes;
   }
   if (c64) {
-    const int64_t need = c64_workspace_size(P.B, P.T, P.H, P.K, P.cu_seqlens ? P.B : 0, P.qkv_dtype);
-    if (P.T > 0 && (W.workspace == nullptr || reinterpret_cast<uintptr_t>(W.workspace) % 256 != 0 ||
-                    W.workspace_bytes < need))
-      return GDN_ERR_WORKSPACE;
-    return c64_launch(W, s);
+    // segment length: as many chunks per sequence as the workspace holds
+    const int64_t per_chunk = (int64_t)P.B * P.H * c64_record_bytes(P.K, P.qkv_dtype);
+    const int64_t L = W.workspace == nullptr ? 0 : W.workspace_bytes / per_chunk;
+    if (P.T > 0 && (reinterpret_cast<uintptr_t>(W.workspace) % 256 != 0 || L < 1)) return GDN_ERR_WORKSPACE;
+    return c64_launch(W, (int)(L < 1 ? 1 : L < 0x7fffffff ? L : 0x7fffffff), s);
   }
   if (scan32) {
     // segment length: as many chunks per sequence as the workspace holds

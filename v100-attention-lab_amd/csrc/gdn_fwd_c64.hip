@@ -23,8 +23,11 @@
 // pairs) keep T diag(beta), P and the gates there; the scan forms K S, u and
 // o from the q, k, v rows it loads anyway, and reads 67 KB per chunk and V
 // slice (K = 128; 98 KB with W in the record).
-// Packed sequences (cu_seqlens) number their chunk slots floor(t0 / C) + i
-// onwards, as in the backward.
+// The records of a segment of L chunks per (sequence, head) live in the
+// caller's workspace, [sequence][head][L]: a sequence of more than L chunks
+// runs as several (prep, scan) pairs, the state passing from one segment to
+// the next through final_state (in fp32, so the result does not depend on
+// L).  The workspace is bounded by B * H * L records, independent of T.
 
 #include "gdn_tiles_f16.h"
 
@@ -54,13 +57,30 @@ struct FArgs {
   float* rec;
   int64_t sq[3], sk[3], sv[3], sg[3], sb[3], so[3];
   int64_t sh0[4], sfs[4];
-  int B, T, H, V, nv, nchmax, units;
+  int B, T, H, V, nv, nchmax, units;  // B: sequences (units of row_span)
+  int c0, L;   // this segment: chunks [c0, c0 + L) of every sequence
+  int first;   // initial state from h0 (or zero) rather than final_state
   float scale;
   int g_dtype, beta_dtype, o_dtype;
   const int64_t* cu;
   int xcd_remap;
   int o_vec;  // o rows take 4-element vector stores (base and strides aligned)
 };
+
+// Record workgroup -> (sequence rows, chunk, record index).  The workgroups
+// of a segment enumerate (j, sequence, head), head fastest; record
+// ((sequence * H) + head) * L + j holds chunk c0 + j.  False past the end of
+// the sequence.
+__device__ __forceinline__ bool seg_chunk(const FArgs& p, int64_t blk, RowSpan& rs, int& c, int64_t& ri) {
+  const int hi = (int)(blk % p.H);
+  const int64_t rest = blk / p.H;
+  const int bi = (int)(rest % p.B);
+  const int j = (int)(rest / p.B);
+  rs = row_span(p.cu, p.T, bi);
+  c = p.c0 + j;
+  ri = ((int64_t)bi * p.H + hi) * p.L + j;
+  return (int64_t)c * C < rs.T;
+}
 
 // Per-(slot, head) record for fp32 inputs, in floats: T and P as [C][C], W
 // as [C][K], then gam and D as [C] each and gam_C (first of a [C] row).
@@ -171,13 +191,13 @@ __global__ __launch_bounds__(NT) void prep_kernel(const FArgs p) {
   using R = Rec<K>;
   __shared__ PSmem<K> s;
   const int tid = threadIdx.x;
-  const int64_t slot = blockIdx.x / p.H;
-  const int hi = blockIdx.x % p.H;
   RowSpan rs;
   int c;
-  if (!slot_chunk<C>(p, slot, rs, c)) return;
+  int64_t ri;
+  if (!seg_chunk(p, blockIdx.x, rs, c, ri)) return;
   const int t0 = c * C, nval = min(C, rs.T - t0);
-  float* const rec = p.rec + (slot * p.H + hi) * (int64_t)R::SIZE;
+  const int hi = blockIdx.x % p.H;
+  float* const rec = p.rec + ri * (int64_t)R::SIZE;
 
   {
     RowLoad<float, C, K, NT> lq, lk;
@@ -292,8 +312,10 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
   const int hi = bh % p.H;
   const int v0 = vs * BV;
   const RowSpan rs = row_span(p.cu, p.T, bi);
-  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
-  const int nch = (rs.T + C - 1) / C;
+  // this segment's chunks [c0, c0 + nloc) and their records
+  const int nloc = max(0, min(p.L, (rs.T + C - 1) / C - p.c0));
+  if (nloc == 0 && !p.first) return;  // state unchanged
+  const int64_t rb = ((int64_t)bi * p.H + hi) * p.L;
   const float scale = p.scale;
   const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
@@ -303,11 +325,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
 
   for (int e = tid; e < K * BV; e += NT) {
     const int kk = e / BV, c2 = e % BV;
-    s.S[kk][c2] = p.h0 ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]] : 0.f;
+    const int64_t off = kk * p.sfs[2] + (v0 + c2) * p.sfs[3];
+    s.S[kk][c2] = !p.first ? p.fs[bi * p.sfs[0] + hi * p.sfs[1] + off]
+                  : p.h0   ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + kk * p.sh0[2] + (v0 + c2) * p.sh0[3]]
+                           : 0.f;
   }
   Next<TIn, K> nx;
-  if (nch > 0) {
-    nx.load(p, tid, slot0 * p.H + hi, qg, kg, vg, bb, 0, min(C, rs.T));
+  if (nloc > 0) {
+    const int t0 = p.c0 * C;
+    nx.load(p, tid, rb, qg, kg, vg, bb, t0, min(C, rs.T - t0));
     nx.store(s, tid, p.beta_dtype);
   }
   __syncthreads();
@@ -315,10 +341,9 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
   // 16 (w - 4) .., then o of those rows
   const int um0 = 16 * (wave & 3);
   constexpr int NST = (K / 16 + 3) / 4;  // state tiles per wave: rows 16 (w + 4 j)
-  for (int c = 0; c < nch; ++c) {
-    const int t0 = c * C, nval = min(C, rs.T - t0);
-    if (c + 1 < nch)
-      nx.load(p, tid, (slot0 + c + 1) * p.H + hi, qg, kg, vg, bb, t0 + C, min(C, rs.T - t0 - C));
+  for (int j = 0; j < nloc; ++j) {
+    const int t0 = (p.c0 + j) * C, nval = min(C, rs.T - t0);
+    if (j + 1 < nloc) nx.load(p, tid, rb + j + 1, qg, kg, vg, bb, t0 + C, min(C, rs.T - t0 - C));
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (wave < 4) {
       // u = T diag(beta) V - W S
@@ -376,7 +401,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(const FArgs p) {
       }
     }
     __syncthreads();
-    if (c + 1 < nch) {
+    if (j + 1 < nloc) {
       nx.store(s, tid, p.beta_dtype);
       __syncthreads();
     }
@@ -445,13 +470,13 @@ template <typename TIn, int K>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(K == 64 ? 6 : 8))) void prep16_kernel(const FArgs p) {
   __shared__ P16mem<K> s;
   const int tid = threadIdx.x;
-  const int64_t slot = blockIdx.x / p.H;
-  const int hi = blockIdx.x % p.H;
   RowSpan rs;
   int c;
-  if (!slot_chunk<C>(p, slot, rs, c)) return;
+  int64_t ri;
+  if (!seg_chunk(p, blockIdx.x, rs, c, ri)) return;
   const int t0 = c * C, nval = min(C, rs.T - t0);
-  float* const rec = p.rec + (slot * p.H + hi) * (int64_t)Rec16::SIZE;
+  const int hi = blockIdx.x % p.H;
+  float* const rec = p.rec + ri * (int64_t)Rec16::SIZE;
   f16* const rh = reinterpret_cast<f16*>(rec);
 
   {
@@ -550,16 +575,32 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(K == 64 ? 6 
   }
 }
 
+// Row pitches of the scan's LDS arrays (in halves), from LDS bank-conflict
+// counters (64 banks of 4 bytes) of each access pattern:
+//  * arrays read only as 16-byte operand rows (q, k, T diag(beta), P; k is
+//    also read transposed): a pitch of 16 halves past a multiple of 64
+//    (8 words past a multiple of 32) gives conflict-free 16-byte row reads;
+//  * arrays written in the accumulator layout (8 bytes per lane, lane (r, kq)
+//    at row r: S^T, Y^T, u^T, (D u)^T) and read as operand rows: a pitch of
+//    4 halves past a multiple of 64 (2 words past a multiple of 32) gives
+//    conflict-free 8-byte stores, and the rows are then read by two 8-byte
+//    reads (frag8_2; the rows are only 8-byte aligned).  At 8 halves of
+//    padding the stores conflicted two ways and the 16-byte reads as well.
+template <int K>
+constexpr int s16_kq() {
+  return (K + 63) / 64 * 64 + 16;
+}
 template <int K>
 struct alignas(16) S16mem {
-  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
-  f16 q[C][K + HP], k[C][K + HP];
-  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
-  f16 ph[C][C + HP], pl[C][C + HP];    // P
-  f16 vt[BV][C + HP];                  // V^T of the slice
-  f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
-  f16 uh[BV][C + HP], ul[BV][C + HP];  // u^T
-  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
+  static constexpr int KQ = s16_kq<K>(), CQ = C + 16, KS = K + 4, CS = C + 4;
+  f16 sh[BV][KS], sl[BV][KS];  // S^T
+  f16 q[C][KQ], k[C][KQ];
+  f16 th[C][CQ], tl[C][CQ];    // T diag(beta)
+  f16 ph[C][CQ], pl[C][CQ];    // P
+  f16 vt[BV][CS];              // V^T of the slice
+  f16 yh[BV][CS], yl[BV][CS];  // (V - diag(gam) K S)^T
+  f16 uh[BV][CS], ul[BV][CS];  // u^T
+  f16 dh[BV][CS], dl[BV][CS];  // (diag(D) u)^T
   // gam, D, b, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
   float gv[NT / C][C];
@@ -618,17 +659,25 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
   const int hi = bh % p.H;
   const int v0 = vs * BV;
   const RowSpan rs = row_span(p.cu, p.T, bi);
-  const int64_t slot0 = p.cu ? rs.t0 / C + bi : (int64_t)bi * p.nchmax;
-  const int nch = (rs.T + C - 1) / C;
+  // this segment's chunks [c0, c0 + nloc) and their records
+  const int nloc = max(0, min(p.L, (rs.T + C - 1) / C - p.c0));
+  if (nloc == 0 && !p.first) return;  // state unchanged
+  const int64_t rb = ((int64_t)bi * p.H + hi) * p.L;
   const TIn* const qg = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq);
   const TIn* const kg = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk);
   const TIn* const vg = static_cast<const TIn*>(p.v) + head_base(rs, hi, p.sv) + v0;
   const int64_t ob = head_base(rs, hi, p.so) + v0;
-  // bf16: this slice's v and h0 scaled into fp16's range, o and the final
-  // state scaled back (identity for fp16)
+  // the state entering the segment: h0 (or zero), or the previous segment's
+  const float* const s_in = p.first ? (p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr)
+                                    : p.fs + bi * p.sfs[0] + hi * p.sfs[1] + v0 * p.sfs[3];
+  const int64_t sik = p.first ? p.sh0[2] : p.sfs[2], siv = p.first ? p.sh0[3] : p.sfs[3];
+  // bf16: this segment's rows of the v slice and its entering state scaled
+  // into fp16's range, o and the state leaving it scaled back (identity for
+  // fp16)
+  const int r0 = min(rs.T, p.c0 * C);
   const RangeScale rsc = slice_range_scale<TIn>(
-      reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), rs.T, BV,
-      p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, p.scale);
+      reinterpret_cast<const char*>(vg + (int64_t)r0 * p.sv[1]), p.sv[1] * (int64_t)sizeof(TIn),
+      min(rs.T - r0, nloc * C), BV, s_in, sik, siv, K, p.scale);
   const float scale = rsc.o;
 
   constexpr int NST = (K / 16 + 3) / 4;
@@ -652,33 +701,31 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
       const int m0 = 16 * (wave + 4 * j);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        st[j][i] = (p.h0 && m0 < K)
-                       ? p.h0[bi * p.sh0[0] + hi * p.sh0[1] + (m0 + 4 * kq + i) * p.sh0[2] + (v0 + r) * p.sh0[3]] * rsc.v
-                       : 0.f;
+        st[j][i] = (s_in && m0 < K) ? s_in[(m0 + 4 * kq + i) * sik + r * siv] * rsc.v : 0.f;
     }
     put_state();
   }
   Next16<TIn, K> nx;
-  if (nch > 0) {
-    nx.load(p, tid, slot0 * p.H + hi, qg, kg, vg, 0, min(C, rs.T));
+  if (nloc > 0) {
+    nx.load(p, tid, rb, qg, kg, vg, r0, min(C, rs.T - r0));
     nx.store(s, tid, rsc.v);
   }
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
-    const int t0 = c * C, nval = min(C, rs.T - t0);
+  for (int j = 0; j < nloc; ++j) {
+    const int t0 = (p.c0 + j) * C, nval = min(C, rs.T - t0);
     // the next chunk's record and rows (the last chunk's again at the end:
     // every load is then consumed by the staging below, on every path)
-    const int cn = min(c + 1, nch - 1);
-    nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, vg, cn * C, min(C, rs.T - cn * C));
+    const int jn = min(j + 1, nloc - 1), tn = (p.c0 + jn) * C;
+    nx.load(p, tid, rb + jn, qg, kg, vg, tn, min(C, rs.T - tn));
     // K S (waves 0-3) or Q S (waves 4-7) for rows um0 ..
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     {
-      const f16(*const a)[K + HP] = upper ? s.k : s.q;
+      const f16(*const a)[S16mem<K>::KQ] = upper ? s.k : s.q;
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
         const f16x8 af = frag8(&a[um0 + r][kb + 8 * kq]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8(&s.sh[r][kb + 8 * kq]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8(&s.sl[r][kb + 8 * kq]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8_2(&s.sh[r][kb + 8 * kq]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, frag8_2(&s.sl[r][kb + 8 * kq]), acc, 0, 0, 0);
       }
     }
     if (upper) {
@@ -698,9 +745,9 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 #pragma unroll
       for (int jb = 0; jb < C; jb += 32)
         if (jb < um0 + 16) {
-          const f16x8 th = frag8(&s.th[um0 + r][jb + 8 * kq]), yh = frag8(&s.yh[r][jb + 8 * kq]);
+          const f16x8 th = frag8(&s.th[um0 + r][jb + 8 * kq]), yh = frag8_2(&s.yh[r][jb + 8 * kq]);
           au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, yh, au, 0, 0, 0);
-          au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8(&s.yl[r][jb + 8 * kq]), au, 0, 0, 0);
+          au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8_2(&s.yl[r][jb + 8 * kq]), au, 0, 0, 0);
           au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][jb + 8 * kq]), yh, au, 0, 0, 0);
         }
       // u^T and (diag(D) u)^T as fp16 pairs: lane holds u rows um0 + 4 kq + i, column r
@@ -721,8 +768,8 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 #pragma unroll
           for (int tb = 0; tb < C; tb += 32) {
             const f16x8 kt = frag8_t(s.k, tb, m0, r, kq);
-            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][tb + 8 * kq]), a, 0, 0, 0);
-            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][tb + 8 * kq]), a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8_2(&s.dh[r][tb + 8 * kq]), a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8_2(&s.dl[r][tb + 8 * kq]), a, 0, 0, 0);
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) st[j][i] = s.gv[3][0] * st[j][i] + a[i];
@@ -735,9 +782,9 @@ __global__ __launch_bounds__(NT) void scan16_kernel(const FArgs p) {
 #pragma unroll
       for (int jb = 0; jb < C; jb += 32)
         if (jb < um0 + 16) {
-          const f16x8 ph = frag8(&s.ph[um0 + r][jb + 8 * kq]), uh = frag8(&s.uh[r][jb + 8 * kq]);
+          const f16x8 ph = frag8(&s.ph[um0 + r][jb + 8 * kq]), uh = frag8_2(&s.uh[r][jb + 8 * kq]);
           ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, uh, ao, 0, 0, 0);
-          ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
+          ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, frag8_2(&s.ul[r][jb + 8 * kq]), ao, 0, 0, 0);
           ao = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.pl[um0 + r][jb + 8 * kq]), uh, ao, 0, 0, 0);
         }
       const int row0 = um0 + 4 * kq;
@@ -807,18 +854,24 @@ inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace c64
 
-// Chunk slots x heads x record size, in bytes.
+// Bytes of one record (chunk, head) for this input dtype.
+int64_t c64_record_bytes(int K, int qkv_dtype) { return c64::rec_floats(K, qkv_dtype != GDN_DTYPE_F32) * 4; }
+
+// Records of min(ceil(T / C), kSegC64) chunks per (sequence, head), in bytes:
+// longer sequences run in segments of that many chunks.
 int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype) {
   const int64_t nch = (T + c64::C - 1) / c64::C;
-  const int64_t nslot = n_seq > 0 ? nch + n_seq : (int64_t)B * nch;
-  return c64::align256(nslot * H * c64::rec_floats(K, qkv_dtype != GDN_DTYPE_F32) * 4);
+  const int64_t L = nch < kSegC64 ? nch : kSegC64;
+  const int64_t nseq = n_seq > 0 ? n_seq : B;
+  return c64::align256(nseq * H * L * c64_record_bytes(K, qkv_dtype));
 }
 
 bool c64_supported(int K, int C, int V) { return C == c64::C && (K == 32 || K == 64 || K == 128) && V % 16 == 0; }
 
-// Enqueue the two launches (arguments checked by the caller).
-int c64_launch(const GdnFwdParams& P, hipStream_t stream) {
-  const int n_seq = P.cu_seqlens ? P.B : 0;
+// Enqueue the (prep, scan) launches of every segment of seg_chunks chunks
+// (arguments, and a workspace of B * H * seg_chunks records, checked by the
+// caller).
+int c64_launch(const GdnFwdParams& P, int seg_chunks, hipStream_t stream) {
   c64::FArgs a = {};
   a.q = P.q; a.k = P.k; a.v = P.v; a.g = P.g; a.beta = P.beta; a.h0 = P.h0;
   a.o = P.o; a.fs = P.final_state;
@@ -842,14 +895,24 @@ int c64_launch(const GdnFwdParams& P, hipStream_t stream) {
     a.o_vec = reinterpret_cast<uintptr_t>(P.o) % vb == 0 && (P.o_stride[0] * eb) % vb == 0 &&
               (P.o_stride[1] * eb) % vb == 0 && (P.o_stride[2] * eb) % vb == 0;
   }
-  const int64_t nslot = n_seq > 0 ? a.nchmax + n_seq : (int64_t)P.B * a.nchmax;
-  const int64_t nrec = P.T > 0 ? nslot * P.H : 0;
+  // every sequence has at most ceil(T / C) chunks (the offsets are not read here)
+  const int L = a.nchmax > 0 ? (seg_chunks < a.nchmax ? seg_chunks : a.nchmax) : 1;
+  const int nseg = a.nchmax > 0 ? (a.nchmax + L - 1) / L : 1;
+  const int64_t nrec = a.nchmax > 0 ? (int64_t)P.B * P.H * L : 0;
   if (nrec > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
-  switch (P.qkv_dtype) {
-    case GDN_DTYPE_F16: return c64::launch_t<f16>(a, P.K, nrec, stream);
-    case GDN_DTYPE_BF16: return c64::launch_t<bf16_t>(a, P.K, nrec, stream);
-    default: return c64::launch_t<float>(a, P.K, nrec, stream);
+  a.L = L;
+  for (int sg = 0; sg < nseg; ++sg) {
+    a.c0 = sg * L;
+    a.first = sg == 0;
+    int st;
+    switch (P.qkv_dtype) {
+      case GDN_DTYPE_F16: st = c64::launch_t<f16>(a, P.K, nrec, stream); break;
+      case GDN_DTYPE_BF16: st = c64::launch_t<bf16_t>(a, P.K, nrec, stream); break;
+      default: st = c64::launch_t<float>(a, P.K, nrec, stream); break;
+    }
+    if (st != 0) return st;
   }
+  return GDN_OK;
 }
 
 }  // namespace gdn

@@ -865,8 +865,12 @@ int launch_pipe_bf16(const KArgs& a, int K, int bv, int grid, hipStream_t s);
 // 64-row chunks with K in {32, 64, 128} run as two launches (gdn_fwd_c64.hip)
 // over a caller-owned workspace of per-chunk records.
 bool c64_supported(int K, int C, int V);
+// 64-row chunks: chunks per (sequence, head) whose records the default
+// workspace holds; longer sequences run in segments of this many chunks.
+constexpr int64_t kSegC64 = 64;
+int64_t c64_record_bytes(int K, int qkv_dtype);
 int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype);
-int c64_launch(const GdnFwdParams& P, hipStream_t stream);
+int c64_launch(const GdnFwdParams& P, int seg_chunks, hipStream_t stream);
 // 32-row chunks, fp16, K in {64, 128}, BV in {16, 32}: per-chunk records
 // then the scan (gdn_fwd_scan32.hip), in segments of at most seg_chunks
 // chunks per sequence whose records fit the caller's workspace.

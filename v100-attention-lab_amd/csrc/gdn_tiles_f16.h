@@ -19,6 +19,11 @@ using namespace tiles;
 constexpr int HP = 8;  // LDS row padding in halves (rows stay 16-byte aligned)
 
 __device__ __forceinline__ f16x8 frag8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
+// the same 8 halves by two 8-byte reads (rows only 8-byte aligned)
+__device__ __forceinline__ f16x8 frag8_2(const f16* p) {
+  const f16x4 a = *reinterpret_cast<const f16x4*>(p), b = *reinterpret_cast<const f16x4*>(p + 4);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 // x as an fp16 pair hi + lo.
 __device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {

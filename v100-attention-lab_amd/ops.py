@@ -180,13 +180,13 @@ def _make_plan(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, k
     ws = lib.gdn_fwd_workspace_size(ctypes.byref(P))
     if ws < 0:
         raise ValueError(f"unsupported forward shape B={B} T={T} H={H} K={K} V={V}")
-    if seg_chunks is not None and ws > 0 and chunk_size == 32:
+    if seg_chunks is not None and ws > 0:
         # the records of seg_chunks chunks per sequence (what a call of
-        # seg_chunks * 32 rows takes): the call then runs in segments of that
-        # many chunks (fewer records, more launches)
+        # seg_chunks * chunk_size rows takes): the call then runs in segments
+        # of that many chunks (fewer records, more launches)
         if int(seg_chunks) < 1:
             raise ValueError(f"max_segment_chunks must be >= 1, got {seg_chunks}")
-        P.T = min(T, 32 * int(seg_chunks))
+        P.T = min(T, chunk_size * int(seg_chunks))
         ws = lib.gdn_fwd_workspace_size(ctypes.byref(P))
         P.T = T
     P.cu_seqlens = None
@@ -292,9 +292,10 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         packed along t of a batch of one (B = 1); sequence i is rows
         ``cu_seqlens[i]:cu_seqlens[i+1]`` with its own ``h0[i]`` and
         ``final_state[i]`` (h0 and final_state are then ``[N, H, K, V]``).
-      max_segment_chunks: for the two-launch 32-row path, the records of at
-        most this many chunks per sequence are held at once; a longer
-        sequence runs as several segments (default: 256 chunks).
+      max_segment_chunks: for the two-launch paths, the records of at most
+        this many chunks per sequence are held at once; a longer sequence
+        runs as several segments (default: 256 chunks of 32 rows, 64 chunks
+        of 64 rows).
 
     Returns:
       ``o [B, T, H, V]`` and ``final_state [B, H, K, V]`` float32.  When an
