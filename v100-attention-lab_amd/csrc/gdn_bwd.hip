@@ -1027,7 +1027,10 @@ struct alignas(16) GSmem {
 // VS: V columns per step of the V walk (32, or 16 when V is an odd
 // multiple of 16).  ST16: ckS and ckD hold fp16 in the walks' shifted units
 // (the 16-bit walks), scaled back per 16-column slice by scl when staged.
-template <typename TIn, int K, int VS, bool ST16>
+// NVS: the number of V steps when fixed at compile time (V = 128 or 64;
+// 0: V / VS at run time), so that the walk unrolls into straight-line code
+// whose waits cover exactly the step being staged.
+template <typename TIn, int K, int VS, bool ST16, int NVS>
 __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   using R = Rec<K>;
   constexpr int RL = NTG / C;
@@ -1102,52 +1105,78 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   float vu_acc[4] = {0.f, 0.f, 0.f, 0.f};
   float dgc_acc = 0.f;
 
-  const int nvs = p.V / VS;
-  RowLoad<TIn, C, VS, NTG> lv;
-  RowLoad<float, C, VS, NTG> lu, ldu;
-  RowLoad<TS, K, VS, NTG> lS, ldS;
-  float scS[2] = {1.f, 1.f}, scD[2] = {1.f, 1.f};
+  const int nvs = NVS > 0 ? NVS : p.V / VS;
   constexpr int NDO = C * VS / NTG;
   static_assert(C * VS % NTG == 0, "dO elements per thread");
-  uint32_t rdo[NDO];
-  auto load_step = [&](int vsi) __attribute__((always_inline)) {
+  // One V step's rows in registers.  Two of them alternate, so that the
+  // loads of a step are issued two steps before it (each has a whole step's
+  // products to arrive).
+  // Every load of a step is unconditional (rows past the chunk's end read
+  // its last row again and are zeroed when stored), so that staging one
+  // step waits only for that step's loads.  With the 16-bit walks dO has
+  // q's dtype and 4-byte aligned rows: one element pair per thread.
+  constexpr int NDP = C * VS / 2;  // dO element pairs of a step (VS = 16: waves 0-3 only)
+  static_assert(!ST16 || NDP == NTG || NDP == NTG / 2, "at most one dO pair per thread");
+  struct StepRows {
+    RowLoad<TIn, C, VS, NTG> lv;
+    RowLoad<float, C, VS, NTG> lu, ldu;
+    RowLoad<TS, K, VS, NTG> lS, ldS;
+    float scS[2], scD[2];
+    uint32_t rdo[NDO];
+  };
+  auto load_step = [&](StepRows& x, int vsi) __attribute__((always_inline)) {
     const int v0 = vsi * VS;
-    lv.load(tid, static_cast<const TIn*>(p.v) + vb + v0, p.sv[1], nval);
-    lu.load(tid, uu + v0, p.V, C);
-    ldu.load(tid, dug + v0, p.V, C);
-    lS.load(tid, cks + v0, p.V, K);
-    ldS.load(tid, ckd + v0, p.V, K);
+    x.lv.load_clamped(tid, static_cast<const TIn*>(p.v) + vb + v0, p.sv[1], nval);
+    x.lu.load_clamped(tid, uu + v0, p.V, C);
+    x.ldu.load_clamped(tid, dug + v0, p.V, C);
+    x.lS.load_clamped(tid, cks + v0, p.V, K);
+    x.ldS.load_clamped(tid, ckd + v0, p.V, K);
+    x.scS[0] = x.scS[1] = x.scD[0] = x.scD[1] = 1.f;
     if constexpr (ST16) {
 #pragma unroll
       for (int j = 0; j < VS / 16; ++j) {
-        scS[j] = sclS[v0 / 16 + j];
-        scD[j] = sclD[v0 / 16 + j];
+        x.scS[j] = sclS[v0 / 16 + j];
+        x.scD[j] = sclD[v0 / 16 + j];
+      }
+      const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
+      if (NDP == NTG || tid < NDP)
+        x.rdo[0] = *reinterpret_cast<const uint32_t*>(static_cast<const TIn*>(p.d_o) + dob +
+                                                      (int64_t)min(t, nval - 1) * p.sdo[1] + v0 + c2);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NDO; ++i) {
+        const int e = tid + i * NTG, t = e / VS, c2 = e % VS;
+        x.rdo[i] = t < nval ? load_bits(p.d_o, dob + (int64_t)t * p.sdo[1] + v0 + c2, p.do_dtype) : 0u;
       }
     }
-#pragma unroll
-    for (int i = 0; i < NDO; ++i) {
-      const int e = tid + i * NTG, t = e / VS, c2 = e % VS;
-      rdo[i] = t < nval ? load_bits(p.d_o, dob + (int64_t)t * p.sdo[1] + v0 + c2, p.do_dtype) : 0u;
-    }
   };
-  auto store_step = [&]() __attribute__((always_inline)) {
-    lv.store(tid, s.v);
-    lu.store(tid, s.u);
-    ldu.store(tid, s.du);
+  auto store_step = [&](const StepRows& x) __attribute__((always_inline)) {
+    x.lv.store_masked(tid, s.v, nval);
+    x.lu.store(tid, s.u);
+    x.ldu.store(tid, s.du);
     if constexpr (ST16) {
-      lS.store_scaled(tid, s.S, scS[0], scS[1]);
-      ldS.store_scaled(tid, s.dS, scD[0], scD[1]);
+      x.lS.store_scaled(tid, s.S, x.scS[0], x.scS[1]);
+      x.ldS.store_scaled(tid, s.dS, x.scD[0], x.scD[1]);
+      const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
+      if (NDP == NTG || tid < NDP) {
+        // dO has q's dtype here: a compile-time conversion
+        constexpr int dt = std::is_same<TIn, f16>::value ? GDN_DTYPE_F16 : GDN_DTYPE_BF16;
+        const bool ok = t < nval;
+        s.dO[t][c2] = ok ? bits_to_float(x.rdo[0] & 0xffffu, dt) : 0.f;
+        s.dO[t][c2 + 1] = ok ? bits_to_float(x.rdo[0] >> 16, dt) : 0.f;
+      }
     } else {
-      lS.store(tid, s.S);
-      ldS.store(tid, s.dS);
-    }
+      x.lS.store(tid, s.S);
+      x.ldS.store(tid, s.dS);
 #pragma unroll
-    for (int i = 0; i < NDO; ++i) {
-      const int e = tid + i * NTG;
-      s.dO[e / VS][e % VS] = bits_to_float(rdo[i], p.do_dtype);
+      for (int i = 0; i < NDO; ++i) {
+        const int e = tid + i * NTG;
+        s.dO[e / VS][e % VS] = bits_to_float(x.rdo[i], p.do_dtype);
+      }
     }
   };
-  load_step(0);
+  StepRows ra, rb;
+  load_step(ra, 0);
   lq.store(tid, s.q);
   lk.store(tid, s.k);
   lt.store(tid, s.t);
@@ -1163,13 +1192,16 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   } else if (tid == 3 * C) {
     s.gC = gate;
   }
-  store_step();
+  store_step(ra);
+  if (nvs > 1) load_step(rb, 1);
   __syncthreads();
   for (int e = tid; e < C * C; e += NTG) {
     const int t = e / C, j = e % C;
     s.m[t][j] = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
   }
-  for (int vsi = 0; vsi < nvs; ++vsi) {
+  // step vsi: `cur` holds step vsi + 1's rows (loaded a step ago), `nxt`
+  // receives step vsi + 2's
+  auto step = [&](int vsi, StepRows& cur, StepRows& nxt) __attribute__((always_inline)) {
     const int v0 = vsi * VS;
     // dU~ of the step and dv first: its stores go out before the next
     // step's loads, so that waiting for those loads does not wait for them
@@ -1185,7 +1217,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
         vu_acc[i] = __builtin_fmaf(s.v[row][col], a[0][i], vu_acc[i]);
       }
     }
-    if (vsi + 1 < nvs) load_step(vsi + 1);
+    if (vsi + 2 < nvs) load_step(nxt, vsi + 2);
     // Products contracted over the step's V columns, all of the form
     // X[m][v] Y[n][v]: the contraction runs in 16-column groups in which
     // lane (r, kq) covers columns 4 kq .. 4 kq + 3 over four MFMA steps, so
@@ -1217,8 +1249,20 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     for (int e = tid; e < K * VS; e += NTG) dgc_acc = __builtin_fmaf(s.S[e / VS][e % VS], s.dS[e / VS][e % VS], dgc_acc);
     __syncthreads();
     if (vsi + 1 < nvs) {
-      store_step();
+      store_step(cur);
       __syncthreads();
+    }
+  };
+  if constexpr (NVS > 0) {
+#pragma unroll
+    for (int vsi = 0; vsi < NVS; vsi += 2) {
+      step(vsi, rb, ra);
+      if (vsi + 1 < NVS) step(vsi + 1, ra, rb);
+    }
+  } else {
+    for (int vsi = 0; vsi < nvs; vsi += 2) {
+      step(vsi, rb, ra);
+      if (vsi + 1 < nvs) step(vsi + 1, ra, rb);
     }
   }
 
@@ -1413,12 +1457,15 @@ int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
   if (nrec > 0) {
     const dim3 grid((unsigned)nrec);
     const bool st16 = !std::is_same<TIn, float>::value && a.w16;
-    if (a.V % 32 == 0) {
-      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 32, true>), grid, dim3(NTG), 0, s, a);
-      else hipLaunchKernelGGL((grad_kernel<TIn, K, 32, false>), grid, dim3(NTG), 0, s, a);
+    if (a.V == 128) {
+      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 32, true, 4>), grid, dim3(NTG), 0, s, a);
+      else hipLaunchKernelGGL((grad_kernel<TIn, K, 32, false, 4>), grid, dim3(NTG), 0, s, a);
+    } else if (a.V % 32 == 0) {
+      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 32, true, 0>), grid, dim3(NTG), 0, s, a);
+      else hipLaunchKernelGGL((grad_kernel<TIn, K, 32, false, 0>), grid, dim3(NTG), 0, s, a);
     } else {
-      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 16, true>), grid, dim3(NTG), 0, s, a);
-      else hipLaunchKernelGGL((grad_kernel<TIn, K, 16, false>), grid, dim3(NTG), 0, s, a);
+      if (st16) hipLaunchKernelGGL((grad_kernel<TIn, K, 16, true, 0>), grid, dim3(NTG), 0, s, a);
+      else hipLaunchKernelGGL((grad_kernel<TIn, K, 16, false, 0>), grid, dim3(NTG), 0, s, a);
     }
   }
   return (int)hipGetLastError();

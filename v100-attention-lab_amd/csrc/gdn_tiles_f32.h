@@ -69,6 +69,36 @@ struct RowLoad {
       r[i] = (e < ROWS * RV && t < nvalid) ? *reinterpret_cast<const u32x4*>(base + t * rs + col) : z;
     }
   }
+  // Every lane loads (rows >= nvalid >= 1 read row nvalid - 1 again), so
+  // that no load is lane-masked: a masked load makes the compiler wait for
+  // every load in flight before the values are used.  store_masked zeroes
+  // those rows.
+  __device__ __forceinline__ void load_clamped(int tid, const TIn* base, int64_t rs, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (ROWS * RV % NT == 0 || e < ROWS * RV)
+        r[i] = *reinterpret_cast<const u32x4*>(base + min(t, nvalid - 1) * rs + col);
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void store_masked(int tid, float (*dst)[LD], int nvalid) const {
+    static_assert(LD % 4 == 0, "16-byte rows");
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (ROWS * RV % NT == 0 || e < ROWS * RV) {
+        float x[VEC];
+        unpack16<TIn>(r[i], x);
+        const bool ok = t < nvalid;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) x[j] = ok ? x[j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4)
+          *reinterpret_cast<f32x4*>(&dst[t][col + j]) = f32x4{x[j], x[j + 1], x[j + 2], x[j + 3]};
+      }
+    }
+  }
   template <int LD>
   __device__ __forceinline__ void store(int tid, float (*dst)[LD]) const {
 #pragma unroll
