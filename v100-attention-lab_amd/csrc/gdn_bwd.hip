@@ -1014,8 +1014,20 @@ struct alignas(16) GSmem {
   float yp[C][CD];   // dQK o Q K^T = scale (dO u^T) o P
   float dt[C][CD];   // dT, then dA
   float z[C][CD];    // T^T dT, then dKK
-  float v[C][SD], dO[C][SD], u[C][SD], du[C][SD];
-  float S[K][SD], dS[K][SD];
+  // The V step's tiles: fp32 (w), or for fp16 inputs with fp16 states
+  // MFMA operand rows in fp16 (h: v, dO and the states exact, u and du as
+  // hi + lo pairs; HD = VS + 16 halves, 16-byte aligned rows).
+  static constexpr int HD = VS + 16;
+  union {
+    struct {
+      float v[C][SD], dO[C][SD], u[C][SD], du[C][SD];
+      float S[K][SD], dS[K][SD];
+    } w;
+    struct {
+      f16 v[C][HD], dO[C][HD], uh[C][HD], ul[C][HD], dh[C][HD], dl[C][HD];
+      f16 S[K][HD], dS[K][HD];
+    } h;
+  };
   float b[C], gam[C], D[C], bt[C];
   float rq[K / 16][C], rk[K / 16][C];  // row partials, one row per 16-column tile
   float vu[VS / 16][C];  // v.dU~ row partials, one row per 16-column tile
@@ -1034,6 +1046,9 @@ template <typename TIn, int K, int VS, bool ST16, int NVS>
 __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   using R = Rec<K>;
   constexpr int RL = NTG / C;
+  // fp16 inputs with fp16 states (no range shift): the V walk's products on
+  // v_mfma_f32_16x16x32_f16, one 32-column step per product
+  constexpr bool F16W = ST16 && std::is_same<TIn, f16>::value && VS == 32;
   __shared__ GSmem<K, VS> s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1151,27 +1166,37 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     }
   };
   auto store_step = [&](const StepRows& x) __attribute__((always_inline)) {
-    x.lv.store_masked(tid, s.v, nval);
-    x.lu.store(tid, s.u);
-    x.ldu.store(tid, s.du);
+    if constexpr (F16W) {
+      x.lv.store_raw(tid, s.h.v, nval);
+      x.lu.store_pairs(tid, s.h.uh, s.h.ul);
+      x.ldu.store_pairs(tid, s.h.dh, s.h.dl);
+      x.lS.store_raw(tid, s.h.S);
+      x.ldS.store_raw(tid, s.h.dS);
+      const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
+      if (NDP == NTG || tid < NDP) *reinterpret_cast<uint32_t*>(&s.h.dO[t][c2]) = t < nval ? x.rdo[0] : 0u;
+      return;
+    }
+    x.lv.store_masked(tid, s.w.v, nval);
+    x.lu.store(tid, s.w.u);
+    x.ldu.store(tid, s.w.du);
     if constexpr (ST16) {
-      x.lS.store_scaled(tid, s.S, x.scS[0], x.scS[1]);
-      x.ldS.store_scaled(tid, s.dS, x.scD[0], x.scD[1]);
+      x.lS.store_scaled(tid, s.w.S, x.scS[0], x.scS[1]);
+      x.ldS.store_scaled(tid, s.w.dS, x.scD[0], x.scD[1]);
       const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
       if (NDP == NTG || tid < NDP) {
         // dO has q's dtype here: a compile-time conversion
         constexpr int dt = std::is_same<TIn, f16>::value ? GDN_DTYPE_F16 : GDN_DTYPE_BF16;
         const bool ok = t < nval;
-        s.dO[t][c2] = ok ? bits_to_float(x.rdo[0] & 0xffffu, dt) : 0.f;
-        s.dO[t][c2 + 1] = ok ? bits_to_float(x.rdo[0] >> 16, dt) : 0.f;
+        s.w.dO[t][c2] = ok ? bits_to_float(x.rdo[0] & 0xffffu, dt) : 0.f;
+        s.w.dO[t][c2 + 1] = ok ? bits_to_float(x.rdo[0] >> 16, dt) : 0.f;
       }
     } else {
-      x.lS.store(tid, s.S);
-      x.ldS.store(tid, s.dS);
+      x.lS.store(tid, s.w.S);
+      x.ldS.store(tid, s.w.dS);
 #pragma unroll
       for (int i = 0; i < NDO; ++i) {
         const int e = tid + i * NTG;
-        s.dO[e / VS][e % VS] = bits_to_float(x.rdo[i], p.do_dtype);
+        s.w.dO[e / VS][e % VS] = bits_to_float(x.rdo[i], p.do_dtype);
       }
     }
   };
@@ -1207,14 +1232,20 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     // step's loads, so that waiting for those loads does not wait for them
     if (du_wave) {
       f32x4 a[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-      seg_mfma<1>(a, um0, un0, 1, r, kq,
-                  seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.du[kk][n]; }));
+      if constexpr (F16W)
+        seg_mfma<1>(a, um0, un0, 1, r, kq,
+                    seg<C>([&](int m, int kk) { return s.t[kk][m]; },
+                           [&](int kk, int n) { return (float)s.h.dh[kk][n] + (float)s.h.dl[kk][n]; }));
+      else
+        seg_mfma<1>(a, um0, un0, 1, r, kq,
+                    seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.w.du[kk][n]; }));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = um0[0] + 4 * kq + i;
         const int col = un0[0] + r;
         if (row < nval) stx<TIn>(p.dv, dvb + (int64_t)row * p.sdv[1] + v0 + col, s.bt[row] * a[0][i]);
-        vu_acc[i] = __builtin_fmaf(s.v[row][col], a[0][i], vu_acc[i]);
+        const float vv = F16W ? (float)s.h.v[row][col] : s.w.v[row][col];
+        vu_acc[i] = __builtin_fmaf(vv, a[0][i], vu_acc[i]);
       }
     }
     if (vsi + 2 < nvs) load_step(nxt, vsi + 2);
@@ -1222,31 +1253,59 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     // X[m][v] Y[n][v]: the contraction runs in 16-column groups in which
     // lane (r, kq) covers columns 4 kq .. 4 kq + 3 over four MFMA steps, so
     // each operand is one 16-byte read per four steps.
-#pragma unroll
-    for (int c0 = 0; c0 < VS; c0 += 16) {
-      const int cc = c0 + 4 * kq;
+    if constexpr (F16W) {
+      // lane (r, kq) supplies 8 consecutive columns 8 kq .. of its row; the
+      // accumulators keep the layout of the fp32 products below
+      const int c8 = 8 * kq;
 #pragma unroll
       for (int g = 0; g < NPW; ++g) {
         if (g < ana) {
-          const f32x4 sb = ld4(s.S, an0[g] + r, cc), db = ld4(s.dS, an0[g] + r, cc);
-          const f32x4 xa = ld4(s.du, am0[g] + r, cc), xo = ld4(s.dO, am0[g] + r, cc);
-          const f32x4 xu = ld4(s.u, am0[g] + r, cc);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            accW[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], sb[j], accW[g], 0, 0, 0);
-            accQ[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo[j], sb[j], accQ[g], 0, 0, 0);
-            accK[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xu[j], db[j], accK[g], 0, 0, 0);
-          }
+          const f16x8 sb = tiles16::frag8(&s.h.S[an0[g] + r][c8]), db = tiles16::frag8(&s.h.dS[an0[g] + r][c8]);
+          const f16x8 xo = tiles16::frag8(&s.h.dO[am0[g] + r][c8]);
+          accW[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.dh[am0[g] + r][c8]), sb, accW[g], 0, 0, 0);
+          accW[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.dl[am0[g] + r][c8]), sb, accW[g], 0, 0, 0);
+          accQ[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, sb, accQ[g], 0, 0, 0);
+          accK[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.uh[am0[g] + r][c8]), db, accK[g], 0, 0, 0);
+          accK[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.ul[am0[g] + r][c8]), db, accK[g], 0, 0, 0);
         }
       }
-      // dO u^T (waves 0-3) or du (diag(beta) V)^T (waves 4-7)
-      const f32x4 xc = wave < 4 ? ld4(s.dO, cm0[0] + r, cc) : ld4(s.du, cm0[0] + r, cc);
-      f32x4 yc = wave < 4 ? ld4(s.u, cn0[0] + r, cc) : ld4(s.v, cn0[0] + r, cc);
-      if (wave >= 4) yc *= s.bt[cn0[0] + r];
+      // dO u^T (waves 0-3) or du V^T (waves 4-7; diag(beta) applied when stored)
+      const f16x8 xh = tiles16::frag8(wave < 4 ? &s.h.dO[cm0[0] + r][c8] : &s.h.dh[cm0[0] + r][c8]);
+      const f16x8 xl = tiles16::frag8(&s.h.dl[cm0[0] + r][c8]);
+      const f16x8 yh = tiles16::frag8(wave < 4 ? &s.h.uh[cn0[0] + r][c8] : &s.h.v[cn0[0] + r][c8]);
+      const f16x8 yl = tiles16::frag8(&s.h.ul[cn0[0] + r][c8]);
+      accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, yh, accC[0], 0, 0, 0);
+      accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wave < 4 ? xh : xl, wave < 4 ? yl : yh, accC[0], 0, 0, 0);
+      for (int e = tid; e < K * VS; e += NTG)
+        dgc_acc = __builtin_fmaf((float)s.h.S[e / VS][e % VS], (float)s.h.dS[e / VS][e % VS], dgc_acc);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) accC[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[j], yc[j], accC[0], 0, 0, 0);
+      for (int c0 = 0; c0 < VS; c0 += 16) {
+        const int cc = c0 + 4 * kq;
+#pragma unroll
+        for (int g = 0; g < NPW; ++g) {
+          if (g < ana) {
+            const f32x4 sb = ld4(s.w.S, an0[g] + r, cc), db = ld4(s.w.dS, an0[g] + r, cc);
+            const f32x4 xa = ld4(s.w.du, am0[g] + r, cc), xo = ld4(s.w.dO, am0[g] + r, cc);
+            const f32x4 xu = ld4(s.w.u, am0[g] + r, cc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              accW[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], sb[j], accW[g], 0, 0, 0);
+              accQ[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo[j], sb[j], accQ[g], 0, 0, 0);
+              accK[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(xu[j], db[j], accK[g], 0, 0, 0);
+            }
+          }
+        }
+        // dO u^T (waves 0-3) or du (diag(beta) V)^T (waves 4-7)
+        const f32x4 xc = wave < 4 ? ld4(s.w.dO, cm0[0] + r, cc) : ld4(s.w.du, cm0[0] + r, cc);
+        f32x4 yc = wave < 4 ? ld4(s.w.u, cn0[0] + r, cc) : ld4(s.w.v, cn0[0] + r, cc);
+        if (wave >= 4) yc *= s.bt[cn0[0] + r];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) accC[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[j], yc[j], accC[0], 0, 0, 0);
+      }
+      for (int e = tid; e < K * VS; e += NTG)
+        dgc_acc = __builtin_fmaf(s.w.S[e / VS][e % VS], s.w.dS[e / VS][e % VS], dgc_acc);
     }
-    for (int e = tid; e < K * VS; e += NTG) dgc_acc = __builtin_fmaf(s.S[e / VS][e % VS], s.dS[e / VS][e % VS], dgc_acc);
     __syncthreads();
     if (vsi + 1 < nvs) {
       store_step(cur);
@@ -1294,7 +1353,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       s.y[row][col] = scale * s.m[row][col] * accC[0][e];
       s.yp[row][col] = scale * accC[0][e] * s.pm[row][col];
     } else {
-      s.dt[row][col] = accC[0][e];
+      s.dt[row][col] = F16W ? s.bt[col] * accC[0][e] : accC[0][e];
     }
   }
   if (du_wave) {

@@ -122,6 +122,41 @@ struct RowLoad {
       }
     }
   }
+  // 16-bit rows kept 16-bit: the raw 16-byte pieces (rows >= nvalid zeroed)
+  template <typename TD, int LD>
+  __device__ __forceinline__ void store_raw(int tid, TD (*dst)[LD], int nvalid = ROWS) const {
+    static_assert(sizeof(TD) == sizeof(TIn) && LD * sizeof(TD) % 16 == 0, "16-byte rows of the same width");
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (ROWS * RV % NT == 0 || e < ROWS * RV) {
+        const bool ok = t < nvalid;
+        *reinterpret_cast<u32x4*>(&dst[t][col]) =
+            u32x4{ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
+      }
+    }
+  }
+  // fp32 rows as fp16 pairs hi + lo (x - hi rounded), two 8-byte stores
+  template <int LD>
+  __device__ __forceinline__ void store_pairs(int tid, _Float16 (*hi)[LD], _Float16 (*lo)[LD]) const {
+    static_assert(std::is_same<TIn, float>::value && LD % 4 == 0, "fp32 rows, 8-byte pieces");
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int e = tid + i * NT, t = e / RV, col = (e % RV) * VEC;
+      if (ROWS * RV % NT == 0 || e < ROWS * RV) {
+        h4 h, l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = pin(__uint_as_float(r[i][j]));
+          h[j] = (_Float16)x;
+          l[j] = (_Float16)(x - (float)h[j]);
+        }
+        *reinterpret_cast<h4*>(&hi[t][col]) = h;
+        *reinterpret_cast<h4*>(&lo[t][col]) = l;
+      }
+    }
+  }
   // 16-bit rows as floats, columns [0, 16) times sc0 and [16, 32) times sc1
   // (powers of two: exact)
   template <int LD>
