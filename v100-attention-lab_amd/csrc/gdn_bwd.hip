@@ -1027,6 +1027,13 @@ struct alignas(16) GSmem {
       f16 v[C][HD], dO[C][HD], uh[C][HD], ul[C][HD], dh[C][HD], dl[C][HD];
       f16 S[K][HD], dS[K][HD];
     } h;
+    // after the walk (fp16 inputs): operands of the dq / dk products, q and
+    // k exact in fp16, dQK and dKK + dKK^T as hi + lo pairs, all row-major
+    // (transposed operands are read with ds_read_b64_tr_b16)
+    struct {
+      f16 q[C][K + 8], k[C][K + 8];
+      f16 yh[C][C + 8], yl[C][C + 8], zh[C][C + 8], zl[C][C + 8];
+    } x;
   };
   float b[C], gam[C], D[C], bt[C];
   float rq[K / 16][C], rk[K / 16][C];  // row partials, one row per 16-column tile
@@ -1346,12 +1353,35 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       }
     }
   }
+  if constexpr (F16W) {
+    // q and k rows in fp16 (exact: fp16 inputs), 8 per thread
+    static_assert(C * K / 8 <= 2 * NTG, "two 8-element pieces per thread at most");
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * NTG, row = e / (K / 8), c8 = 8 * (e % (K / 8));
+      if (e < C * K / 8) {
+        f16x8 hq, hk;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          hq[j] = (f16)s.q[row][c8 + j];
+          hk[j] = (f16)s.k[row][c8 + j];
+        }
+        *reinterpret_cast<f16x8*>(&s.x.q[row][c8]) = hq;
+        *reinterpret_cast<f16x8*>(&s.x.k[row][c8]) = hk;
+      }
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int row = cm0[0] + 4 * kq + e, col = cn0[0] + r;
     if (wave < 4) {
-      s.y[row][col] = scale * s.m[row][col] * accC[0][e];
+      const float y = pin(scale * s.m[row][col] * accC[0][e]);
+      s.y[row][col] = y;
       s.yp[row][col] = scale * accC[0][e] * s.pm[row][col];
+      if constexpr (F16W) {
+        s.x.yh[row][col] = (f16)y;
+        s.x.yl[row][col] = (f16)(y - (float)(f16)y);
+      }
     } else {
       s.dt[row][col] = F16W ? s.bt[col] * accC[0][e] : accC[0][e];
     }
@@ -1430,6 +1460,16 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     }
   }
   __syncthreads();
+  if constexpr (F16W) {
+    // dKK + dKK^T as fp16 pairs for the dk product (published by the
+    // barrier below)
+    for (int e = tid; e < C * C; e += NTG) {
+      const int t = e / C, j = e % C;
+      const float zz = pin(s.z[t][j] + s.z[j][t]);
+      s.x.zh[t][j] = (f16)zz;
+      s.x.zl[t][j] = (f16)(zz - (float)(f16)zz);
+    }
+  }
   if (wave == 0) {
     // dg_t = sum_{j >= t} db_j: lane l scans db[C - 1 - l]
     const float x = scan32(lane < C ? s.db[C - 1 - lane] : 0.f);
@@ -1447,13 +1487,35 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       aq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       ak[i] = aq[i];
     }
-    seg_mfma<NPW>(aq, am0, an0, ana, r, kq,
-                  seg<C>([&](int m, int kk) { return s.y[m][kk]; }, [&](int kk, int n) { return s.k[kk][n]; }));
-    seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
-                  seg<C>([&](int m, int kk) { return s.y[kk][m]; }, [&](int kk, int n) { return s.q[kk][n]; }));
-    seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
-                  seg<C>([&](int m, int kk) { return s.z[m][kk] + s.z[kk][m]; },
-                         [&](int kk, int n) { return s.k[kk][n]; }));
+    if constexpr (F16W) {
+      __syncthreads();  // the dKK + dKK^T pairs
+      // lane (r, kq): rows of dQK / dQK^T / dKK + dKK^T (A) and columns of
+      // K / Q (B), contraction indices 8 kq .. 8 kq + 7 of the C = 32
+#pragma unroll
+      for (int g = 0; g < NPW; ++g) {
+        if (g < ana) {
+          const f16x8 kt = tiles16::frag8_t(s.x.k, 0, an0[g], r, kq);
+          const f16x8 qt = tiles16::frag8_t(s.x.q, 0, an0[g], r, kq);
+          const int m = am0[g] + r;
+          aq[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.yh[m][8 * kq]), kt, aq[g], 0, 0, 0);
+          aq[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.yl[m][8 * kq]), kt, aq[g], 0, 0, 0);
+          ak[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8_t(s.x.yh, 0, am0[g], r, kq), qt, ak[g], 0,
+                                                         0, 0);
+          ak[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8_t(s.x.yl, 0, am0[g], r, kq), qt, ak[g], 0,
+                                                         0, 0);
+          ak[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.zh[m][8 * kq]), kt, ak[g], 0, 0, 0);
+          ak[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.zl[m][8 * kq]), kt, ak[g], 0, 0, 0);
+        }
+      }
+    } else {
+      seg_mfma<NPW>(aq, am0, an0, ana, r, kq,
+                    seg<C>([&](int m, int kk) { return s.y[m][kk]; }, [&](int kk, int n) { return s.k[kk][n]; }));
+      seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
+                    seg<C>([&](int m, int kk) { return s.y[kk][m]; }, [&](int kk, int n) { return s.q[kk][n]; }));
+      seg_mfma<NPW>(ak, am0, an0, ana, r, kq,
+                    seg<C>([&](int m, int kk) { return s.z[m][kk] + s.z[kk][m]; },
+                           [&](int kk, int n) { return s.k[kk][n]; }));
+    }
 #pragma unroll
     for (int i = 0; i < NPW; ++i) {
       if (i < ana) {
