@@ -1032,11 +1032,15 @@ struct alignas(16) GSmem {
     // (transposed operands are read with ds_read_b64_tr_b16)
     struct {
       f16 q[C][K + 8], k[C][K + 8];
-      f16 yh[C][C + 8], yl[C][C + 8], zh[C][C + 8], zl[C][C + 8];
+      f16 dwh[C][K + 8], dwl[C][K + 8];  // dW
+      f16 yh[C][C + 8], yl[C][C + 8];    // dQK
+      f16 zh[C][C + 8], zl[C][C + 8];    // Z = T^T dT, later dKK + dKK^T
+      f16 th[C][C + 8], tl[C][C + 8];    // T
+      f16 dth[C][C + 8], dtl[C][C + 8];  // dT
     } x;
   };
   float b[C], gam[C], D[C], bt[C];
-  float rq[K / 16][C], rk[K / 16][C];  // row partials, one row per 16-column tile
+  float rq[K / 16][C], rk[K / 16][C], rw[K / 16][C];  // row partials, one row per 16-column tile
   float vu[VS / 16][C];  // v.dU~ row partials, one row per 16-column tile
   float kw[C], dgam[C], dD[C], db[C], dbt[C];
   float red[NTG / 64];
@@ -1341,6 +1345,11 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       for (int e = 0; e < 4; ++e) {
         const int row = am0[i] + 4 * kq + e, col = an0[i] + r;
         s.dw[row][col] = -accW[i][e];
+        if constexpr (F16W) {
+          const float w = pin(-accW[i][e]);
+          s.x.dwh[row][col] = (f16)w;
+          s.x.dwl[row][col] = (f16)(w - (float)(f16)w);
+        }
         pq[e] = sum16(s.q[row][col] * accQ[i][e]);
         pk[e] = sum16(s.k[row][col] * accK[i][e]);
       }
@@ -1354,6 +1363,11 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     }
   }
   if constexpr (F16W) {
+    for (int e = tid; e < C * C; e += NTG) {
+      const float x = pin(s.t[e / C][e % C]);
+      s.x.th[e / C][e % C] = (f16)x;
+      s.x.tl[e / C][e % C] = (f16)(x - (float)(f16)x);
+    }
     // q and k rows in fp16 (exact: fp16 inputs), 8 per thread
     static_assert(C * K / 8 <= 2 * NTG, "two 8-element pieces per thread at most");
 #pragma unroll
@@ -1401,11 +1415,54 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   }
   __syncthreads();
   // dT = du (beta V)^T + dW (beta gam K)^T;  dW~ = T^T dW
-  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] += x; },
-                 seg<K>([&](int m, int kk) { return s.dw[m][kk]; },
-                        [&](int kk, int n) { return s.bt[n] * s.gam[n] * s.k[n][kk]; }));
-  mmx<NTG, C, K>(tid, [&](int m, int n, float x) { s.dwt[m][n] = x; },
-                 seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dw[kk][n]; }));
+  f32x4 aw[NPW];  // fp16 inputs: dW~ in the tiles of accW
+  if constexpr (F16W) {
+    // fp16 MFMA on hi + lo pairs; transposed operands (T^T, dW columns) by
+    // ds_read_b64_tr_b16.  dT: waves 0-3, one 16 x 16 tile each.
+    if (wave < 4) {
+      const int dm = (wave >> 1) * 16, dn = (wave & 1) * 16;
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 kf = tiles16::frag8(&s.x.k[dn + r][kb + 8 * kq]);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.dwh[dm + r][kb + 8 * kq]), kf, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.dwl[dm + r][kb + 8 * kq]), kf, a, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = dm + 4 * kq + e, col = dn + r;
+        const float x = pin(s.dt[row][col] + s.bt[col] * s.gam[col] * a[e]);
+        s.dt[row][col] = x;
+        s.x.dth[row][col] = (f16)x;
+        s.x.dtl[row][col] = (f16)(x - (float)(f16)x);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NPW; ++g) {
+      aw[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (g < ana) {
+        const f16x8 th = tiles16::frag8_t(s.x.th, 0, am0[g], r, kq), tl = tiles16::frag8_t(s.x.tl, 0, am0[g], r, kq);
+        const f16x8 wh = tiles16::frag8_t(s.x.dwh, 0, an0[g], r, kq);
+        aw[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, wh, aw[g], 0, 0, 0);
+        aw[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, tiles16::frag8_t(s.x.dwl, 0, an0[g], r, kq), aw[g], 0,
+                                                       0, 0);
+        aw[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tl, wh, aw[g], 0, 0, 0);
+        float pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pw[e] = sum16(s.k[am0[g] + 4 * kq + e][an0[g] + r] * aw[g][e]);
+        if (r == 0) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s.rw[an0[g] / 16][am0[g] + 4 * kq + e] = pw[e];
+        }
+      }
+    }
+  } else {
+    mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] += x; },
+                   seg<K>([&](int m, int kk) { return s.dw[m][kk]; },
+                          [&](int kk, int n) { return s.bt[n] * s.gam[n] * s.k[n][kk]; }));
+    mmx<NTG, C, K>(tid, [&](int m, int n, float x) { s.dwt[m][n] = x; },
+                   seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dw[kk][n]; }));
+  }
   if (tid < C) {
     float a = 0.f, b = 0.f;
     for (int j = 0; j < NCT; ++j) {
@@ -1422,16 +1479,53 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   }
   __syncthreads();
   // Z = T^T dT;  k_t.dW~_t
-  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.z[m][n] = x; },
-                 seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dt[kk][n]; }));
-  {
+  if constexpr (F16W) {
+    if (wave < 4) {
+      const int zm = (wave >> 1) * 16, zn = (wave & 1) * 16;
+      const f16x8 th = tiles16::frag8_t(s.x.th, 0, zm, r, kq), dh = tiles16::frag8_t(s.x.dth, 0, zn, r, kq);
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, dh, a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, tiles16::frag8_t(s.x.dtl, 0, zn, r, kq), a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8_t(s.x.tl, 0, zm, r, kq), dh, a, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = zm + 4 * kq + e, col = zn + r;
+        const float z = pin(a[e]);
+        s.x.zh[row][col] = (f16)z;
+        s.x.zl[row][col] = (f16)(z - (float)(f16)z);
+      }
+    }
+    if (tid < C) {
+      float x = 0.f;
+      for (int j = 0; j < NCT; ++j) x += s.rw[j][tid];
+      s.kw[tid] = x;
+    }
+  } else {
+    mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.z[m][n] = x; },
+                   seg<C>([&](int m, int kk) { return s.t[kk][m]; }, [&](int kk, int n) { return s.dt[kk][n]; }));
     const float kw = row_sum<NTG, C, K>(tid, [&](int rr, int i) { return s.k[rr][i] * s.dwt[rr][i]; });
     if (tid % RL == 0) s.kw[tid / RL] = kw;
   }
   __syncthreads();
   // dA = -tril_-1(Z T^T) -> dt
-  mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
-                 seg<C>([&](int m, int kk) { return s.z[m][kk]; }, [&](int kk, int n) { return s.t[n][kk]; }));
+  if constexpr (F16W) {
+    if (wave < 4) {
+      const int am = (wave >> 1) * 16, an = (wave & 1) * 16;
+      const f16x8 zh = tiles16::frag8(&s.x.zh[am + r][8 * kq]), th = tiles16::frag8(&s.x.th[an + r][8 * kq]);
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(zh, th, a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(zh, tiles16::frag8(&s.x.tl[an + r][8 * kq]), a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.zl[am + r][8 * kq]), th, a, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = am + 4 * kq + e, col = an + r;
+        s.dt[row][col] = col < row ? -a[e] : 0.f;
+      }
+    }
+  } else {
+    mmx<NTG, C, C>(tid, [&](int m, int n, float x) { s.dt[m][n] = n < m ? -x : 0.f; },
+                   seg<C>([&](int m, int kk) { return s.z[m][kk]; }, [&](int kk, int n) { return s.t[n][kk]; }));
+  }
   __syncthreads();
   // dKK = dA o beta_t M -> z;  dbeta and db
   for (int e = tid; e < C * C; e += NTG) {
@@ -1524,7 +1618,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
           const int row = am0[i] + 4 * kq + e, col = an0[i] + r;
           if (row < nval) {
             const float dq = aq[i][e] + scale * s.gam[row] * accQ[i][e];
-            const float dk = ak[i][e] + s.D[row] * accK[i][e] + s.bt[row] * s.gam[row] * s.dwt[row][col];
+            const float dwt = F16W ? aw[i][e] : s.dwt[row][col];
+            const float dk = ak[i][e] + s.D[row] * accK[i][e] + s.bt[row] * s.gam[row] * dwt;
             stx<TIn>(p.dq, dqb + (int64_t)row * p.sdq[1] + col, dq);
             stx<TIn>(p.dk, dkb + (int64_t)row * p.sdk[1] + col, dk);
           }
