@@ -78,8 +78,9 @@ struct BArgs {
   float* dh0;
   float* rec;  // per (slot, head): the prep kernel's record
   // per (slot, head): S at the chunk start and dS', the gradient of the
-  // state after the chunk, [K][V]; fp32, or fp16 from the 16-bit walks (in
-  // each walk's range-shifted units: scl below scales them back)
+  // state after the chunk: fp32 [K][V], or from the 16-bit walks fp16 [V][K]
+  // (rows = state columns, in each walk's range-shifted units: scl below
+  // scales them back)
   float* ckS;
   float* ckD;
   float* uu;   // per (slot, head): u, [C][V]
@@ -595,7 +596,6 @@ struct alignas(16) FMem {
   // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
   float gv[NTP / C][C];
-  float s32[K][BV + 4];  // S in fp32, for 16-byte stores of its rows
 };
 
 template <int K>
@@ -609,7 +609,6 @@ struct alignas(16) RMem {
   f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
   f16 zh[BV][C + HP], zl[BV][C + HP];  // (diag(gam) (T diag(beta))^T du)^T
   float gv[NTP / C][C];
-  float s32[K][BV + 4];  // dS' in fp32, for 16-byte stores of its rows
 };
 
 template <int K>
@@ -636,18 +635,6 @@ struct State {
                                    : 0.f;
     }
   }
-  // into the fp32 LDS copy (read back by copy_rows after a barrier)
-  template <int LD>
-  __device__ __forceinline__ void put32(float (*s32)[LD], int wave, int r, int kq) const {
-#pragma unroll
-    for (int j = 0; j < NST; ++j) {
-      const int m0 = 16 * (wave + 4 * j);
-      if (m0 < K) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s32[m0 + 4 * kq + i][r] = st[j][i];
-      }
-    }
-  }
   template <int LD>
   __device__ __forceinline__ void put(f16 (*sh)[LD], f16 (*sl)[LD], int wave, int r, int kq) const {
 #pragma unroll
@@ -661,34 +648,18 @@ struct State {
   }
 };
 
-// The K x BV fp32 state copy, times sc (a power of two), -> rows of a
-// [K][V] array, 16 bytes per lane.
+// The state's fp16 values -> rows of the [V][K] chunk-state array (row =
+// state column), 16 bytes per lane.  They are the hi parts of the walk's
+// S^T pair copy (x rounded to nearest), copied as they are.
 template <int K, int LD>
-__device__ __forceinline__ void copy_rows(const float (*s32)[LD], float* dst, int64_t ld, int tid, float sc) {
-  constexpr int NV = K * BV / 4;
+__device__ __forceinline__ void copy_state_rows(const f16 (*sh)[LD], f16* dst, int tid) {
+  constexpr int NV = BV * K / 8;
 #pragma unroll
   for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
     const int e = tid + i * NTP;
     if (NV % NTP == 0 || e < NV)
-      *reinterpret_cast<f32x4*>(dst + (int64_t)(e / 4) * ld + 4 * (e % 4)) =
-          *reinterpret_cast<const f32x4*>(&s32[e / 4][4 * (e % 4)]) * sc;
-  }
-}
-
-// The K x BV fp32 state copy -> fp16 rows of a [K][V] array, 16 bytes per
-// lane (rounded to nearest: the same value as the walk's hi part).
-template <int K, int LD>
-__device__ __forceinline__ void copy_rows16(const float (*s32)[LD], f16* dst, int64_t ld, int tid) {
-  constexpr int NV = K * BV / 8;
-#pragma unroll
-  for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
-    const int e = tid + i * NTP;
-    if (NV % NTP == 0 || e < NV) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(&s32[e / 2][8 * (e % 2)]);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(&s32[e / 2][8 * (e % 2) + 4]);
-      *reinterpret_cast<f16x8*>(dst + (int64_t)(e / 2) * ld + 8 * (e % 2)) =
-          f16x8{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3], (f16)b[0], (f16)b[1], (f16)b[2], (f16)b[3]};
-    }
+      *reinterpret_cast<f16x8*>(dst + (int64_t)(e / (K / 8)) * K + 8 * (e % (K / 8))) =
+          *reinterpret_cast<const f16x8*>(&sh[e / (K / 8)][8 * (e % (K / 8))]);
   }
 }
 
@@ -739,7 +710,6 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
   State<K> S;
   S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq, rsc.v);
   S.put(s.sh, s.sl, wave, r, kq);
-  S.put32(s.s32, wave, r, kq);
   FNext16<TIn, K> nx;
   if (nch > 0) {
     nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
@@ -752,7 +722,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     // is then consumed by the staging below, on every path)
     const int cn = min(c + 1, nch - 1);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
-    copy_rows16<K>(s.s32, reinterpret_cast<f16*>(p.ckS) + ri * (int64_t)K * p.V + v0, p.V, tid);
+    copy_state_rows<K>(s.sh, reinterpret_cast<f16*>(p.ckS) + (ri * p.V + v0) * (int64_t)K, tid);
     if (wave < 2) {
       // Y = V - diag(gam) K S for rows 16 w .. (k exact in fp16), as Y^T pairs
       const int um0 = 16 * wave;
@@ -803,8 +773,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-    S.put32(s.s32, wave, r, kq);
-    __syncthreads();
+      __syncthreads();
     nx.store(s, tid, rsc.v);
     __syncthreads();
   }
@@ -865,7 +834,6 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
   State<K> S;
   S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq, rsd.v);
   S.put(s.sh, s.sl, wave, r, kq);
-  S.put32(s.s32, wave, r, kq);
   RNext16<TIn, K> nx;
   if (nch > 0) {
     const int t0 = (nch - 1) * C;
@@ -878,7 +846,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     // the previous chunk's inputs (chunk 0's again at the end)
     const int cn = max(c - 1, 0);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
-    copy_rows16<K>(s.s32, reinterpret_cast<f16*>(p.ckD) + ri * (int64_t)K * p.V + v0, p.V, tid);
+    copy_state_rows<K>(s.sh, reinterpret_cast<f16*>(p.ckD) + (ri * p.V + v0) * (int64_t)K, tid);
     if (wave < 2) {
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
@@ -957,8 +925,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-    S.put32(s.s32, wave, r, kq);
-    __syncthreads();
+      __syncthreads();
     nx.store(s, tid, rsd.v);
     __syncthreads();
   }
@@ -1025,7 +992,7 @@ struct alignas(16) GSmem {
     } w;
     struct {
       f16 v[C][HD], dO[C][HD], uh[C][HD], ul[C][HD], dh[C][HD], dl[C][HD];
-      f16 S[K][HD], dS[K][HD];
+      f16 ST[VS][K + 8], dST[VS][K + 8];  // S^T, dS'^T rows (as stored)
     } h;
     // after the walk (fp16 inputs): operands of the dq / dk products, q and
     // k exact in fp16, dQK and dKK + dKK^T as hi + lo pairs, all row-major
@@ -1143,10 +1110,12 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   // q's dtype and 4-byte aligned rows: one element pair per thread.
   constexpr int NDP = C * VS / 2;  // dO element pairs of a step (VS = 16: waves 0-3 only)
   static_assert(!ST16 || NDP == NTG || NDP == NTG / 2, "at most one dO pair per thread");
+  // states: fp32 [K][V] rows, or fp16 [V][K] rows from the 16-bit walks
+  using SLoad = typename std::conditional<ST16, RowLoad<f16, VS, K, NTG>, RowLoad<float, K, VS, NTG>>::type;
   struct StepRows {
     RowLoad<TIn, C, VS, NTG> lv;
     RowLoad<float, C, VS, NTG> lu, ldu;
-    RowLoad<TS, K, VS, NTG> lS, ldS;
+    SLoad lS, ldS;
     float scS[2], scD[2];
     uint32_t rdo[NDO];
   };
@@ -1155,8 +1124,13 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     x.lv.load_clamped(tid, static_cast<const TIn*>(p.v) + vb + v0, p.sv[1], nval);
     x.lu.load_clamped(tid, uu + v0, p.V, C);
     x.ldu.load_clamped(tid, dug + v0, p.V, C);
-    x.lS.load_clamped(tid, cks + v0, p.V, K);
-    x.ldS.load_clamped(tid, ckd + v0, p.V, K);
+    if constexpr (ST16) {
+      x.lS.load_clamped(tid, cks + (int64_t)v0 * K, K, VS);
+      x.ldS.load_clamped(tid, ckd + (int64_t)v0 * K, K, VS);
+    } else {
+      x.lS.load_clamped(tid, cks + v0, p.V, K);
+      x.ldS.load_clamped(tid, ckd + v0, p.V, K);
+    }
     x.scS[0] = x.scS[1] = x.scD[0] = x.scD[1] = 1.f;
     if constexpr (ST16) {
 #pragma unroll
@@ -1181,8 +1155,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       x.lv.store_raw(tid, s.h.v, nval);
       x.lu.store_pairs(tid, s.h.uh, s.h.ul);
       x.ldu.store_pairs(tid, s.h.dh, s.h.dl);
-      x.lS.store_raw(tid, s.h.S);
-      x.ldS.store_raw(tid, s.h.dS);
+      x.lS.store_raw(tid, s.h.ST);
+      x.ldS.store_raw(tid, s.h.dST);
       const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
       if (NDP == NTG || tid < NDP) *reinterpret_cast<uint32_t*>(&s.h.dO[t][c2]) = t < nval ? x.rdo[0] : 0u;
       return;
@@ -1191,8 +1165,23 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     x.lu.store(tid, s.w.u);
     x.ldu.store(tid, s.w.du);
     if constexpr (ST16) {
-      x.lS.store_scaled(tid, s.w.S, x.scS[0], x.scS[1]);
-      x.ldS.store_scaled(tid, s.w.dS, x.scD[0], x.scD[1]);
+      // [V][K] fp16 rows -> the fp32 [K][V] tiles, scaled back per 16-column
+      // slice (a power of two: exact)
+      auto scatter = [&](const SLoad& L, float (*dst)[GSmem<K, VS>::SD], const float (&sc)[2]) {
+#pragma unroll
+        for (int i = 0; i < SLoad::N; ++i) {
+          const int e = tid + i * NTG, v = e / (K / 8), k0 = 8 * (e % (K / 8));
+          if (VS * K / 8 % NTG == 0 || e < VS * K / 8) {
+            float xv[8];
+            unpack16<f16>(L.r[i], xv);
+            const float f = sc[v / 16];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[k0 + j][v] = xv[j] * f;
+          }
+        }
+      };
+      scatter(x.lS, s.w.S, x.scS);
+      scatter(x.ldS, s.w.dS, x.scD);
       const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
       if (NDP == NTG || tid < NDP) {
         // dO has q's dtype here: a compile-time conversion
@@ -1271,7 +1260,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 #pragma unroll
       for (int g = 0; g < NPW; ++g) {
         if (g < ana) {
-          const f16x8 sb = tiles16::frag8(&s.h.S[an0[g] + r][c8]), db = tiles16::frag8(&s.h.dS[an0[g] + r][c8]);
+          // S[an0 + r][8 kq + j] = S^T[8 kq + j][an0 + r]: transposed reads
+          const f16x8 sb = tiles16::frag8_t(s.h.ST, 0, an0[g], r, kq), db = tiles16::frag8_t(s.h.dST, 0, an0[g], r, kq);
           const f16x8 xo = tiles16::frag8(&s.h.dO[am0[g] + r][c8]);
           accW[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.dh[am0[g] + r][c8]), sb, accW[g], 0, 0, 0);
           accW[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.h.dl[am0[g] + r][c8]), sb, accW[g], 0, 0, 0);
@@ -1288,7 +1278,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, yh, accC[0], 0, 0, 0);
       accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wave < 4 ? xh : xl, wave < 4 ? yl : yh, accC[0], 0, 0, 0);
       for (int e = tid; e < K * VS; e += NTG)
-        dgc_acc = __builtin_fmaf((float)s.h.S[e / VS][e % VS], (float)s.h.dS[e / VS][e % VS], dgc_acc);
+        dgc_acc = __builtin_fmaf((float)s.h.ST[e / K][e % K], (float)s.h.dST[e / K][e % K], dgc_acc);
     } else {
 #pragma unroll
       for (int c0 = 0; c0 < VS; c0 += 16) {
