@@ -1358,22 +1358,10 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       s.x.th[e / C][e % C] = (f16)x;
       s.x.tl[e / C][e % C] = (f16)(x - (float)(f16)x);
     }
-    // q and k rows in fp16 (exact: fp16 inputs), 8 per thread
-    static_assert(C * K / 8 <= 2 * NTG, "two 8-element pieces per thread at most");
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + i * NTG, row = e / (K / 8), c8 = 8 * (e % (K / 8));
-      if (e < C * K / 8) {
-        f16x8 hq, hk;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          hq[j] = (f16)s.q[row][c8 + j];
-          hk[j] = (f16)s.k[row][c8 + j];
-        }
-        *reinterpret_cast<f16x8*>(&s.x.q[row][c8]) = hq;
-        *reinterpret_cast<f16x8*>(&s.x.k[row][c8]) = hk;
-      }
-    }
+    // q and k rows in fp16: the raw rows loaded at the start (kept in
+    // registers through the walk; rows past the chunk end are zero)
+    lq.store_raw(tid, s.x.q);
+    lk.store_raw(tid, s.x.k);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
