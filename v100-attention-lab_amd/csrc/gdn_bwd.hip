@@ -49,6 +49,7 @@
 // i onwards, one per chunk; the ranges are disjoint, so every launch handles
 // packed sequences like a batch.
 
+#include "gdn_fwd_pipe.h"
 #include "gdn_tiles_f16.h"
 
 namespace gdn {
@@ -248,6 +249,222 @@ __global__ __launch_bounds__(NTP) void prep_kernel(const BArgs p) {
     mmx<NTP, C, K>(tid, [&](int m, int n, float x) { rec[R::W + m * K + n] = x; },
                    seg<C>([&](int m, int kk) { return s.t[m][kk]; },
                           [&](int kk, int n) { return s.bt[kk] * s.gam[kk] * s.k[kk][n]; }));
+}
+
+// 16-bit q or k rows as MFMA operands: 8 elements (16 bytes) per lane, in
+// their own type (exact), on v_mfma_f32_16x16x32_f16 or _bf16.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+template <typename TIn>
+__device__ __forceinline__ f32x4 mma16(const u32x4& a, const u32x4& b, const f32x4& acc) {
+  if constexpr (std::is_same<TIn, f16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                   0, 0, 0);
+}
+// 8 consecutive fp32 values that hold 16-bit inputs, back in their own type
+// (exact).
+template <typename TIn>
+__device__ __forceinline__ u32x4 pack16(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (std::is_same<TIn, f16>::value) {
+      const f16 lo = (f16)x[2 * e], hi = (f16)x[2 * e + 1];
+      r[e] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    } else {
+      r[e] = (__float_as_uint(x[2 * e]) >> 16) | (__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
+    }
+  }
+  return r;
+}
+
+// The prep of the 16-bit recurrences: one wave per two (chunk, head)
+// records, with no workgroup barrier.  Per record: the gates (a prefix sum
+// across lanes), K K^T and Q K^T on the 16-bit matrix cores (exact
+// products, fp32 sums), A = beta_t e^{b_t - b_j} K K^T (t > j) staged as
+// A^T in the wave's LDS, then T = (I + A)^-1 by substitution with one lane
+// per row of T (lanes 0-31: record 0, lanes 32-63: record 1).  It writes T
+// and the gates to the fp32 record, and T diag(beta) and P = M o Q K^T as
+// fp16 pairs; the gradient kernel forms P and K K^T in fp32 itself (from
+// the q and k rows it loads anyway), so they are not written here.  Rows
+// past a chunk's end read the last row again: their beta and gate are
+// zero, which zeroes their rows of A and T (and their rows of P are
+// zeroed), so the record equals that of zero rows.
+constexpr int NRW = 2;  // records per wave
+
+template <typename TIn, int K>
+__global__ __launch_bounds__(256) void prep16_kernel(const BArgs p, int64_t nrec) {
+  using R = Rec<K>;
+  constexpr int KB = K / 32;
+  __shared__ __attribute__((aligned(16))) float s_at[4][NRW][C * C];  // A^T row-major
+  __shared__ __attribute__((aligned(16))) float s_beta[4][NRW][C];
+  __shared__ __attribute__((aligned(16))) float s_b[4][NRW][C];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, gq = lane >> 4;
+  const int half = lane >> 5, c = lane & 31;
+
+  // the records of this wave (wave-uniform)
+  int nval[NRW];
+  const TIn* qh[NRW];
+  const TIn* kh[NRW];
+  int64_t gb[NRW], bb[NRW], ri[NRW];
+#pragma unroll
+  for (int e = 0; e < NRW; ++e) {
+    const int64_t rid = ((int64_t)blockIdx.x * 4 + wave) * NRW + e;
+    nval[e] = 0;
+    qh[e] = kh[e] = nullptr;
+    gb[e] = bb[e] = ri[e] = 0;
+    RowSpan rs;
+    int cc;
+    if (rid < nrec && slot_chunk<C>(p, rid / p.H, rs, cc)) {
+      const int hi = (int)(rid % p.H), t0 = cc * C;
+      nval[e] = min(C, rs.T - t0);
+      qh[e] = static_cast<const TIn*>(p.q) + head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1];
+      kh[e] = static_cast<const TIn*>(p.k) + head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1];
+      gb[e] = head_base(rs, hi, p.sg) + (int64_t)t0 * p.sg[1];
+      bb[e] = head_base(rs, hi, p.sb) + (int64_t)t0 * p.sb[1];
+      ri[e] = rid;
+    }
+  }
+  // q and k rows as operand fragments: lane (n, gq) holds row 16 mt + n,
+  // columns 32 kb + 8 gq .. + 7
+  u32x4 qr[NRW][2][KB], kr[NRW][2][KB];
+#pragma unroll
+  for (int e = 0; e < NRW; ++e) {
+    if (nval[e] > 0) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int64_t row = min(16 * mt + n, nval[e] - 1);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          kr[e][mt][kb] = *reinterpret_cast<const u32x4*>(kh[e] + row * p.sk[1] + 32 * kb + 8 * gq);
+          qr[e][mt][kb] = *reinterpret_cast<const u32x4*>(qh[e] + row * p.sq[1] + 32 * kb + 8 * gq);
+        }
+      }
+    }
+  }
+  // gates of row c of record `half`
+  float gv = 0.f, bv = 0.f;
+  {
+    const int nv = half ? nval[1] : nval[0];
+    if (c < nv) {
+      gv = load_scalar(p.g, (half ? gb[1] : gb[0]) + (int64_t)c * p.sg[1], p.g_dtype);
+      bv = load_scalar(p.beta, (half ? bb[1] : bb[0]) + (int64_t)c * p.sb[1], p.beta_dtype);
+    }
+  }
+  const float b = pipe::scan32(gv);
+  const float bC0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), 31));
+  const float bC1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), 63));
+  const float bC = half ? bC1 : bC0;
+  s_beta[wave][half][c] = bv;
+  s_b[wave][half][c] = b;
+  float* const rec_h = p.rec + (half ? ri[1] : ri[0]) * (int64_t)R::SIZE;
+  if ((half ? nval[1] : nval[0]) > 0) {
+    rec_h[R::G + c] = b;
+    rec_h[R::G + C + c] = expf(b);
+    rec_h[R::G + 2 * C + c] = expf(bC - b);
+    rec_h[R::G + 3 * C + c] = c == 0 ? expf(bC) : 0.f;
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+#pragma unroll
+  for (int e = 0; e < NRW; ++e) {
+    if (nval[e] > 0) {
+      const float* const sb = s_b[wave][e];
+      // A^T from the lower tiles of K K^T (the upper one is never read)
+      float* const sa = s_at[wave][e];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt <= mt; ++nt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) acc = mma16<TIn>(kr[e][mt][kb], kr[e][nt][kb], acc);
+          // acc[i] = (K K^T)[t = 16 mt + 4 gq + i][j = 16 nt + n]
+          const int jj = 16 * nt + n;
+          const float bj = sb[jj];
+          const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&sb[16 * mt + 4 * gq]);
+          const f32x4 be4 = *reinterpret_cast<const f32x4*>(&s_beta[wave][e][16 * mt + 4 * gq]);
+          f32x4 av;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 16 * mt + 4 * gq + i;
+            av[i] = t > jj ? be4[i] * expf(bt4[i] - bj) * acc[i] : 0.f;
+          }
+          *reinterpret_cast<f32x4*>(sa + jj * C + 16 * mt + 4 * gq) = av;
+        }
+      // P = M o Q K^T as fp16 pairs, row-major: the product K Q^T puts 4
+      // consecutive columns of one row of P in each lane
+      f16* const rh = p.r16 + ri[e] * (int64_t)Rec16::SIZE;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int t = 16 * mt + n;
+        const float btv = sb[t];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          f16 h[4] = {(f16)0.f, (f16)0.f, (f16)0.f, (f16)0.f}, l[4] = {h[0], h[1], h[2], h[3]};
+          if (nt <= mt) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc = mma16<TIn>(kr[e][nt][kb], qr[e][mt][kb], acc);
+            const f32x4 bj4 = *reinterpret_cast<const f32x4*>(&sb[16 * nt + 4 * gq]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = 16 * nt + 4 * gq + i;
+              const float x = (j <= t && t < nval[e]) ? expf(btv - bj4[i]) * acc[i] : 0.f;
+              tiles16::split_f16(x, h[i], l[i]);
+            }
+          }
+          const int off = t * C + 16 * nt + 4 * gq;
+          *reinterpret_cast<f16x4*>(rh + Rec16::PH + off) = f16x4{h[0], h[1], h[2], h[3]};
+          *reinterpret_cast<f16x4*>(rh + Rec16::PL + off) = f16x4{l[0], l[1], l[2], l[3]};
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // row c of T of record `half`: xc[i] = T[c][i]
+  float xc[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) xc[i] = 0.f;
+  const float* const at = s_at[wave][half];
+  pipe::solve_rows<19, 32>(at, c, xc);
+  pipe::solve_rows<13, 19>(at, c, xc);
+  pipe::solve_rows<9, 13>(at, c, xc);
+  pipe::solve_rows1<6, 9>(at, c, xc);
+  pipe::solve_rows1<3, 6>(at, c, xc);
+  pipe::solve_rows1<0, 3>(at, c, xc);
+  if ((half ? nval[1] : nval[0]) > 0) {
+    float* const tr = rec_h + R::T + c * C;
+#pragma unroll
+    for (int i = 0; i < C; i += 4) *reinterpret_cast<f32x4*>(tr + i) = f32x4{xc[i], xc[i + 1], xc[i + 2], xc[i + 3]};
+    // row c of T diag(beta) as fp16 pairs
+    f16* const rh = p.r16 + (half ? ri[1] : ri[0]) * (int64_t)Rec16::SIZE + c * C;
+    const float* const be = s_beta[wave][half];
+#pragma unroll
+    for (int j = 0; j < C; j += 8) {
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(be + j), b1 = *reinterpret_cast<const f32x4*>(be + j + 4);
+      f16x8 h, l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f16 hh, ll;
+        tiles16::split_f16(xc[j + i] * b0[i], hh, ll);
+        h[i] = hh;
+        l[i] = ll;
+        tiles16::split_f16(xc[j + 4 + i] * b1[i], hh, ll);
+        h[4 + i] = hh;
+        l[4 + i] = ll;
+      }
+      *reinterpret_cast<f16x8*>(rh + Rec16::TBH + j) = h;
+      *reinterpret_cast<f16x8*>(rh + Rec16::TBL + j) = l;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -972,7 +1189,9 @@ struct alignas(16) GSmem {
   // SD = VS + 4: rows of the V-step tiles are read 16 bytes per lane, lane
   // (r, kq) at row r, columns 4 kq .. 4 kq + 3 of a 16-column group; a row
   // stride of 4 (mod 32) words makes each 8-lane group's reads conflict-free.
-  static constexpr int KD = K + 1, CD = C + 1, SD = VS + 4;
+  // KD = K + 4: accumulator-layout accesses (lane (r, kq) at row 4 kq + i,
+  // column r) fall in 64 different banks, and rows are 16-byte aligned.
+  static constexpr int KD = K + 4, CD = C + 1, SD = VS + 4;
   float q[C][KD], k[C][KD];
   float dw[C][KD];   // dW = -du S^T
   float dwt[C][KD];  // dW~ = T^T dW
@@ -1063,8 +1282,10 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   lq.load(tid, static_cast<const TIn*>(p.q) + qb, p.sq[1], nval);
   lk.load(tid, static_cast<const TIn*>(p.k) + kb, p.sk[1], nval);
   lt.load(tid, rec + R::T, C, C);
-  lp.load(tid, rec + R::PM, C, C);
-  lkk.load(tid, rec + R::KK, C, C);
+  if constexpr (!ST16) {
+    lp.load(tid, rec + R::PM, C, C);
+    lkk.load(tid, rec + R::KK, C, C);
+  }
   const float gate = tid < 4 * C ? rec[R::G + tid] : 0.f;
   const uint32_t bvb =
       tid < nval ? load_bits(p.beta, head_base(rs, hi, p.sb) + (int64_t)(t0 + tid) * p.sb[1], p.beta_dtype) : 0u;
@@ -1205,8 +1426,10 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   lq.store(tid, s.q);
   lk.store(tid, s.k);
   lt.store(tid, s.t);
-  lp.store(tid, s.pm);
-  lkk.store(tid, s.kk);
+  if constexpr (!ST16) {
+    lp.store(tid, s.pm);
+    lkk.store(tid, s.kk);
+  }
   if (tid < C) {
     s.b[tid] = gate;
     s.bt[tid] = bits_to_float(bvb, p.beta_dtype);
@@ -1223,6 +1446,25 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   for (int e = tid; e < C * C; e += NTG) {
     const int t = e / C, j = e % C;
     s.m[t][j] = j <= t ? expf(s.b[t] - s.b[j]) : 0.f;
+  }
+  if constexpr (ST16 && !F16W) {
+    // K K^T (waves 0-3) and P = M o Q K^T (waves 4-7) from the 16-bit q
+    // and k rows (the 16-bit prep does not store them): one 16 x 16 tile
+    // per wave, the products exact and the sums in fp32 as in the prep
+    // (fp16 inputs form them after the V walk instead)
+    const int mt = (wave >> 1) & 1, nt = wave & 1;
+    constexpr int KD = GSmem<K, VS>::KD;
+    const float* const arow = (wave < 4 ? &s.k[0][0] : &s.q[0][0]) + (16 * mt + r) * KD + 8 * kq;
+    const float* const brow = &s.k[0][0] + (16 * nt + r) * KD + 8 * kq;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < K; kb += 32) acc = mma16<TIn>(pack16<TIn>(arow + kb), pack16<TIn>(brow + kb), acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * mt + 4 * kq + i, j = 16 * nt + r;
+      if (wave < 4) s.kk[t][j] = acc[i];
+      else s.pm[t][j] = j <= t ? expf(s.b[t] - s.b[j]) * acc[i] : 0.f;
+    }
   }
   // step vsi: `cur` holds step vsi + 1's rows (loaded a step ago), `nxt`
   // receives step vsi + 2's
@@ -1369,7 +1611,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     if (wave < 4) {
       const float y = pin(scale * s.m[row][col] * accC[0][e]);
       s.y[row][col] = y;
-      s.yp[row][col] = scale * accC[0][e] * s.pm[row][col];
+      if constexpr (!F16W) s.yp[row][col] = scale * accC[0][e] * s.pm[row][col];
       if constexpr (F16W) {
         s.x.yh[row][col] = (f16)y;
         s.x.yl[row][col] = (f16)(y - (float)(f16)y);
@@ -1413,6 +1655,24 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
         s.dt[row][col] = x;
         s.x.dth[row][col] = (f16)x;
         s.x.dtl[row][col] = (f16)(x - (float)(f16)x);
+      }
+    } else {
+      // K K^T and Q K^T (the 16-bit prep does not store them; exact
+      // products of the fp16 rows), one 16 x 16 tile of each per wave:
+      // K K^T -> kk, dQK o Q K^T = y o Q K^T -> yp
+      const int pm0 = ((wave - 4) >> 1) * 16, pn0 = (wave & 1) * 16;
+      f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
+#pragma unroll
+      for (int kb = 0; kb < K; kb += 32) {
+        const f16x8 kf = tiles16::frag8(&s.x.k[pn0 + r][kb + 8 * kq]);
+        akk = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.k[pm0 + r][kb + 8 * kq]), kf, akk, 0, 0, 0);
+        aqk = __builtin_amdgcn_mfma_f32_16x16x32_f16(tiles16::frag8(&s.x.q[pm0 + r][kb + 8 * kq]), kf, aqk, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = pm0 + 4 * kq + e, col = pn0 + r;
+        s.kk[row][col] = akk[e];
+        s.yp[row][col] = s.y[row][col] * aqk[e];
       }
     }
 #pragma unroll
@@ -1641,7 +1901,17 @@ inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
 
 template <typename TIn, int K>
 int launch_k(const BArgs& a, int64_t nrec, hipStream_t s) {
-  if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
+  if constexpr (!std::is_same<TIn, float>::value) {
+    if (nrec > 0) {
+      if (a.w16)
+        hipLaunchKernelGGL((prep16_kernel<TIn, K>), dim3((unsigned)((nrec + 4 * NRW - 1) / (4 * NRW))), dim3(256), 0,
+                           s, a, nrec);
+      else
+        hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
+    }
+  } else {
+    if (nrec > 0) hipLaunchKernelGGL((prep_kernel<TIn, K>), dim3((unsigned)nrec), dim3(NTP), 0, s, a);
+  }
   if constexpr (!std::is_same<TIn, float>::value) {
     if (a.w16) hipLaunchKernelGGL((recur16_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
     else hipLaunchKernelGGL((recur_kernel<TIn, K>), dim3(2 * a.units), dim3(NTP), 0, s, a);
