@@ -1207,7 +1207,14 @@ struct alignas(16) GSmem {
   union {
     struct {
       float v[C][SD], dO[C][SD], u[C][SD], du[C][SD];
-      float S[K][SD], dS[K][SD];
+      union {
+        struct {
+          float S[K][SD], dS[K][SD];  // fp32 states
+        } f;
+        struct {
+          f16 ST[VS][K + 8], dST[VS][K + 8];  // fp16 states of the 16-bit walks, as stored
+        } h;
+      } st;
     } w;
     struct {
       f16 v[C][HD], dO[C][HD], uh[C][HD], ul[C][HD], dh[C][HD], dl[C][HD];
@@ -1229,6 +1236,7 @@ struct alignas(16) GSmem {
   float rq[K / 16][C], rk[K / 16][C], rw[K / 16][C];  // row partials, one row per 16-column tile
   float vu[VS / 16][C];  // v.dU~ row partials, one row per 16-column tile
   float kw[C], dgam[C], dD[C], db[C], dbt[C];
+  float scs[VS / 16], scd[VS / 16];  // the V step's state scales (16-bit walks)
   float red[NTG / 64];
   float gC, dgC;
 };
@@ -1386,23 +1394,14 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
     x.lu.store(tid, s.w.u);
     x.ldu.store(tid, s.w.du);
     if constexpr (ST16) {
-      // [V][K] fp16 rows -> the fp32 [K][V] tiles, scaled back per 16-column
-      // slice (a power of two: exact)
-      auto scatter = [&](const SLoad& L, float (*dst)[GSmem<K, VS>::SD], const float (&sc)[2]) {
-#pragma unroll
-        for (int i = 0; i < SLoad::N; ++i) {
-          const int e = tid + i * NTG, v = e / (K / 8), k0 = 8 * (e % (K / 8));
-          if (VS * K / 8 % NTG == 0 || e < VS * K / 8) {
-            float xv[8];
-            unpack16<f16>(L.r[i], xv);
-            const float f = sc[v / 16];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) dst[k0 + j][v] = xv[j] * f;
-          }
-        }
-      };
-      scatter(x.lS, s.w.S, x.scS);
-      scatter(x.ldS, s.w.dS, x.scD);
+      // [V][K] fp16 rows as they are; the products read them transposed and
+      // scale them back per 16-column slice
+      x.lS.store_raw(tid, s.w.st.h.ST);
+      x.ldS.store_raw(tid, s.w.st.h.dST);
+      if (tid < VS / 16) {
+        s.scs[tid] = x.scS[tid];
+        s.scd[tid] = x.scD[tid];
+      }
       const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
       if (NDP == NTG || tid < NDP) {
         // dO has q's dtype here: a compile-time conversion
@@ -1412,8 +1411,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
         s.w.dO[t][c2 + 1] = ok ? bits_to_float(x.rdo[0] >> 16, dt) : 0.f;
       }
     } else {
-      x.lS.store(tid, s.w.S);
-      x.ldS.store(tid, s.w.dS);
+      x.lS.store(tid, s.w.st.f.S);
+      x.ldS.store(tid, s.w.st.f.dS);
 #pragma unroll
       for (int i = 0; i < NDO; ++i) {
         const int e = tid + i * NTG;
@@ -1528,7 +1527,21 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 #pragma unroll
         for (int g = 0; g < NPW; ++g) {
           if (g < ana) {
-            const f32x4 sb = ld4(s.w.S, an0[g] + r, cc), db = ld4(s.w.dS, an0[g] + r, cc);
+            f32x4 sb, db;
+            if constexpr (ST16) {
+              // S[an0 + r][cc + j] = S^T[cc + j][an0 + r]: transposed reads
+              const f16x4 hs = tiles16::frag4_t(s.w.st.h.ST, c0, an0[g], r, kq);
+              const f16x4 hd = tiles16::frag4_t(s.w.st.h.dST, c0, an0[g], r, kq);
+              const float fs = s.scs[c0 / 16], fd = s.scd[c0 / 16];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                sb[j] = (float)hs[j] * fs;
+                db[j] = (float)hd[j] * fd;
+              }
+            } else {
+              sb = ld4(s.w.st.f.S, an0[g] + r, cc);
+              db = ld4(s.w.st.f.dS, an0[g] + r, cc);
+            }
             const f32x4 xa = ld4(s.w.du, am0[g] + r, cc), xo = ld4(s.w.dO, am0[g] + r, cc);
             const f32x4 xu = ld4(s.w.u, am0[g] + r, cc);
 #pragma unroll
@@ -1546,8 +1559,16 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) accC[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[j], yc[j], accC[0], 0, 0, 0);
       }
-      for (int e = tid; e < K * VS; e += NTG)
-        dgc_acc = __builtin_fmaf(s.w.S[e / VS][e % VS], s.w.dS[e / VS][e % VS], dgc_acc);
+      if constexpr (ST16) {
+        for (int e = tid; e < K * VS; e += NTG) {
+          const int v = e / K, kk = e % K;
+          dgc_acc = __builtin_fmaf((float)s.w.st.h.ST[v][kk] * s.scs[v / 16],
+                                   (float)s.w.st.h.dST[v][kk] * s.scd[v / 16], dgc_acc);
+        }
+      } else {
+        for (int e = tid; e < K * VS; e += NTG)
+          dgc_acc = __builtin_fmaf(s.w.st.f.S[e / VS][e % VS], s.w.st.f.dS[e / VS][e % VS], dgc_acc);
+      }
     }
     __syncthreads();
     if (vsi + 1 < nvs) {

@@ -63,6 +63,16 @@ __device__ __forceinline__ f16x8 frag8_t(const f16 (*x)[LD], int t0, int m0, int
   return u.f;
 }
 
+// The same with 4 contraction indices t0 + 4 kq .. t0 + 4 kq + 3 (one
+// ds_read_b64_tr_b16): lane (r, kq) receives X[t0 + 4 kq + j][m0 + r].
+template <int LD>
+__device__ __forceinline__ f16x4 frag4_t(const f16 (*x)[LD], int t0, int m0, int r, int kq) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const f16* const a0 = &x[t0 + 4 * kq + (r >> 2)][m0 + 4 * (r & 3)];
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0));
+}
+
 // The loaders below load unconditionally, guarded at most by a wave-uniform
 // test (none when the vectors fill every lane): a lane-masked load, a zero
 // written into a register a load may still target, or a load that a later
