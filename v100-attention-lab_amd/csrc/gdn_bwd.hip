@@ -1212,7 +1212,11 @@ struct alignas(16) GSmem {
           float S[K][SD], dS[K][SD];  // fp32 states
         } f;
         struct {
-          f16 ST[VS][K + 8], dST[VS][K + 8];  // fp16 states of the 16-bit walks, as stored
+          // fp16 states of the 16-bit walks, as stored; K + 16 halves (8
+          // words past a multiple of 64) puts the 8-byte transposed reads
+          // of 32 lanes (rows 4 kq + r / 4, columns 4 (r % 4)) in 64
+          // different banks
+          f16 ST[VS][K + 16], dST[VS][K + 16];
         } h;
       } st;
     } w;
@@ -1236,7 +1240,7 @@ struct alignas(16) GSmem {
   float rq[K / 16][C], rk[K / 16][C], rw[K / 16][C];  // row partials, one row per 16-column tile
   float vu[VS / 16][C];  // v.dU~ row partials, one row per 16-column tile
   float kw[C], dgam[C], dD[C], db[C], dbt[C];
-  float scs[VS / 16], scd[VS / 16];  // the V step's state scales (16-bit walks)
+  float scs[VS], scd[VS];  // the V step's state scales per state column (16-bit walks)
   float red[NTG / 64];
   float gC, dgC;
 };
@@ -1398,9 +1402,15 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       // scale them back per 16-column slice
       x.lS.store_raw(tid, s.w.st.h.ST);
       x.ldS.store_raw(tid, s.w.st.h.dST);
-      if (tid < VS / 16) {
-        s.scs[tid] = x.scS[tid];
-        s.scd[tid] = x.scD[tid];
+      {
+        // every thread writes its column's scales (the same value as the
+        // other threads of the column): the scale loads are consumed on
+        // every lane, so they stay where they were issued, a step ahead
+        // (constant indices into the register arrays: a variable index
+        // would put the step's rows in scratch memory)
+        const int v = (tid / (K / 8)) % VS;
+        s.scs[v] = v < 16 ? x.scS[0] : x.scS[VS / 16 - 1];
+        s.scd[v] = v < 16 ? x.scD[0] : x.scD[VS / 16 - 1];
       }
       const int t = tid / (VS / 2), c2 = 2 * (tid % (VS / 2));
       if (NDP == NTG || tid < NDP) {
@@ -1467,6 +1477,21 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
   }
   // step vsi: `cur` holds step vsi + 1's rows (loaded a step ago), `nxt`
   // receives step vsi + 2's
+  // this thread's part of <S, dS'> over the step's fp16 state rows ([V][K]
+  // as stored): 8 consecutive keys of state column tid / (K / 8), times the
+  // column's two scales
+  auto state_dot = [&](const auto& st, const auto& dst, float fs, float fd) __attribute__((always_inline)) {
+    static_assert(VS * K / 8 <= NTG, "one 8-key piece per thread at most");
+    float x = 0.f;
+    const int v = tid / (K / 8), k0 = 8 * (tid % (K / 8));
+    if (VS * K / 8 == NTG || tid < VS * K / 8) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>(&st[v][k0]);
+      const f16x8 b = *reinterpret_cast<const f16x8*>(&dst[v][k0]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x = __builtin_fmaf((float)a[j], (float)b[j], x);
+    }
+    return x * (fs * fd);
+  };
   auto step = [&](int vsi, StepRows& cur, StepRows& nxt) __attribute__((always_inline)) {
     const int v0 = vsi * VS;
     // dU~ of the step and dv first: its stores go out before the next
@@ -1518,8 +1543,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
       const f16x8 yl = tiles16::frag8(&s.h.ul[cn0[0] + r][c8]);
       accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, yh, accC[0], 0, 0, 0);
       accC[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wave < 4 ? xh : xl, wave < 4 ? yl : yh, accC[0], 0, 0, 0);
-      for (int e = tid; e < K * VS; e += NTG)
-        dgc_acc = __builtin_fmaf((float)s.h.ST[e / K][e % K], (float)s.h.dST[e / K][e % K], dgc_acc);
+      dgc_acc += state_dot(s.h.ST, s.h.dST, 1.f, 1.f);
     } else {
 #pragma unroll
       for (int c0 = 0; c0 < VS; c0 += 16) {
@@ -1532,7 +1556,7 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
               // S[an0 + r][cc + j] = S^T[cc + j][an0 + r]: transposed reads
               const f16x4 hs = tiles16::frag4_t(s.w.st.h.ST, c0, an0[g], r, kq);
               const f16x4 hd = tiles16::frag4_t(s.w.st.h.dST, c0, an0[g], r, kq);
-              const float fs = s.scs[c0 / 16], fd = s.scd[c0 / 16];
+              const float fs = s.scs[c0], fd = s.scd[c0];
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
                 sb[j] = (float)hs[j] * fs;
@@ -1560,11 +1584,8 @@ __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
         for (int j = 0; j < 4; ++j) accC[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[j], yc[j], accC[0], 0, 0, 0);
       }
       if constexpr (ST16) {
-        for (int e = tid; e < K * VS; e += NTG) {
-          const int v = e / K, kk = e % K;
-          dgc_acc = __builtin_fmaf((float)s.w.st.h.ST[v][kk] * s.scs[v / 16],
-                                   (float)s.w.st.h.dST[v][kk] * s.scd[v / 16], dgc_acc);
-        }
+        const int v = (tid / (K / 8)) % VS;
+        dgc_acc += state_dot(s.w.st.h.ST, s.w.st.h.dST, s.scs[v], s.scd[v]);
       } else {
         for (int e = tid; e < K * VS; e += NTG)
           dgc_acc = __builtin_fmaf(s.w.st.f.S[e / VS][e % VS], s.w.st.f.dS[e / VS][e % VS], dgc_acc);
