@@ -416,7 +416,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   constexpr int R = S::R, RR = S::RR;
   constexpr int ND = dma_per_chunk<K, BV>();
   static_assert(sizeof(TIn) == 2, "16-bit inputs");
-  static_assert((D - 1) * ND < 64, "outstanding DMA copies fit vmcnt");
+  static_assert((D - 2) * ND < 64, "outstanding DMA copies fit vmcnt");
   static_assert(C * BV * 2 % 1024 == 0, "v slice rows fill whole DMA copies");
 
   __shared__ S s;
@@ -493,58 +493,71 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       s.so[0][cb][kb][lane] = sB[kb];
     }
     PS_DECL;
-    if (nloc > 0) wg_barrier();
-    for (int it = 0; it < nloc; ++it) {
+    // One chunk's operands of the chain, in registers.  Chunk it + 1's are
+    // read from LDS while chunk it computes (the LOAD wave publishes chunks
+    // two ahead), so the chain K S -> u -> S waits on no LDS read.
+    struct ScanOps {
+      f16x8 kR[2][KB], kA[KT];
+      f16x4 va, vb;
+      f16x8 tu0, tu1;
+      f32x4 eb_lo, eb_hi, ec_lo, ec_hi;
+      float ebC;
+    };
+    const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
+    const int vc = (16 * cb + 4 * (n & 3)) * 2;
+    auto read_ops = [&](int it, ScanOps& o) __attribute__((always_inline)) {
       const int sl = it % R;
       const char* rc = s.rec[it % RR];
-      f16x8 kR[2][KB], kA[KT];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+        for (int kb = 0; kb < KB; ++kb) o.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
       const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
-      const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
 #pragma unroll
       for (int r = 0; r < KT; ++r) {
         const int piece = 4 * (r >> 1) + (n & 3);
         const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
         const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
-        kA[r] = cat8(lo, hi4);
+        o.kA[r] = cat8(lo, hi4);
       }
       // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
       const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
-      const int vc = (16 * cb + 4 * (n & 3)) * 2;
-      const f16x4 va = lds_tr16(vbase + t0 * (BV * 2) + vc);
-      const f16x4 vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+      o.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+      o.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
       const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
-      const f16x8 tu0 = tu[lane], tu1 = tu[64 + lane];
+      o.tu0 = tu[lane];
+      o.tu1 = tu[64 + lane];
       const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
       const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
-      const f32x4 eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
-      const f32x4 eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
-      const f32x4 ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
-      const f32x4 ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
-      const float ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+      o.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+      o.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+      o.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+      o.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+      o.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+    };
+    auto chunk = [&](int it, const ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
+      // the next chunk's operands (the last chunk's again at the end)
+      read_ops(min(it + 1, nloc - 1), nx);
       // K S: rows t, so its two row tiles form a B operand over t
       f32x4 ks[2] = {z4, z4};
-      PS_BEGIN(kR[0][0], kR[1][0], sB[0], kA[0]);
+      PS_BEGIN(o.kR[0][0], o.kR[1][0], sB[0], o.kA[0]);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(kR[mt][kb], sB[kb], ks[mt]);
+        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(o.kR[mt][kb], sB[kb], ks[mt]);
       f32x4 y0, y1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        y0[i] = (float)va[i] - eb_lo[i] * ks[0][i];
-        y1[i] = (float)vb[i] - eb_hi[i] * ks[1][i];
+        y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
+        y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
       }
       const f16x8 yB = M::from_acc(y0, y1);
       f32x4 u[2];
-      u[0] = M::mma(tu0, yB, z4);
-      u[1] = M::mma(tu1, yB, z4);
-      const f16x8 utB = M::from_acc(u[0] * ec_lo, u[1] * ec_hi);
+      u[0] = M::mma(o.tu0, yB, z4);
+      u[1] = M::mma(o.tu1, yB, z4);
+      const f16x8 utB = M::from_acc(u[0] * o.ec_lo, u[1] * o.ec_hi);
 #pragma unroll
-      for (int r = 0; r < KT; ++r) st[r] = M::mma(kA[r], utB, st[r] * ebC);
+      for (int r = 0; r < KT; ++r) st[r] = M::mma(o.kA[r], utB, st[r] * o.ebC);
       {
         const f16x8 uh = M::from_acc(u[0], u[1]);
         s.uo[it & 1][cb][0][lane] = uh;
@@ -556,6 +569,15 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
       wg_barrier();
+    };
+    ScanOps oa, ob;
+    if (nloc > 0) {
+      wg_barrier();
+      read_ops(0, oa);
+    }
+    for (int it = 0; it < nloc; it += 2) {
+      chunk(it, oa, ob);
+      if (it + 1 < nloc) chunk(it + 1, ob, oa);
     }
     PS_RECORD(1, nloc, 2 * KB + 2 + KT, 0);
     float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
@@ -729,18 +751,20 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 #pragma unroll
       for (int i = 0; i < REC_BYTES / 1024; ++i) dma16(rsrc + 1024 * i + 16 * lane, s.rec[it % RR] + 1024 * i);
     };
+    // Chunks 0 and 1 are published at the first barrier, and chunk it + 2
+    // at iteration it's: the SCAN wave reads chunk it + 1's operands during
+    // iteration it.
     for (int it = 0; it < D; ++it)
       if (it < nloc) issue(it);
     if (nloc >= D)
-      wait_vm<(D - 1) * ND>();
+      wait_vm<(D - 2) * ND>();
     else
       wait_vm<0>();
     wg_barrier();
     for (int it = 0; it < nloc; ++it) {
-      // chunk it + 1 must be in LDS at this iteration's barrier
       if (it + D < nloc) {
         issue(it + D);
-        wait_vm<(D - 1) * ND>();
+        wait_vm<(D - 2) * ND>();
       } else {
         wait_vm<0>();
       }
