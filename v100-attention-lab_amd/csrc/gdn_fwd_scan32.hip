@@ -535,16 +535,31 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       o.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
       o.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
     };
-    auto chunk = [&](int it, const ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
-      // the next chunk's operands (the last chunk's again at the end)
-      read_ops(min(it + 1, nloc - 1), nx);
-      // K S: rows t, so its two row tiles form a B operand over t
+    // The next chunk's reads go out between the chain's MFMAs (a few per
+    // MFMA, placed by sched_group_barrier): issued all at once they would
+    // fill the wave's LDS queue and hold the first MFMA back until most had
+    // returned.
+    constexpr int SG_MFMA = 0x8, SG_DSR = 0x100;
+    auto chunk = [&](int it, ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
+      const int itn = min(it + 1, nloc - 1);  // the last chunk's again at the end
+      const int sl = itn % R;
+      const char* rc = s.rec[itn % RR];
+      // K S: rows t, so its two row tiles form a B operand over t; the next
+      // chunk's k rows in between
       f32x4 ks[2] = {z4, z4};
       PS_BEGIN(o.kR[0][0], o.kR[1][0], sB[0], o.kA[0]);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) ks[mt] = M::mma(o.kR[mt][kb], sB[kb], ks[mt]);
+        for (int mt = 0; mt < 2; ++mt) {
+          ks[mt] = M::mma(o.kR[mt][kb], sB[kb], ks[mt]);
+          nx.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+        }
+#pragma unroll
+      for (int g = 0; g < 2 * KB; ++g) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
+      }
       f32x4 y0, y1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -555,9 +570,42 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       f32x4 u[2];
       u[0] = M::mma(o.tu0, yB, z4);
       u[1] = M::mma(o.tu1, yB, z4);
+      {
+        // the next chunk's v column and record fields
+        const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
+        nx.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+        nx.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+        const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
+        nx.tu0 = tu[lane];
+        nx.tu1 = tu[64 + lane];
+        const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
+        const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
+        nx.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+        nx.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+        nx.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+        nx.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+        nx.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DSR, 5, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DSR, 4, 0);
       const f16x8 utB = M::from_acc(u[0] * o.ec_lo, u[1] * o.ec_hi);
+      // state update; the next chunk's transposed k fragments in between
+      const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
 #pragma unroll
-      for (int r = 0; r < KT; ++r) st[r] = M::mma(o.kA[r], utB, st[r] * o.ebC);
+      for (int r = 0; r < KT; ++r) {
+        st[r] = M::mma(o.kA[r], utB, st[r] * o.ebC);
+        const int piece = 4 * (r >> 1) + (n & 3);
+        const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
+        const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
+        nx.kA[r] = cat8(lo, hi4);
+      }
+#pragma unroll
+      for (int r = 0; r < KT; ++r) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DSR, 2, 0);
+      }
       {
         const f16x8 uh = M::from_acc(u[0], u[1]);
         s.uo[it & 1][cb][0][lane] = uh;
