@@ -122,7 +122,8 @@ typedef struct GdnFwdParams {
 /* Enqueue one chunked GDN forward on `stream` (a hipStream_t; NULL = the
  * legacy default stream).  Returns a GdnStatus / hipError_t value.
  * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140).
- *   - C = 32, fp16 q/k/v, K in {64, 128}, with a workspace, and C = 64 with
+ *   - C = 32, fp16 or bf16 q/k/v (bf16: V <= 2496), K in {64, 128}, with a
+ *     workspace, and C = 64 with
  *     K in {32, 64, 128} (any dtype; block_v is 16 there): two launches per
  *     segment of the sequence (per-chunk records of the state-independent
  *     work, then the scan over chunks).  The segment length is what the
@@ -131,8 +132,8 @@ typedef struct GdnFwdParams {
  *     gdn_fwd_workspace_size() bytes runs the call; a longer sequence runs
  *     as several segments, its state passing through final_state in fp32.
  *     C = 64 needs params->workspace.
- *   - C = 32 without a workspace (or GDN_FLAG_FUSED_KERNEL), bf16, or K = 256
- *     / GDN_FLAG_PHASED_KERNEL: one fused kernel, no workspace.
+ *   - C = 32 without a workspace (or GDN_FLAG_FUSED_KERNEL), or K = 256 /
+ *     GDN_FLAG_PHASED_KERNEL: one fused kernel, no workspace.
  * The state stays on chip in every path: no chunk state is written. */
 int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
 
@@ -145,10 +146,10 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  * workspace (32-row records, 64-row records) use a static device array of
  * gdn_fwd_scratch_bytes() bytes (32 MiB) held by each device from the
  * library's load to the end of the process.
- *   - 32-row chunks (fp16): the sequence runs in segments of as many chunks
- *     as the array holds (B * H records of 3 KB per chunk); the call fails
- *     with GDN_ERR_SCRATCH_LIMIT only if one chunk per sequence does not
- *     fit (B * H > 10922).
+ *   - 32-row chunks (fp16, bf16): the sequence runs in segments of as many
+ *     chunks as the array holds (B * H records of 3 KB per chunk); if one
+ *     chunk per sequence does not fit (B * H > 10922), bf16 runs on the
+ *     fused kernel and fp16 fails with GDN_ERR_SCRATCH_LIMIT.
  *   - 64-row chunks: likewise in segments (records of 33 KB per chunk and
  *     head for 16-bit inputs, 66 KB for fp32 at K = 128); GDN_ERR_SCRATCH_LIMIT
  *     only if one chunk per sequence does not fit (B * H > 992 for 16-bit

@@ -97,8 +97,8 @@ def _params(L, **kw):
 
 
 def test_fwd_workspace_size(lib, pkg):
-    """Fused kernels need no workspace.  32-row chunks with fp16 q/k/v and
-    K in {64, 128} take one 3 KB record per (sequence, head, chunk) of a
+    """Fused kernels need no workspace.  32-row chunks with fp16 or bf16
+    q/k/v and K in {64, 128} take one 3 KB record per (sequence, head, chunk) of a
     segment of at most 256 chunks.  64-row chunks with K <= 128 take one
     record per (chunk slot, head).  fp32 inputs: T and P (C x C), W (C x K)
     in fp32, then three gate rows.  16-bit inputs: T diag(beta) and P (C x C)
@@ -112,7 +112,8 @@ def test_fwd_workspace_size(lib, pkg):
     assert size(T=0) == 0
     assert size(B=3, T=100, cu_seqlens=0x2000) == 3 * H * 4 * 3072
     assert size(flags=2) == 0                            # fused kernel forced: none
-    assert size(qkv_dtype=2) == 0                        # bf16: fused kernel, none
+    assert size(qkv_dtype=2) == 2 * H * 128 * 3072       # bf16: the same records
+    assert size(qkv_dtype=2, V=2512) == 0                # bf16, V / 16 > 156: fused kernel, none
     assert size(qkv_dtype=0) == 0                        # fp32: phased kernel, none
     assert size(K=32) == 0 and size(K=256) == 0          # phased kernel, none
     assert size(chunk_size=64, K=256) == 0               # phased kernel, none

@@ -290,13 +290,14 @@ def test_c64_degenerate_and_agrees_with_phased(pkg, cuda):
 
 
 SEG_CASES = [(1000, 3, 32, torch.float16), (4096, 1, 32, torch.float16), (77, 2, 32, torch.float16),
+             (1000, 3, 32, torch.bfloat16),
              (1000, 3, 64, torch.float16), (4096, 1, 64, torch.float16), (200, 2, 64, torch.bfloat16),
              (300, 2, 64, torch.float32)]
 
 
 @pytest.mark.parametrize("T,seg,C,dtype", SEG_CASES)
 def test_segments_equal_one_pass(pkg, cuda, T, seg, C, dtype):
-    """The two-launch paths (32-row fp16, 64-row any dtype) with records for
+    """The two-launch paths (32-row fp16/bf16, 64-row any dtype) with records for
     only `seg` chunks per sequence run a sequence as consecutive segments,
     the state passing through final_state (fp32, exact): outputs are
     bit-equal to the one-segment run, with and without h0, batched and

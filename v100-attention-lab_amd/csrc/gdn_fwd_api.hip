@@ -54,7 +54,7 @@ constexpr int64_t kSegChunks = 256;
 // another kernel is asked for.
 static bool uses_scan32(const GdnFwdParams& P, int bv) {
   return !(P.flags & (GDN_FLAG_PHASED_KERNEL | GDN_FLAG_FUSED_KERNEL)) &&
-         scan32_supported(P.qkv_dtype, P.K, P.chunk_size, bv) && pipe_offsets_fit(P);
+         scan32_supported(P.qkv_dtype, P.K, P.chunk_size, bv, P.V) && pipe_offsets_fit(P);
 }
 
 // ---------------------------------------------------------------------------
@@ -127,7 +127,12 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   }
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
-  const bool scan32 = uses_scan32(P, bv) && (scratch_bytes > 0 || P.workspace != nullptr);
+  bool scan32 = uses_scan32(P, bv) && (scratch_bytes > 0 || P.workspace != nullptr);
+  // bf16 runs on the fused kernel (no workspace) when the static scratch
+  // cannot hold its records
+  if (scan32 && scratch_bytes > 0 && P.qkv_dtype == GDN_DTYPE_BF16 &&
+      (int64_t)P.B * P.H * scan32_record_bytes() > scratch_bytes)
+    scan32 = false;
   // workspace: the caller's, or the static scratch array when it holds
   // what the path needs
   GdnFwdParams W = P;

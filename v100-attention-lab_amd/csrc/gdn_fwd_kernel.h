@@ -171,6 +171,37 @@ struct InTraits<float> {
 __device__ __forceinline__ uint32_t bf16x2_absmax_bits(uint32_t w) {
   return max((w & 0x7fffu) << 16, w & 0x7fff0000u);
 }
+__device__ __forceinline__ uint32_t bf16x8_absmax_bits(const uint4& x) {
+  return max(max(bf16x2_absmax_bits(x.x), bf16x2_absmax_bits(x.y)),
+             max(bf16x2_absmax_bits(x.z), bf16x2_absmax_bits(x.w)));
+}
+
+// This thread's part of the largest magnitude of h0[K x cols] (fp32,
+// element strides sk and sc; nullable), as float bits.
+__device__ __forceinline__ uint32_t state_absmax_bits(const float* h0, int64_t sk, int64_t sc, int K, int cols) {
+  uint32_t m = 0;
+  if (h0 != nullptr) {
+    const int64_t nh = (int64_t)K * cols;
+    for (int64_t i = threadIdx.x; i < nh; i += blockDim.x) {
+      const int64_t kk = i / cols;
+      const int c = (int)(i - kk * cols);
+      m = max(m, __float_as_uint(h0[kk * sk + c * sc]) & 0x7fffffffu);
+    }
+  }
+  return m;
+}
+
+// Maximum of m over the workgroup (every thread calls it; one barrier;
+// red holds a value per wave).
+__device__ __forceinline__ uint32_t block_max_bits(uint32_t m, uint32_t* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = 0;
+  for (int w = 0; w < (int)(blockDim.x + 63) / 64; ++w) m = max(m, red[w]);
+  return m;
+}
 
 // Largest magnitude of v[rows x cols] (bf16, rows `rstride` bytes apart,
 // cols a multiple of 8, 16-byte aligned rows) and of h0[K x cols] (fp32,
@@ -182,29 +213,30 @@ __device__ __forceinline__ float slice_absmax_bf16(const char* v, int64_t rstrid
   const int tid = threadIdx.x, nthr = blockDim.x;
   uint32_t m = 0;
   const int pieces = cols >> 3;
-  const int64_t nv = (int64_t)rows * pieces;
-  for (int64_t i = tid; i < nv; i += nthr) {
-    const int64_t r = i / pieces;
-    const int c = (int)(i - r * pieces);
-    const uint4 x = *reinterpret_cast<const uint4*>(v + r * rstride + c * 16);
-    m = max(m, max(max(bf16x2_absmax_bits(x.x), bf16x2_absmax_bits(x.y)),
-                   max(bf16x2_absmax_bits(x.z), bf16x2_absmax_bits(x.w))));
-  }
-  if (h0 != nullptr) {
-    const int64_t nh = (int64_t)K * cols;
-    for (int64_t i = tid; i < nh; i += nthr) {
-      const int64_t kk = i / cols;
-      const int c = (int)(i - kk * cols);
-      m = max(m, __float_as_uint(h0[kk * sk + c * sc]) & 0x7fffffffu);
+  auto piece_max = [](const uint4& x) { return bf16x8_absmax_bits(x); };
+  if (nthr % pieces == 0) {
+    // a fixed 16-byte column piece per thread, rows nthr / pieces apart,
+    // eight loads in flight
+    const int rstep = nthr / pieces;
+    const char* const vc = v + (tid % pieces) * 16;
+    int r = tid / pieces;
+    for (; r + 7 * rstep < rows; r += 8 * rstep) {
+      uint4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const uint4*>(vc + (int64_t)(r + u * rstep) * rstride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) m = max(m, piece_max(x[u]));
+    }
+    for (; r < rows; r += rstep) m = max(m, piece_max(*reinterpret_cast<const uint4*>(vc + (int64_t)r * rstride)));
+  } else {
+    const int64_t nv = (int64_t)rows * pieces;
+    for (int64_t i = tid; i < nv; i += nthr) {
+      const int64_t r = i / pieces;
+      const int c = (int)(i - r * pieces);
+      m = max(m, piece_max(*reinterpret_cast<const uint4*>(v + r * rstride + c * 16)));
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
-  if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
-  m = 0;
-  for (int w = 0; w < (nthr + 63) / 64; ++w) m = max(m, red[w]);
-  return __uint_as_float(m);
+  return __uint_as_float(block_max_bits(max(m, state_absmax_bits(h0, sk, sc, K, cols)), red));
 }
 
 // The shift s for a slice whose largest magnitude is m: 0 when m is zero,
@@ -222,6 +254,17 @@ __device__ __forceinline__ int range_shift(float m) {
 struct RangeScale {
   float v = 1.f, o = 1.f, fs = 1.f;
 };
+
+// The scale factors for a slice whose largest magnitude is m (v and h0
+// taken together).
+__device__ __forceinline__ RangeScale range_scale_of(float m, float scale) {
+  RangeScale r;
+  const int sh = range_shift(m);
+  r.v = ldexpf(1.f, sh);
+  r.fs = ldexpf(1.f, -sh);
+  r.o = scale * r.fs;
+  return r;
+}
 
 template <typename TIn>
 __device__ __forceinline__ RangeScale slice_range_scale(const char* v, int64_t rstride, int rows, int cols,
@@ -871,10 +914,10 @@ constexpr int64_t kSegC64 = 64;
 int64_t c64_record_bytes(int K, int qkv_dtype);
 int64_t c64_workspace_size(int B, int T, int H, int K, int n_seq, int qkv_dtype);
 int c64_launch(const GdnFwdParams& P, int seg_chunks, hipStream_t stream);
-// 32-row chunks, fp16, K in {64, 128}, BV in {16, 32}: per-chunk records
+// 32-row chunks, fp16 or bf16 (V / 16 <= 156), K in {64, 128}, BV in {16, 32}: per-chunk records
 // then the scan (gdn_fwd_scan32.hip), in segments of at most seg_chunks
 // chunks per sequence whose records fit the caller's workspace.
-bool scan32_supported(int dtype, int K, int C, int BV);
+bool scan32_supported(int dtype, int K, int C, int BV, int V);
 int64_t scan32_record_bytes();
 int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t stream);
 

@@ -60,6 +60,8 @@ constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b (flat past the sequ
 constexpr int R_EB = 2176;  // float [32]: e^b
 constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
 constexpr int R_EBC = 2432; // float: e^{bC}
+constexpr int R_VMAX = 2448; // float [V / 16] (bf16 inputs): largest |v| of each 16-column slice of the rows
+constexpr int kMaxVSlices = (REC_BYTES - R_VMAX) / 4;
 
 struct SArgs {
   const void* q;
@@ -203,6 +205,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   // the two records of this wave: geometry (wave-uniform)
   int nval[2];
   const char* kh[2];
+  const char* vh[2];
   char* rp[2];
   uint32_t skb[2];
 #pragma unroll
@@ -210,6 +213,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
     const int r = (blockIdx.x * 4 + wave) * 2 + e;
     nval[e] = 0;
     kh[e] = nullptr;
+    vh[e] = nullptr;
     rp[e] = nullptr;
     skb[e] = 0;
     if (r < p.nrec) {
@@ -221,6 +225,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
         nval[e] = min(C, rs.T - t0);
         kh[e] = static_cast<const char*>(p.k) + (head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1]) * EB;
         skb[e] = (uint32_t)p.sk[1] * EB;
+        vh[e] = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + (int64_t)t0 * p.sv[1]) * EB;
         rp[e] = p.rec + (int64_t)r * REC_BYTES;
       }
     }
@@ -353,6 +358,37 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
       tu[mt * 64 + 16 * g4 + nl] = fu;
     }
   }
+  // bf16 inputs: the largest |v| of each 16-column slice of the record's
+  // rows (rows past the end re-read the last row), from which the scan
+  // takes its range scale.  Lane (rg, sl8): rows 4 rg .. 4 rg + 3 of slice
+  // sb + sl8, reduced over rg.
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    const int nsl = p.V / 16, sl8 = lane & 7, rg = lane >> 3;
+    const int64_t svb = p.sv[1] * (int64_t)EB;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      if (nval[e] == 0) continue;
+      for (int sb = 0; sb < nsl; sb += 8) {
+        const int slc = sb + sl8;
+        uint32_t m = 0;
+        if (slc < nsl) {
+          uint4 x[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const char* row = vh[e] + (int64_t)min(4 * rg + i, nval[e] - 1) * svb + slc * 32;
+            x[2 * i] = *reinterpret_cast<const uint4*>(row);
+            x[2 * i + 1] = *reinterpret_cast<const uint4*>(row + 16);
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) m = max(m, bf16x8_absmax_bits(x[i]));
+        }
+        m = max(m, (uint32_t)__shfl_xor((int)m, 8));
+        m = max(m, (uint32_t)__shfl_xor((int)m, 16));
+        m = max(m, (uint32_t)__shfl_xor((int)m, 32));
+        if (rg == 0 && slc < nsl) reinterpret_cast<float*>(rp[e] + R_VMAX)[slc] = __uint_as_float(m);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -416,6 +452,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   constexpr int R = S::R, RR = S::RR;
   constexpr int ND = dma_per_chunk<K, BV>();
   static_assert(sizeof(TIn) == 2, "16-bit inputs");
+  static_assert(std::is_same<TIn, f16>::value || std::is_same<TIn, bf16_t>::value, "fp16 or bf16 inputs");
   static_assert((D - 2) * ND < 64, "outstanding DMA copies fit vmcnt");
   static_assert(C * BV * 2 % 1024 == 0, "v slice rows fill whole DMA copies");
 
@@ -448,21 +485,43 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   const char* kh = static_cast<const char*>(p.k) + head_base(rs, hi, p.sk) * EB;
   const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
   const char* rech = p.rec + (int64_t)(bi * p.H + hi) * p.L * REC_BYTES;
+  // bf16: this slice's v and initial state scaled by a power of two into
+  // fp16's range (from their absolute maximum over the whole sequence), o
+  // and the final state scaled back; identity for fp16
+  const float* const st_src = p.first ? p.h0 : p.fs;
+  const int64_t* const st_sd = p.first ? p.sh0 : p.sfs;
+  RangeScale rsc;
+  rsc.o = p.scale;
+  if constexpr (std::is_same<TIn, bf16_t>::value) {
+    // the largest |v| of this slice over the segment's records and of the
+    // incoming state
+    __shared__ uint32_t red[8];
+    uint32_t m = state_absmax_bits(st_src ? st_src + bi * st_sd[0] + hi * st_sd[1] + v0 * st_sd[3] : nullptr,
+                                   st_sd[2], st_sd[3], K, BV);
+    for (int i = tid; i < nloc * NSW; i += 64 * scan_waves<BV>()) {
+      const float* vm = reinterpret_cast<const float*>(rech + (int64_t)(i / NSW) * REC_BYTES + R_VMAX);
+      m = max(m, __float_as_uint(vm[v0 / 16 + i % NSW]));
+    }
+    rsc = range_scale_of(__uint_as_float(block_max_bits(m, red)), p.scale);
+  }
 
   auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int cc) { return tile[r][swz<K>(r, cc)]; };
 
+  // Waves w and w + 4 share SIMD w % 4.  At BV = 32 (six waves) the SCAN
+  // waves take waves 2 and 3, alone on their SIMDs.  For fp16 the OUT waves
+  // share theirs with PQK and LOAD; for bf16, whose LOAD wave also converts
+  // the staged tiles, the two OUT waves share one SIMD and PQK and LOAD the
+  // other.
   int role, ridx;
-  if (wave < NSW) {
-    role = SR_SCAN;
-    ridx = wave;
-  } else if (wave < 2 * NSW) {
-    role = SR_OUT;
-    ridx = wave - NSW;
-  } else if (wave == 2 * NSW) {
-    role = SR_PQK;
-    ridx = 0;
+  if constexpr (NSW == 2) {
+    constexpr bool pair_out = std::is_same<TIn, bf16_t>::value;
+    constexpr int roles[6] = {SR_OUT, pair_out ? SR_PQK : SR_OUT, SR_SCAN, SR_SCAN,
+                              pair_out ? SR_OUT : SR_PQK, SR_LOAD};
+    constexpr int idx[6] = {0, pair_out ? 0 : 1, 0, 1, pair_out ? 1 : 0, 0};
+    role = roles[wave];
+    ridx = idx[wave];
   } else {
-    role = SR_LOAD;
+    role = wave == 0 ? SR_SCAN : wave == 1 ? SR_OUT : wave == 2 ? SR_PQK : SR_LOAD;
     ridx = 0;
   }
 
@@ -474,8 +533,8 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     auto key_of = [&](int r, int i) { return 32 * (r >> 1) + 8 * gq + 4 * (r & 1) + i; };
     f32x4 st[KT];
     {
-      const float* src = p.first ? p.h0 : p.fs;
-      const int64_t* sd = p.first ? p.sh0 : p.sfs;
+      const float* src = st_src;
+      const int64_t* sd = st_sd;
 #pragma unroll
       for (int r = 0; r < KT; ++r) st[r] = z4;
       if (src != nullptr) {
@@ -483,7 +542,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 #pragma unroll
         for (int r = 0; r < KT; ++r)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) st[r][i] = s0[key_of(r, i) * sd[2]];
+          for (int i = 0; i < 4; ++i) st[r][i] = s0[key_of(r, i) * sd[2]] * rsc.v;
       }
     }
     f16x8 sB[KB];
@@ -632,7 +691,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 #pragma unroll
     for (int r = 0; r < KT; ++r)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i];
+      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i] * rsc.fs;
   } else if (nloc == 0) {
     return;
   } else if (role == SR_OUT) {
@@ -659,7 +718,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         f32x4 pu = M::mma(pAs[mt], ul, z4);
         pu = M::mma(pLs[mt], uh, pu);
         pu = M::mma(pAs[mt], uh, pu);
-        ov[mt] = (pu + ebv[mt] * oq[mt]) * p.scale;
+        ov[mt] = (pu + ebv[mt] * oq[mt]) * rsc.o;
       }
       PS_END_B(ov[0], ov[1]);
       const int t0 = (p.c0 + it) * C;
@@ -802,12 +861,43 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     // Chunks 0 and 1 are published at the first barrier, and chunk it + 2
     // at iteration it's: the SCAN wave reads chunk it + 1's operands during
     // iteration it.
+    // bf16 inputs: once chunk it's copies have landed, its q, k and v
+    // tiles are converted to fp16 in place (v times the slice's range
+    // scale), before the barrier that publishes them; each lane converts
+    // whole 16-byte pieces, so the tiles' swizzle does not matter.
+    auto convert = [&](int it) __attribute__((always_inline)) {
+      if constexpr (std::is_same<TIn, bf16_t>::value) {
+        if (it >= nloc) return;
+        const int sl = it % R;
+        constexpr int NPQ = C * K / 8 / 64, NPV = C * BV / 8 / 64;
+        f16x8* const q8 = &s.rq[sl][0][0];
+        f16x8* const k8 = &s.rk[sl][0][0];
+        f16x8* const v8 = &s.rv[sl][0][0];
+        f16x8 xq[NPQ], xk[NPQ], xv[NPV];
+#pragma unroll
+        for (int i = 0; i < NPQ; ++i) {
+          xq[i] = q8[64 * i + lane];
+          xk[i] = k8[64 * i + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < NPV; ++i) xv[i] = v8[64 * i + lane];
+#pragma unroll
+        for (int i = 0; i < NPQ; ++i) {
+          q8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xq[i]));
+          k8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xk[i]));
+        }
+#pragma unroll
+        for (int i = 0; i < NPV; ++i) v8[64 * i + lane] = to_f16x8_sc<TIn>(__builtin_bit_cast(uint4, xv[i]), rsc.v);
+      }
+    };
     for (int it = 0; it < D; ++it)
       if (it < nloc) issue(it);
     if (nloc >= D)
       wait_vm<(D - 2) * ND>();
     else
       wait_vm<0>();
+    convert(0);
+    convert(1);
     wg_barrier();
     for (int it = 0; it < nloc; ++it) {
       if (it + D < nloc) {
@@ -816,6 +906,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       } else {
         wait_vm<0>();
       }
+      convert(it + 2);
       wg_barrier();
     }
   }
@@ -844,8 +935,10 @@ int launch_t(const SArgs& a, int K, int bv, int units, hipStream_t s) {
 
 }  // namespace s32
 
-bool scan32_supported(int dtype, int K, int C, int BV) {
-  return dtype == GDN_DTYPE_F16 && C == s32::C && (K == 64 || K == 128) && (BV == 16 || BV == 32);
+bool scan32_supported(int dtype, int K, int C, int BV, int V) {
+  if (dtype == GDN_DTYPE_BF16 && V / 16 > s32::kMaxVSlices) return false;
+  return (dtype == GDN_DTYPE_F16 || dtype == GDN_DTYPE_BF16) && C == s32::C && (K == 64 || K == 128) &&
+         (BV == 16 || BV == 32);
 }
 
 int64_t scan32_record_bytes() { return s32::REC_BYTES; }
@@ -886,6 +979,8 @@ int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t str
     int st;
     if (P.qkv_dtype == GDN_DTYPE_F16)
       st = s32::launch_t<f16>(a, P.K, bv, (int)units, stream);
+    else if (P.qkv_dtype == GDN_DTYPE_BF16)
+      st = s32::launch_t<bf16_t>(a, P.K, bv, (int)units, stream);
     else
       st = GDN_ERR_UNSUPPORTED;
     if (st != 0) return st;
