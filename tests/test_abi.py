@@ -112,7 +112,9 @@ def test_fwd_workspace_size(lib, pkg):
     assert size(T=0) == 0
     assert size(B=3, T=100, cu_seqlens=0x2000) == 3 * H * 4 * 3072
     assert size(flags=2) == 0                            # fused kernel forced: none
-    assert size(qkv_dtype=2) == 2 * H * 128 * 3072       # bf16: the same records
+    # bf16: the record, then the chunk's k rows in fp16
+    assert size(qkv_dtype=2) == 2 * H * 128 * (3072 + 32 * 128 * 2)
+    assert size(qkv_dtype=2, K=64) == 2 * H * 128 * (3072 + 32 * 64 * 2)
     assert size(qkv_dtype=2, V=2512) == 0                # bf16, V / 16 > 156: fused kernel, none
     assert size(qkv_dtype=0) == 0                        # fp32: phased kernel, none
     assert size(K=32) == 0 and size(K=256) == 0          # phased kernel, none

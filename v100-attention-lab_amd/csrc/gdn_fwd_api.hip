@@ -131,14 +131,14 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   // bf16 runs on the fused kernel (no workspace) when the static scratch
   // cannot hold its records
   if (scan32 && scratch_bytes > 0 && P.qkv_dtype == GDN_DTYPE_BF16 &&
-      (int64_t)P.B * P.H * scan32_record_bytes() > scratch_bytes)
+      (int64_t)P.B * P.H * scan32_record_bytes(P.qkv_dtype, P.K) > scratch_bytes)
     scan32 = false;
   // workspace: the caller's, or the static scratch array when it holds
   // what the path needs
   GdnFwdParams W = P;
   if (scratch_bytes > 0 && (c64 || scan32) && P.T > 0) {
     // one chunk per sequence and head (longer sequences run in segments)
-    const int64_t need = (int64_t)P.B * P.H * (c64 ? c64_record_bytes(P.K, P.qkv_dtype) : scan32_record_bytes());
+    const int64_t need = (int64_t)P.B * P.H * (c64 ? c64_record_bytes(P.K, P.qkv_dtype) : scan32_record_bytes(P.qkv_dtype, P.K));
     if (need > scratch_bytes) return GDN_ERR_SCRATCH_LIMIT;
     void* ptr = nullptr;
     const int st = scratch_address(&ptr);
@@ -155,7 +155,7 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   }
   if (scan32) {
     // segment length: as many chunks per sequence as the workspace holds
-    const int64_t per_chunk = (int64_t)P.B * P.H * scan32_record_bytes();
+    const int64_t per_chunk = (int64_t)P.B * P.H * scan32_record_bytes(P.qkv_dtype, P.K);
     const int64_t L = W.workspace_bytes / per_chunk;
     if (P.T > 0 && (reinterpret_cast<uintptr_t>(W.workspace) % 256 != 0 || L < 1)) return GDN_ERR_WORKSPACE;
     return scan32_launch(W, bv, (int)(L < 1 ? 1 : L < 0x7fffffff ? L : 0x7fffffff), s);
@@ -229,7 +229,7 @@ int64_t gdn_fwd_workspace_size(const GdnFwdParams* prm) {
   if (bv > 0 && P.V % bv == 0 && uses_scan32(P, bv)) {
     const int64_t nch = (P.T + 31) / 32;
     const int64_t L = nch < kSegChunks ? nch : kSegChunks;
-    const int64_t bytes = (int64_t)P.B * P.H * L * scan32_record_bytes();
+    const int64_t bytes = (int64_t)P.B * P.H * L * scan32_record_bytes(P.qkv_dtype, P.K);
     return (bytes + 255) / 256 * 256;
   }
   return 0;

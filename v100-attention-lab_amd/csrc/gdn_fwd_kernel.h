@@ -918,7 +918,7 @@ int c64_launch(const GdnFwdParams& P, int seg_chunks, hipStream_t stream);
 // then the scan (gdn_fwd_scan32.hip), in segments of at most seg_chunks
 // chunks per sequence whose records fit the caller's workspace.
 bool scan32_supported(int dtype, int K, int C, int BV, int V);
-int64_t scan32_record_bytes();
+int64_t scan32_record_bytes(int dtype, int K);  // per (chunk, head)
 int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t stream);
 
 }  // namespace gdn

@@ -62,6 +62,21 @@ constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
 constexpr int R_EBC = 2432; // float: e^{bC}
 constexpr int R_VMAX = 2448; // float [V / 16] (bf16 inputs): largest |v| of each 16-column slice of the rows
 constexpr int kMaxVSlices = (REC_BYTES - R_VMAX) / 4;
+// bf16 inputs: the record is followed by the chunk's k and q rows in fp16
+// (C x K each, in frag_piece order, rows past the end holding the last
+// row), which the scan copies instead of the inputs.
+template <typename TIn, int K>
+constexpr int rec_stride() {
+  return std::is_same<TIn, bf16_t>::value ? REC_BYTES + C * K * 2 : REC_BYTES;
+}
+constexpr int R_K16 = REC_BYTES;  // then q at R_K16 + C K 2
+// 16-byte piece c (columns 8 c ..) of row r of those copies, in the order
+// the record kernel's lanes hold them (lane (n, gq) of operand (mt, kb) is
+// row 16 mt + n, piece 4 kb + gq): each of its stores is 1 KB contiguous.
+template <int K>
+__device__ __forceinline__ int frag_piece(int r, int c) {
+  return ((((r >> 4) * (K / 32) + (c >> 2)) * 4 + (c & 3)) << 4) + (r & 15);
+}
 
 struct SArgs {
   const void* q;
@@ -205,6 +220,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   // the two records of this wave: geometry (wave-uniform)
   int nval[2];
   const char* kh[2];
+  const char* qh[2];
   const char* vh[2];
   char* rp[2];
   uint32_t skb[2];
@@ -213,6 +229,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
     const int r = (blockIdx.x * 4 + wave) * 2 + e;
     nval[e] = 0;
     kh[e] = nullptr;
+    qh[e] = nullptr;
     vh[e] = nullptr;
     rp[e] = nullptr;
     skb[e] = 0;
@@ -226,7 +243,8 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
         kh[e] = static_cast<const char*>(p.k) + (head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1]) * EB;
         skb[e] = (uint32_t)p.sk[1] * EB;
         vh[e] = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + (int64_t)t0 * p.sv[1]) * EB;
-        rp[e] = p.rec + (int64_t)r * REC_BYTES;
+        qh[e] = static_cast<const char*>(p.q) + (head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1]) * EB;
+        rp[e] = p.rec + (int64_t)r * rec_stride<TIn, K>();
       }
     }
   }
@@ -291,6 +309,16 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) kf[mt][kb] = to_f16x8<TIn>(kr[e][mt][kb]);
+      if constexpr (std::is_same<TIn, bf16_t>::value) {
+        // the k rows in fp16 after the record (lane (n, gq): rows 16 mt + n,
+        // columns 32 kb + 8 gq ..; rows past the end repeat the last row)
+        f16* const k16 = reinterpret_cast<f16*>(rp[e] + R_K16);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+            *reinterpret_cast<f16x8*>(k16 + 8 * frag_piece<K>(16 * mt + n, 4 * kb + gq)) = kf[mt][kb];
+      }
       float* sa = s_at[wave][e];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -484,7 +512,8 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   const char* qh = static_cast<const char*>(p.q) + head_base(rs, hi, p.sq) * EB;
   const char* kh = static_cast<const char*>(p.k) + head_base(rs, hi, p.sk) * EB;
   const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
-  const char* rech = p.rec + (int64_t)(bi * p.H + hi) * p.L * REC_BYTES;
+  constexpr int RS = rec_stride<TIn, K>();
+  const char* rech = p.rec + (int64_t)(bi * p.H + hi) * p.L * RS;
   // bf16: this slice's v and initial state scaled by a power of two into
   // fp16's range (from their absolute maximum over the whole sequence), o
   // and the final state scaled back; identity for fp16
@@ -499,7 +528,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     uint32_t m = state_absmax_bits(st_src ? st_src + bi * st_sd[0] + hi * st_sd[1] + v0 * st_sd[3] : nullptr,
                                    st_sd[2], st_sd[3], K, BV);
     for (int i = tid; i < nloc * NSW; i += 64 * scan_waves<BV>()) {
-      const float* vm = reinterpret_cast<const float*>(rech + (int64_t)(i / NSW) * REC_BYTES + R_VMAX);
+      const float* vm = reinterpret_cast<const float*>(rech + (int64_t)(i / NSW) * RS + R_VMAX);
       m = max(m, __float_as_uint(vm[v0 / 16 + i % NSW]));
     }
     rsc = range_scale_of(__uint_as_float(block_max_bits(m, red)), p.scale);
@@ -837,16 +866,30 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       const int j = p.c0 + it;
       const int row0 = j * C;
       const int last = T - 1 - row0;          // rows > last re-read row last
-      const char* qb = qh + (int64_t)row0 * sqb;
-      const char* kb = kh + (int64_t)row0 * skb;
       const char* vb = vh + (int64_t)row0 * svb;
       const int sl = it % R;
+      if constexpr (std::is_same<TIn, bf16_t>::value) {
+        // q and k from the record's fp16 copies (rows past the end already
+        // repeat the last row)
+        const char* const kb = rech + (int64_t)it * RS + R_K16;
+        const char* qb = qh + (int64_t)row0 * sqb;
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) {
-        const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
-        const uint32_t rr = (uint32_t)min(r, last);
-        dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
-        dma16(kb + rr * skb + cc * 16, &s.rk[sl][0][0] + 64 * i);
+        for (int i = 0; i < NQ; ++i) {
+          const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
+          const uint32_t rr = (uint32_t)min(r, last);
+          dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
+          dma16(kb + 16 * frag_piece<K>(r, cc), &s.rk[sl][0][0] + 64 * i);
+        }
+      } else {
+        const char* qb = qh + (int64_t)row0 * sqb;
+        const char* kb = kh + (int64_t)row0 * skb;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+          const int pc = 64 * i + lane, r = pc / RCH, cc = swz<K>(r, pc % RCH);  // swz is an involution
+          const uint32_t rr = (uint32_t)min(r, last);
+          dma16(qb + rr * sqb + cc * 16, &s.rq[sl][0][0] + 64 * i);
+          dma16(kb + rr * skb + cc * 16, &s.rk[sl][0][0] + 64 * i);
+        }
       }
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
@@ -854,38 +897,30 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         const uint32_t rr = (uint32_t)min(r, last);
         dma16(vb + rr * svb + cc * 16, &s.rv[sl][0][0] + 64 * i);
       }
-      const char* rsrc = rech + (int64_t)it * REC_BYTES;
+      const char* rsrc = rech + (int64_t)it * RS;
 #pragma unroll
       for (int i = 0; i < REC_BYTES / 1024; ++i) dma16(rsrc + 1024 * i + 16 * lane, s.rec[it % RR] + 1024 * i);
     };
     // Chunks 0 and 1 are published at the first barrier, and chunk it + 2
     // at iteration it's: the SCAN wave reads chunk it + 1's operands during
     // iteration it.
-    // bf16 inputs: once chunk it's copies have landed, its q, k and v
-    // tiles are converted to fp16 in place (v times the slice's range
-    // scale), before the barrier that publishes them; each lane converts
-    // whole 16-byte pieces, so the tiles' swizzle does not matter.
+    // bf16 inputs: once chunk it's copies have landed, its v tile is
+    // converted to fp16 in place (times the slice's range scale), before
+    // the barrier that publishes it (q and k arrive in fp16 from the
+    // record).
     auto convert = [&](int it) __attribute__((always_inline)) {
       if constexpr (std::is_same<TIn, bf16_t>::value) {
         if (it >= nloc) return;
-        const int sl = it % R;
         constexpr int NPQ = C * K / 8 / 64, NPV = C * BV / 8 / 64;
-        f16x8* const q8 = &s.rq[sl][0][0];
-        f16x8* const k8 = &s.rk[sl][0][0];
-        f16x8* const v8 = &s.rv[sl][0][0];
-        f16x8 xq[NPQ], xk[NPQ], xv[NPV];
+        f16x8* const q8 = &s.rq[it % R][0][0];
+        f16x8* const v8 = &s.rv[it % R][0][0];
+        f16x8 xq[NPQ], xv[NPV];
 #pragma unroll
-        for (int i = 0; i < NPQ; ++i) {
-          xq[i] = q8[64 * i + lane];
-          xk[i] = k8[64 * i + lane];
-        }
+        for (int i = 0; i < NPQ; ++i) xq[i] = q8[64 * i + lane];
 #pragma unroll
         for (int i = 0; i < NPV; ++i) xv[i] = v8[64 * i + lane];
 #pragma unroll
-        for (int i = 0; i < NPQ; ++i) {
-          q8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xq[i]));
-          k8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xk[i]));
-        }
+        for (int i = 0; i < NPQ; ++i) q8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xq[i]));
 #pragma unroll
         for (int i = 0; i < NPV; ++i) v8[64 * i + lane] = to_f16x8_sc<TIn>(__builtin_bit_cast(uint4, xv[i]), rsc.v);
       }
@@ -941,7 +976,10 @@ bool scan32_supported(int dtype, int K, int C, int BV, int V) {
          (BV == 16 || BV == 32);
 }
 
-int64_t scan32_record_bytes() { return s32::REC_BYTES; }
+int64_t scan32_record_bytes(int dtype, int K) {
+  if (dtype != GDN_DTYPE_BF16) return s32::REC_BYTES;
+  return K == 64 ? s32::rec_stride<bf16_t, 64>() : s32::rec_stride<bf16_t, 128>();
+}
 
 // Enqueues the segments of one call: for each, the records then the scan
 // (arguments checked by the caller; seg_chunks >= 1).
