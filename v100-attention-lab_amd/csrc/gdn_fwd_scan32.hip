@@ -537,16 +537,12 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
   auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int cc) { return tile[r][swz<K>(r, cc)]; };
 
   // Waves w and w + 4 share SIMD w % 4.  At BV = 32 (six waves) the SCAN
-  // waves take waves 2 and 3, alone on their SIMDs.  For fp16 the OUT waves
-  // share theirs with PQK and LOAD; for bf16, whose LOAD wave also converts
-  // the staged tiles, the two OUT waves share one SIMD and PQK and LOAD the
-  // other.
+  // waves take waves 2 and 3, alone on their SIMDs, and the OUT waves share
+  // theirs with PQK and LOAD.
   int role, ridx;
   if constexpr (NSW == 2) {
-    constexpr bool pair_out = std::is_same<TIn, bf16_t>::value;
-    constexpr int roles[6] = {SR_OUT, pair_out ? SR_PQK : SR_OUT, SR_SCAN, SR_SCAN,
-                              pair_out ? SR_OUT : SR_PQK, SR_LOAD};
-    constexpr int idx[6] = {0, pair_out ? 0 : 1, 0, 1, pair_out ? 1 : 0, 0};
+    constexpr int roles[6] = {SR_OUT, SR_OUT, SR_SCAN, SR_SCAN, SR_PQK, SR_LOAD};
+    constexpr int idx[6] = {0, 1, 0, 1, 0, 0};
     role = roles[wave];
     ridx = idx[wave];
   } else {
