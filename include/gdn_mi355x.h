@@ -148,9 +148,9 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  * library's load to the end of the process.
  *   - 32-row chunks (fp16, bf16): the sequence runs in segments of as many
  *     chunks as the array holds (B * H records per chunk, of 3 KB for fp16
- *     and 3 KB + 4 C K bytes for bf16, which also carry the chunk's q and k
- *     rows in fp16); if one chunk per sequence does not fit (fp16:
- *     B * H > 10922; bf16 at K = 128: B * H > 1724), bf16 runs on the fused
+ *     and 3 KB + 2 C K bytes for bf16, which also carry the chunk's k rows
+ *     in fp16); if one chunk per sequence does not fit (fp16:
+ *     B * H > 10922; bf16 at K = 128: B * H > 2978), bf16 runs on the fused
  *     kernel and fp16 fails with GDN_ERR_SCRATCH_LIMIT.
  *   - 64-row chunks: likewise in segments (records of 33 KB per chunk and
  *     head for 16-bit inputs, 66 KB for fp32 at K = 128); GDN_ERR_SCRATCH_LIMIT

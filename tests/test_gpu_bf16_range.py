@@ -6,8 +6,8 @@ magnitude and scales o and final_state back, which is exact because o and
 the state are jointly linear in (v, h0) and every state column evolves on
 its own.  These cases would overflow fp16 (|v| up to 1e5 > 65504) or sink
 into its subnormals (|v| ~ 1e-6) without it.  Every forward kernel that
-takes bf16 is covered (the fused pipelined kernel at C = 32, the record +
-scan launches at C = 64, the phase-by-phase kernel), against the fp64 step
+takes bf16 is covered (the record + scan launches at C = 32 and C = 64, the
+fused pipelined kernel at C = 32, the phase-by-phase kernel), against the fp64 step
 recurrence at the north star's 1e-3 (max-norm relative error,
 bench_gdn.py:89-94), with fp32-stored outputs.
 """
@@ -22,7 +22,8 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 CASES = [  # (name, chunk, kernel, K)
-    ("pipelined C=32", 32, "auto", 128),
+    ("records + scan C=32", 32, "auto", 128),
+    ("pipelined C=32", 32, "fused", 128),
     ("two-launch C=64", 64, "auto", 64),
     ("phased C=32", 32, "phased", 64),
 ]
@@ -77,16 +78,17 @@ def test_bf16_per_head_scales(pkg, cuda, case):
     _check(pkg, cuda, f"{name} heads 1e-6..1e5", q, k, v, g, beta, h0, chunk, kernel, per_head=True)
 
 
-def test_bf16_in_range_unchanged(pkg, cuda):
+@pytest.mark.parametrize("kernel", ["auto", "fused"])
+def test_bf16_in_range_unchanged(pkg, cuda, kernel):
     """Inside [2^-6, 2^10] the shift is zero, and bf16 values are exact in
-    fp16: the fused kernel on bf16 inputs then gives the bits it gives on the
-    same values in fp16."""
+    fp16: the record + scan launches and the fused kernel on bf16 inputs
+    then give the bits they give on the same values in fp16."""
     q, k, v, g, beta, h0 = _inputs(1, 200, 2, 128, 32, 97, 1.0, 1.0)
     d = lambda t: t.to(cuda)
-    o_b, f_b = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), kernel="fused",
+    o_b, f_b = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), kernel=kernel,
                            output_dtype=torch.float32)
     h = lambda t: d(t.to(torch.float16))
-    o_h, f_h = pkg.gdn_fwd(h(q), h(k), h(v), d(g), d(beta), d(h0), kernel="fused",
+    o_h, f_h = pkg.gdn_fwd(h(q), h(k), h(v), d(g), d(beta), d(h0), kernel=kernel,
                            output_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(o_b.cpu(), o_h.cpu()) and torch.equal(f_b.cpu(), f_h.cpu())

@@ -18,9 +18,9 @@ pytestmark = pytest.mark.gpu
 TOL_F32 = 1e-5
 TOL_LOWP = 1e-3
 
-# "auto": for fp16 at C = 32 the per-chunk records and the scan (two
-# launches), for bf16 the fused pipelined kernel; "fused": the pipelined
-# kernel for both; "phased": the phase-by-phase kernel.
+# "auto": for fp16 and bf16 at C = 32 the per-chunk records and the scan
+# (two launches); "fused": the pipelined kernel for both; "phased": the
+# phase-by-phase kernel.
 KERNELS = ["auto", "fused", "phased"]
 
 

@@ -282,10 +282,10 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
       block_v: V columns per workgroup (16, 32, 64); None picks one.
       output_dtype: dtype of ``o``; defaults to ``q.dtype`` (as the
         reference, gdn_triton.py:126).
-      kernel: ``"auto"`` picks per shape: for fp16 with chunk 32 and K in
-        {64, 128}, per-chunk records then the scan (two launches per
-        segment, a workspace of records); for bf16 there, the single fused
-        pipelined kernel; the phase-by-phase kernel elsewhere.  ``"fused"``
+      kernel: ``"auto"`` picks per shape: for fp16 or bf16 with chunk 32
+        and K in {64, 128}, per-chunk records then the scan (two launches
+        per segment, a workspace of records; bf16 records also carry the
+        chunk's k rows in fp16); the phase-by-phase kernel elsewhere.  ``"fused"``
         forces the fused pipelined kernel (no workspace) where it applies,
         ``"phased"`` the phase-by-phase kernel.
       cu_seqlens: optional int64 ``[N + 1]`` row offsets: N sequences
