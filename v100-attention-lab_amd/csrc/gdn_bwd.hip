@@ -802,30 +802,44 @@ using tiles16::frag8;
 using tiles16::frag8_t;
 using tiles16::store_pair4;
 
+// A chunk's inputs of the forward walk in LDS.
 template <int K>
-struct alignas(16) FMem {
-  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
+struct alignas(16) FIn {
   f16 k[C][K + HP];
   f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
   f16 vt[BV][C + HP];                  // V^T of the slice
-  f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
-  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
   // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
   // (rows 4 .. 7 repeat them)
+  float gv[NTP / C][C];
+};
+
+// The walks' inputs are double-buffered: chunk c in in[c & 1], so that the
+// next chunk's are staged during the state update, three barriers a chunk.
+template <int K>
+struct alignas(16) FMem {
+  f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
+  f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
+  f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
+  FIn<K> in[2];
+};
+
+// A chunk's inputs of the backward walk in LDS.
+template <int K>
+struct alignas(16) RIn {
+  f16 q[C][K + HP], k[C][K + HP];
+  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
+  f16 ph[C][C + HP], pl[C][C + HP];    // P
+  f16 dot[BV][C + HP];                 // dO^T of the slice
   float gv[NTP / C][C];
 };
 
 template <int K>
 struct alignas(16) RMem {
   f16 sh[BV][K + HP], sl[BV][K + HP];  // dS'^T
-  f16 q[C][K + HP], k[C][K + HP];
-  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
-  f16 ph[C][C + HP], pl[C][C + HP];    // P
-  f16 dot[BV][C + HP];                 // dO^T of the slice
   f16 gh[BV][C + HP], gl[BV][C + HP];  // (diag(gam) dO)^T
   f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
   f16 zh[BV][C + HP], zl[BV][C + HP];  // (diag(gam) (T diag(beta))^T du)^T
-  float gv[NTP / C][C];
+  RIn<K> in[2];
 };
 
 template <int K>
@@ -897,7 +911,7 @@ struct FNext16 {
     v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
   }
-  __device__ __forceinline__ void store(FMem<K>& s, int tid, float vsc) const {
+  __device__ __forceinline__ void store(FIn<K>& s, int tid, float vsc) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
     k.store(tid, s.k);
@@ -930,11 +944,12 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
   FNext16<TIn, K> nx;
   if (nch > 0) {
     nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
-    nx.store(s, tid, rsc.v);
+    nx.store(s.in[0], tid, rsc.v);
   }
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
     const int64_t ri = (slot0 + c) * p.H + hi;
+    FIn<K>& in = s.in[c & 1];
     // the next chunk's inputs (the last chunk's again at the end: every load
     // is then consumed by the staging below, on every path)
     const int cn = min(c + 1, nch - 1);
@@ -946,14 +961,14 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       f32x4 ak = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 kf = frag8(&s.k[um0 + r][kb + 8 * kq]);
+        const f16x8 kf = frag8(&in.k[um0 + r][kb + 8 * kq]);
         ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), ak, 0, 0, 0);
         ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), ak, 0, 0, 0);
       }
       const int t = um0 + 4 * kq;
-      const f16x4 vv = *reinterpret_cast<const f16x4*>(&s.vt[r][t]);
-      const float y[4] = {(float)vv[0] - s.gv[1][t] * ak[0], (float)vv[1] - s.gv[1][t + 1] * ak[1],
-                          (float)vv[2] - s.gv[1][t + 2] * ak[2], (float)vv[3] - s.gv[1][t + 3] * ak[3]};
+      const f16x4 vv = *reinterpret_cast<const f16x4*>(&in.vt[r][t]);
+      const float y[4] = {(float)vv[0] - in.gv[1][t] * ak[0], (float)vv[1] - in.gv[1][t + 1] * ak[1],
+                          (float)vv[2] - in.gv[1][t + 2] * ak[2], (float)vv[3] - in.gv[1][t + 3] * ak[3]};
       store_pair4(&s.yh[r][t], &s.yl[r][t], y);
     }
     __syncthreads();
@@ -961,16 +976,16 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       // u = T diag(beta) Y, rows 16 w .. (W S = T diag(beta) diag(gam) K S)
       const int um0 = 16 * wave;
       f32x4 au = {0.f, 0.f, 0.f, 0.f};
-      const f16x8 th = frag8(&s.th[um0 + r][8 * kq]), yh = frag8(&s.yh[r][8 * kq]);
+      const f16x8 th = frag8(&in.th[um0 + r][8 * kq]), yh = frag8(&s.yh[r][8 * kq]);
       au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, yh, au, 0, 0, 0);
       au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8(&s.yl[r][8 * kq]), au, 0, 0, 0);
-      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&s.tl[um0 + r][8 * kq]), yh, au, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&in.tl[um0 + r][8 * kq]), yh, au, 0, 0, 0);
       const int t = um0 + 4 * kq;
       float du[4];
       float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        du[i] = s.gv[2][t + i] * au[i];
+        du[i] = in.gv[2][t + i] * au[i];
         uo[(int64_t)(t + i) * p.V + r] = au[i] * rsc.fs;
       }
       store_pair4(&s.dh[r][t], &s.dl[r][t], du);
@@ -981,17 +996,16 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     for (int j = 0; j < State<K>::NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        const f16x8 kt = frag8_t(s.k, 0, m0, r, kq);
+        const f16x8 kt = frag8_t(in.k, 0, m0, r, kq);
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
         a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][8 * kq]), a, 0, 0, 0);
         a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][8 * kq]), a, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S.st[j][i] = s.gv[3][0] * S.st[j][i] + a[i];
+        for (int i = 0; i < 4; ++i) S.st[j][i] = in.gv[3][0] * S.st[j][i] + a[i];
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-      __syncthreads();
-    nx.store(s, tid, rsc.v);
+    nx.store(s.in[(c + 1) & 1], tid, rsc.v);
     __syncthreads();
   }
 }
@@ -1016,7 +1030,7 @@ struct RNext16 {
     d.load(tid, dg + (int64_t)t0 * p.sdo[1], p.sdo[1], nval);
     gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
   }
-  __device__ __forceinline__ void store(RMem<K>& s, int tid, float dsc) const {
+  __device__ __forceinline__ void store(RIn<K>& s, int tid, float dsc) const {
     th.store(tid, s.th);
     tl.store(tid, s.tl);
     ph.store(tid, s.ph);
@@ -1055,11 +1069,12 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
   if (nch > 0) {
     const int t0 = (nch - 1) * C;
     nx.load(p, tid, (slot0 + nch - 1) * p.H + hi, qg, kg, dg, t0, rs.T - t0);
-    nx.store(s, tid, rsd.v);
+    nx.store(s.in[(nch - 1) & 1], tid, rsd.v);
   }
   __syncthreads();
   for (int c = nch - 1; c >= 0; --c) {
     const int64_t ri = (slot0 + c) * p.H + hi;
+    RIn<K>& in = s.in[c & 1];
     // the previous chunk's inputs (chunk 0's again at the end)
     const int cn = max(c - 1, 0);
     nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
@@ -1068,12 +1083,12 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
-      const f16x8 df = frag8(&s.dot[r][8 * kq]);
-      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(s.ph, 0, um0, r, kq), df, a1, 0, 0, 0);
-      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(s.pl, 0, um0, r, kq), df, a1, 0, 0, 0);
+      const f16x8 df = frag8(&in.dot[r][8 * kq]);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(in.ph, 0, um0, r, kq), df, a1, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(in.pl, 0, um0, r, kq), df, a1, 0, 0, 0);
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 kf = frag8(&s.k[um0 + r][kb + 8 * kq]);
+        const f16x8 kf = frag8(&in.k[um0 + r][kb + 8 * kq]);
         a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), a2, 0, 0, 0);
         a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), a2, 0, 0, 0);
       }
@@ -1082,16 +1097,16 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       float* const duo = p.du + ri * (int64_t)C * p.V + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        du[i] = scale * a1[i] + s.gv[2][t + i] * a2[i];
+        du[i] = scale * a1[i] + in.gv[2][t + i] * a2[i];
         duo[(int64_t)(t + i) * p.V + r] = du[i] * rsd.fs;
       }
       store_pair4(&s.uh[r][t], &s.ul[r][t], du);
     } else {
       // (diag(gam) dO)^T as pairs: lane -> column tid % 16, rows 4 (tid / 16) ..
       const int l = tid - 128, col = l & 15, t4 = 4 * (l >> 4);
-      const f16x4 dv = *reinterpret_cast<const f16x4*>(&s.dot[col][t4]);
-      const float x[4] = {s.gv[1][t4] * (float)dv[0], s.gv[1][t4 + 1] * (float)dv[1],
-                          s.gv[1][t4 + 2] * (float)dv[2], s.gv[1][t4 + 3] * (float)dv[3]};
+      const f16x4 dv = *reinterpret_cast<const f16x4*>(&in.dot[col][t4]);
+      const float x[4] = {in.gv[1][t4] * (float)dv[0], in.gv[1][t4 + 1] * (float)dv[1],
+                          in.gv[1][t4 + 2] * (float)dv[2], in.gv[1][t4 + 3] * (float)dv[3]};
       store_pair4(&s.gh[col][t4], &s.gl[col][t4], x);
     }
     __syncthreads();
@@ -1105,7 +1120,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
         const int m0 = 16 * (wave + 4 * j);
         aq[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (m0 < K) {
-          const f16x8 qt = frag8_t(s.q, 0, m0, r, kq);
+          const f16x8 qt = frag8_t(in.q, 0, m0, r, kq);
           aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gh[r][8 * kq]), aq[j], 0, 0, 0);
           aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gl[r][8 * kq]), aq[j], 0, 0, 0);
         }
@@ -1113,15 +1128,15 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     };
     if (wave < 2) {
       const int um0 = 16 * wave;
-      const f16x8 tth = frag8_t(s.th, 0, um0, r, kq), ttl = frag8_t(s.tl, 0, um0, r, kq);
+      const f16x8 tth = frag8_t(in.th, 0, um0, r, kq), ttl = frag8_t(in.tl, 0, um0, r, kq);
       const f16x8 uh = frag8(&s.uh[r][8 * kq]);
       f32x4 az = {0.f, 0.f, 0.f, 0.f};
       az = __builtin_amdgcn_mfma_f32_16x16x32_f16(tth, uh, az, 0, 0, 0);
       az = __builtin_amdgcn_mfma_f32_16x16x32_f16(tth, frag8(&s.ul[r][8 * kq]), az, 0, 0, 0);
       az = __builtin_amdgcn_mfma_f32_16x16x32_f16(ttl, uh, az, 0, 0, 0);
       const int t = um0 + 4 * kq;
-      const float z[4] = {s.gv[1][t] * az[0], s.gv[1][t + 1] * az[1], s.gv[1][t + 2] * az[2],
-                          s.gv[1][t + 3] * az[3]};
+      const float z[4] = {in.gv[1][t] * az[0], in.gv[1][t + 1] * az[1], in.gv[1][t + 2] * az[2],
+                          in.gv[1][t + 3] * az[3]};
       store_pair4(&s.zh[r][t], &s.zl[r][t], z);
     } else {
       q_term();
@@ -1133,17 +1148,16 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     for (int j = 0; j < State<K>::NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        const f16x8 kt = frag8_t(s.k, 0, m0, r, kq);
+        const f16x8 kt = frag8_t(in.k, 0, m0, r, kq);
         f32x4 b = {0.f, 0.f, 0.f, 0.f};
         b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zh[r][8 * kq]), b, 0, 0, 0);
         b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zl[r][8 * kq]), b, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S.st[j][i] = scale * aq[j][i] + s.gv[3][0] * S.st[j][i] - b[i];
+        for (int i = 0; i < 4; ++i) S.st[j][i] = scale * aq[j][i] + in.gv[3][0] * S.st[j][i] - b[i];
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-      __syncthreads();
-    nx.store(s, tid, rsd.v);
+    nx.store(s.in[(c + 1) & 1], tid, rsd.v);
     __syncthreads();
   }
   if (p.dh0 != nullptr) {
