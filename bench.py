@@ -239,18 +239,23 @@ def cpu_baseline(B, T, H, K, V, dtype, C, budget_s=12.0):
     }
 
 
+# The sources the 32-row forward's two launches are built from (the record
+# and scan kernels, the headers they include, the dispatch that launches
+# them): the code a forward traffic profile measures.
+FWD_SOURCES = ("gdn_fwd_api.hip", "gdn_fwd_kernel.h", "gdn_fwd_pipe.h", "gdn_fwd_scan32.hip")
+
+
 def sources_digest():
-    """sha256 (first 16 hex digits) over the library's HIP sources, names and
-    bytes: it identifies the build a traffic profile was measured on, also on
-    a machine without the git history."""
+    """sha256 (first 16 hex digits) over the forward's HIP sources
+    (FWD_SOURCES), names and bytes: it identifies the build a traffic profile
+    was measured on, also on a machine without the git history."""
     import hashlib
     d = os.path.join(REPO, "v100-attention-lab_amd", "csrc")
     h = hashlib.sha256()
-    for name in sorted(os.listdir(d)):
-        if name.endswith((".hip", ".h")):
-            h.update(name.encode())
-            with open(os.path.join(d, name), "rb") as f:
-                h.update(f.read())
+    for name in FWD_SOURCES:
+        h.update(name.encode())
+        with open(os.path.join(d, name), "rb") as f:
+            h.update(f.read())
     return h.hexdigest()[:16]
 
 

@@ -94,6 +94,9 @@ CASES = [
     (1, 200, 2, 128, 48, torch.bfloat16, 64),
     (2, 333, 4, 128, 128, torch.bfloat16, 32),
     (1, 600, 512, 64, 32, torch.float16, 64),
+    # bf16 records carry the chunk's k rows in fp16 (11 KB per chunk and
+    # head at K = 128): 1024 heads run 7 chunks in 4 segments of 2
+    (2, 200, 512, 128, 64, torch.bfloat16, 32),
 ]
 
 
@@ -122,4 +125,25 @@ def test_noalloc_against_oracle(pkg, cuda):
     (_, _), (o, fs) = _both(pkg, cuda, B, T, H, K, V, torch.float16, 32, seed=71)
     o_ref, h_ref = ref.recurrent(q, k, v, beta, g, ref.to_vk(h0), dtype=torch.float64)
     assert ref.rel_err(0.8 * o_ref, o.float().cpu()) <= 1e-3
+    assert ref.rel_err(ref.to_kv(h_ref), fs.cpu()) <= 1e-3
+
+
+def test_noalloc_bf16_beyond_scratch_runs_fused(pkg, cuda):
+    """bf16 at 32-row chunks whose records do not fit the scratch array even
+    one chunk per sequence-head (3000 heads x 11 KB > 32 MiB) run on the
+    fused kernel instead of failing: checked against the fp64 recurrence."""
+    B, T, H, K, V = 1, 40, 3000, 128, 16
+    q, k, v, g, beta, h0 = _inputs(cuda, B, T, H, K, V, torch.bfloat16, 81)
+    L = pkg._lib
+    lib = L.load_library()
+    o = torch.full((B, T, H, V), float("nan"), dtype=torch.float32, device=cuda)
+    fs = torch.full((B, H, K, V), float("nan"), dtype=torch.float32, device=cuda)
+    P = _params(L, q, k, v, g, beta, h0, o, fs, 32)
+    print(f"[no_alloc] bf16 B={B} T={T} H={H} beyond the scratch array", flush=True)
+    rc = lib.gdn_fwd_launch_noalloc(ctypes.byref(P), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, L.status_string(rc)
+    qc, kc, vc, gc, bc, hc = (t.cpu() for t in (q, k, v, g, beta, h0))
+    o_ref, h_ref = ref.recurrent(qc, kc, vc, bc, gc, ref.to_vk(hc), dtype=torch.float64)
+    assert ref.rel_err(0.8 * o_ref, o.cpu()) <= 1e-3
     assert ref.rel_err(ref.to_kv(h_ref), fs.cpu()) <= 1e-3
