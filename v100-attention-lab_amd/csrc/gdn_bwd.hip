@@ -799,38 +799,201 @@ namespace w16 {
 
 using tiles16::HP;
 using tiles16::frag8;
-using tiles16::frag8_t;
+using tiles16::frag4_t;
 using tiles16::store_pair4;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// A chunk's inputs reach LDS by LDS-DMA: global_load_lds_dwordx4 (_dword)
+// copies 16 (4) bytes a lane from global memory to LDS at M0 + 16 (4) lane,
+// complete once the issuing wave's vmcnt has drained.  The walks' barriers
+// wait for LDS accesses only, so copies issued in a chunk's first phase stay
+// in flight across its other two; the issuing waves drain them before the
+// chunk's last barrier.  The copies are written as inline assembly: the
+// compiler then sees no LDS write in flight and adds no vmcnt wait before
+// the transposing LDS reads (which it cannot tell apart from the copies'
+// targets).  M0 is written here and nowhere else in these kernels.
+// LDS address of a generic pointer into LDS: its low 32 bits (the LDS
+// aperture sits in the high half)
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds_base))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds_base))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ f16x4 read_tr4(const f16* a) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a));
+}
+
+// Rows of W halves (W = 32, 64, 128) unpadded in LDS, each row's 16-byte
+// pieces permuted: piece s of row t sits at s ^ swz<W>(t).  The 16 rows that
+// a row read (frag8, 16-lane passes) takes at one piece, and the 8 rows x 2
+// pieces of a pass of a transposing read (frag8_ts, 32-lane passes), then
+// use every bank once.
+template <int W>
+__device__ __forceinline__ int swz(int t) {
+  if constexpr (W == 128) return (((t >> 3) & 1) << 3) | ((t & 3) << 1) | ((t >> 2) & 1);
+  else if constexpr (W == 64) return (((t >> 3) & 1) << 2) | (((t >> 1) & 1) << 1) | ((t >> 2) & 1);
+  else {
+    static_assert(W == 32, "rows of 32, 64 or 128 halves");
+    return (((t >> 3) & 1) << 1) | ((t >> 2) & 1);
+  }
+}
+// offset in halves of element (t, col)
+template <int W>
+__device__ __forceinline__ int soff(int t, int col) {
+  return t * W + ((((col >> 3) ^ swz<W>(t))) << 3) + (col & 7);
+}
+// halves col .. col + 7 of row t
+template <int W>
+__device__ __forceinline__ f16x8 frag8_s(const f16* x, int t, int col) {
+  return frag8(x + soff<W>(t, col));
+}
+// Row m0 + r of X^T, contraction indices t0 + 8 kq .. + 7, by two
+// ds_read_b64_tr_b16 (lane layout as tiles16::frag8_t)
+template <int W>
+__device__ __forceinline__ f16x8 frag8_ts(const f16* x, int t0, int m0, int r, int kq) {
+  const int t = t0 + 8 * kq + (r >> 2), col = m0 + 4 * (r & 3);
+  const f16x4 lo = read_tr4(x + soff<W>(t, col)), hi = read_tr4(x + soff<W>(t + 4, col));
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// dO rows of a slice (BV halves) in LDS: row t at row dperm(t), bits 2 and
+// 3 of t swapped, so that the rows of a 32-lane pass of a transposing read
+// (t = 0..3 and 8..11, + 4 h) fill 256 contiguous bytes.
+__device__ __forceinline__ int dperm(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+// lane (r, kq) receives dO[8 kq + j][r], j = 0..7: row r of dO^T
+__device__ __forceinline__ f16x8 dot_frag8(const f16* x, int r, int kq) {
+  const int t = 8 * kq + (r >> 2), col = 4 * (r & 3);
+  const f16x4 lo = read_tr4(x + dperm(t) * BV + col), hi = read_tr4(x + dperm(t + 4) * BV + col);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Rows t0 .. t0 + C - 1 of a row-major 16-bit input (rows ld elements apart,
+// row starts 16-byte aligned; rows >= nval read row nval - 1) -> rows of W
+// halves swizzled by swz<W>.  The tile's C W / 512 copies (16 bytes a lane)
+// are shared round robin by NW waves (this one: lw).
+template <int W, int NW>
+__device__ __forceinline__ void dma_rows(const uint16_t* src, int64_t ld, int nval, f16* dst, int lw, int lane) {
+  constexpr int NJ = C * W / 512;
+  static_assert(NJ % NW == 0, "whole copies per wave");
+#pragma unroll
+  for (int jj = 0; jj < NJ / NW; ++jj) {
+    const int j = NW * jj + lw;
+    const int pos = 512 * j + 8 * lane;  // halves
+    const int t = pos / W, pc = (pos % W) / 8;
+    dma16(src + min(t, nval - 1) * ld + 8 * (pc ^ swz<W>(t)), dst + 512 * j);
+  }
+}
+// Once a wave's copies of dma_rows have landed: bf16 -> fp16, rows >= nval
+// -> zero, each lane on the pieces it copied itself.
+template <typename TIn, int W, int NW>
+__device__ __forceinline__ void fix_rows(f16* dst, int nval, int lw, int lane) {
+  constexpr int NJ = C * W / 512;
+#pragma unroll
+  for (int jj = 0; jj < NJ / NW; ++jj) {
+    const int pos = 512 * (NW * jj + lw) + 8 * lane;
+    f16x8* const a = reinterpret_cast<f16x8*>(dst + pos);
+    if (pos / W >= nval) {
+      *a = f16x8{};
+    } else if constexpr (!std::is_same<TIn, f16>::value) {
+      f16 x[8];
+      InTraits<TIn>::to_op(*reinterpret_cast<const uint4*>(a), x);
+      *a = f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+    }
+  }
+}
+
+// Rows t0 .. t0 + C - 1 of a BV-column slice of dO (rows ld elements apart,
+// 4-byte aligned; rows >= nval read row nval - 1) -> rows at dperm(t): 4
+// bytes a lane, C BV / 128 copies alternating between the loader waves.
+__device__ __forceinline__ void dma_dot(const uint16_t* src, int64_t ld, int nval, f16* dst, int lw, int lane) {
+  constexpr int NJ = C * BV / 128;
+#pragma unroll
+  for (int jj = 0; jj < NJ / 2; ++jj) {
+    const int j = 2 * jj + lw;
+    const int pos = 128 * j + 2 * lane;
+    dma4(src + min(dperm(pos / BV), nval - 1) * ld + pos % BV, dst + 128 * j);
+  }
+}
+// bf16 values times sc (a power of two: exact) -> fp16, rows >= nval -> zero
+template <typename TIn>
+__device__ __forceinline__ void fix_dot(f16* dst, int nval, float sc, int lw, int lane) {
+  constexpr int NJ = C * BV / 128;
+#pragma unroll
+  for (int jj = 0; jj < NJ / 2; ++jj) {
+    const int pos = 128 * (2 * jj + lw) + 2 * lane;
+    uint32_t* const a = reinterpret_cast<uint32_t*>(dst + pos);
+    if (dperm(pos / BV) >= nval) {
+      *a = 0u;
+    } else if constexpr (!std::is_same<TIn, f16>::value) {
+      const uint32_t w = *a;
+      const f16 lo = (f16)(bf16_bits_to_float(w & 0xffffu) * sc), hi = (f16)(bf16_bits_to_float(w >> 16) * sc);
+      *a = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+  }
+}
+
+// Rows t0 .. t0 + C - 1 of a BV-column slice of v (16-byte aligned rows, as
+// q, k, v are) -> rows of BV halves in order: one copy, 16 bytes a lane.
+__device__ __forceinline__ void dma_v(const uint16_t* src, int64_t ld, int nval, f16* dst, int lane) {
+  static_assert(C * BV == 512, "one copy");
+  const int pos = 8 * lane;
+  dma16(src + min(pos / BV, nval - 1) * ld + pos % BV, dst);
+}
+template <typename TIn>
+__device__ __forceinline__ void fix_v(f16* dst, int nval, float sc, int lane) {
+  const int pos = 8 * lane;
+  f16x8* const a = reinterpret_cast<f16x8*>(dst + pos);
+  if (pos / BV >= nval) {
+    *a = f16x8{};
+  } else if constexpr (!std::is_same<TIn, f16>::value) {
+    f16 x[8];
+    InTraits<TIn>::to_op_sc(*reinterpret_cast<const uint4*>(a), x, sc);
+    *a = f16x8{x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  }
+}
 
 // A chunk's inputs of the forward walk in LDS.
 template <int K>
 struct alignas(16) FIn {
-  f16 k[C][K + HP];
-  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
-  f16 vt[BV][C + HP];                  // V^T of the slice
-  // b, gam, D, {gam_C, 0 ..}: the record's gate rows, staged by every lane
-  // (rows 4 .. 7 repeat them)
-  float gv[NTP / C][C];
+  f16 k[C * K];               // K rows, swz<K>
+  f16 th[C * C], tl[C * C];   // T diag(beta) as fp16 pairs, swz<C>
+  f16 v[C * BV];              // V rows of the slice
+  float gv[4][C];             // b, gam, D, {gam_C, 0 ..}
 };
 
-// The walks' inputs are double-buffered: chunk c in in[c & 1], so that the
-// next chunk's are staged during the state update, three barriers a chunk.
+// The forward walk's inputs are triple-buffered (chunk c in in[c % 3]): a
+// chunk's copies are issued two chunks ahead and have a whole chunk to land.
 template <int K>
 struct alignas(16) FMem {
   f16 sh[BV][K + HP], sl[BV][K + HP];  // S^T
   f16 yh[BV][C + HP], yl[BV][C + HP];  // (V - diag(gam) K S)^T
   f16 dh[BV][C + HP], dl[BV][C + HP];  // (diag(D) u)^T
-  FIn<K> in[2];
+  float uf[C][BV];                     // u rows, on their way to uu
+  FIn<K> in[3];
 };
 
 // A chunk's inputs of the backward walk in LDS.
 template <int K>
 struct alignas(16) RIn {
-  f16 q[C][K + HP], k[C][K + HP];
-  f16 th[C][C + HP], tl[C][C + HP];    // T diag(beta)
-  f16 ph[C][C + HP], pl[C][C + HP];    // P
-  f16 dot[BV][C + HP];                 // dO^T of the slice
-  float gv[NTP / C][C];
+  f16 q[C * K], k[C * K];     // Q, K rows, swz<K>
+  f16 th[C * C], tl[C * C];   // T diag(beta), swz<C>
+  f16 ph[C * C], pl[C * C];   // P, swz<C>
+  f16 dot[C * BV];            // dO rows of the slice, row t at dperm(t)
+  float gv[4][C];
 };
 
 template <int K>
@@ -839,6 +1002,7 @@ struct alignas(16) RMem {
   f16 gh[BV][C + HP], gl[BV][C + HP];  // (diag(gam) dO)^T
   f16 uh[BV][C + HP], ul[BV][C + HP];  // du^T
   f16 zh[BV][C + HP], zl[BV][C + HP];  // (diag(gam) (T diag(beta))^T du)^T
+  float duf[C][BV];                    // du rows, on their way to du
   RIn<K> in[2];
 };
 
@@ -848,8 +1012,6 @@ union Mem {
   RMem<K> r;
 };
 
-// The state block of this wave (accumulator layout) <-> fp32 rows of a
-// [K][V] array, and its S^T hi / lo copy in LDS.
 template <int K>
 struct State {
   static constexpr int NST = (K / 16 + 3) / 4;
@@ -880,51 +1042,30 @@ struct State {
 };
 
 // The state's fp16 values -> rows of the [V][K] chunk-state array (row =
-// state column), 16 bytes per lane.  They are the hi parts of the walk's
+// state column), 16 bytes a lane (NT lanes).  They are the hi parts of the walk's
 // S^T pair copy (x rounded to nearest), copied as they are.
-template <int K, int LD>
+template <int K, int NT, int LD>
 __device__ __forceinline__ void copy_state_rows(const f16 (*sh)[LD], f16* dst, int tid) {
   constexpr int NV = BV * K / 8;
 #pragma unroll
-  for (int i = 0; i < (NV + NTP - 1) / NTP; ++i) {
-    const int e = tid + i * NTP;
-    if (NV % NTP == 0 || e < NV)
+  for (int i = 0; i < (NV + NT - 1) / NT; ++i) {
+    const int e = tid + i * NT;
+    if (NV % NT == 0 || e < NV)
       *reinterpret_cast<f16x8*>(dst + (int64_t)(e / (K / 8)) * K + 8 * (e % (K / 8))) =
           *reinterpret_cast<const f16x8*>(&sh[e / (K / 8)][8 * (e % (K / 8))]);
   }
 }
 
-// Next chunk's inputs of the forward walk, in registers.
-template <typename TIn, int K>
-struct FNext16 {
-  tiles16::HalfRows<C, C, NTP> th, tl;
-  tiles16::InRows<TIn, C, K, NTP> k;
-  tiles16::SlicePairs<TIn, C, BV, NTP> v;
-  float gate;
-  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* kg, const TIn* vg, int t0,
-                                       int nval) {
-    using R16 = Rec16;
-    const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
-    th.load(tid, rh + R16::TBH, C);
-    tl.load(tid, rh + R16::TBL, C);
-    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
-    v.load(tid, vg + (int64_t)t0 * p.sv[1], p.sv[1], nval);
-    gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
-  }
-  __device__ __forceinline__ void store(FIn<K>& s, int tid, float vsc) const {
-    th.store(tid, s.th);
-    tl.store(tid, s.tl);
-    k.store(tid, s.k);
-    v.store(tid, s.vt, vsc);
-    s.gv[tid / C][tid % C] = gate;
-  }
-};
-
 // Forward walk: S at each chunk start -> ckS (fp16), u -> uu.  For bf16
 // inputs the walk runs on v and h0 shifted into fp16's range
 // (slice_range_scale: both outputs are linear in them) and shifts u back;
 // ckS stays in the shifted units, and the factor that takes it back goes to
-// scl[unit].
+// scl[unit].  Waves 2 and 3 (the loaders) carry every global access of the
+// loop, chunks alternating between them: in chunk c wave 2 + c % 2 issues
+// the copies of chunk c + 2 and stores chunk c's state rows and u rows,
+// while the other waits for the copies of chunk c + 1 it issued a chunk
+// earlier (its only memory operations in flight).  Waves 0 and 1 hold the
+// chain's products (Y, u).
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                int v0, int64_t slot0) {
@@ -938,65 +1079,87 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       reinterpret_cast<const char*>(vg), p.sv[1] * (int64_t)sizeof(TIn), rs.T, BV,
       p.h0 ? p.h0 + bi * p.sh0[0] + hi * p.sh0[1] + v0 * p.sh0[3] : nullptr, p.sh0[2], p.sh0[3], K, 1.f);
   if (tid == 0) p.scl[((int64_t)bi * p.H + hi) * p.nv + v0 / BV] = rsc.fs;
+  const bool loader = wave >= 2;
+  const int lw = wave - 2;
+  // a loader: chunk cn's inputs -> in[b]
+  auto fetch = [&](int cn, int b) __attribute__((always_inline)) {
+    FIn<K>& d = s.in[b];
+    const int64_t ri = (slot0 + cn) * p.H + hi;
+    const int nval = min(C, rs.T - cn * C);
+    const uint16_t* const rh = reinterpret_cast<const uint16_t*>(p.r16 + ri * (int64_t)Rec16::SIZE);
+    dma_rows<K, 1>(reinterpret_cast<const uint16_t*>(kg) + (int64_t)cn * C * p.sk[1], p.sk[1], nval, d.k, 0, lane);
+    dma_rows<C, 1>(rh + Rec16::TBH, C, C, d.th, 0, lane);
+    dma_rows<C, 1>(rh + Rec16::TBL, C, C, d.tl, 0, lane);
+    dma_v(reinterpret_cast<const uint16_t*>(vg) + (int64_t)cn * C * p.sv[1], p.sv[1], nval, d.v, lane);
+    if (lane < C) dma16(p.rec + ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + 4 * lane, &d.gv[0][0]);
+  };
+  // the loader that fetched chunk cn, before the barrier that publishes it
+  auto settle = [&](int cn, int b) __attribute__((always_inline)) {
+    wait_dma();
+    const int nval = min(C, rs.T - cn * C);
+    if (!std::is_same<TIn, f16>::value || nval < C) {
+      fix_rows<TIn, K, 1>(s.in[b].k, nval, 0, lane);
+      fix_v<TIn>(s.in[b].v, nval, rsc.v, lane);
+    }
+  };
   State<K> S;
   S.load(p.h0, p.sh0, bi, hi, v0, wave, r, kq, rsc.v);
   S.put(s.sh, s.sl, wave, r, kq);
-  FNext16<TIn, K> nx;
-  if (nch > 0) {
-    nx.load(p, tid, slot0 * p.H + hi, kg, vg, 0, min(C, rs.T));
-    nx.store(s.in[0], tid, rsc.v);
+  if (loader && lw < nch) {
+    fetch(lw, lw);
+    if (lw == 0) settle(0, 0);
   }
-  __syncthreads();
-  for (int c = 0; c < nch; ++c) {
+  bar();
+  for (int c = 0, b = 0; c < nch; ++c, b = b == 2 ? 0 : b + 1) {
     const int64_t ri = (slot0 + c) * p.H + hi;
-    FIn<K>& in = s.in[c & 1];
-    // the next chunk's inputs (the last chunk's again at the end: every load
-    // is then consumed by the staging below, on every path)
-    const int cn = min(c + 1, nch - 1);
-    nx.load(p, tid, (slot0 + cn) * p.H + hi, kg, vg, cn * C, min(C, rs.T - cn * C));
-    copy_state_rows<K>(s.sh, reinterpret_cast<f16*>(p.ckS) + (ri * p.V + v0) * (int64_t)K, tid);
-    if (wave < 2) {
+    FIn<K>& in = s.in[b];
+    const int b1 = b == 2 ? 0 : b + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+    const bool issuer = loader && lw == (c & 1);
+    if (!loader) {
       // Y = V - diag(gam) K S for rows 16 w .. (k exact in fp16), as Y^T pairs
       const int um0 = 16 * wave;
       f32x4 ak = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 kf = frag8(&in.k[um0 + r][kb + 8 * kq]);
+        const f16x8 kf = frag8_s<K>(in.k, um0 + r, kb + 8 * kq);
         ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), ak, 0, 0, 0);
         ak = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), ak, 0, 0, 0);
       }
       const int t = um0 + 4 * kq;
-      const f16x4 vv = *reinterpret_cast<const f16x4*>(&in.vt[r][t]);
+      const f16x4 vv = frag4_t(reinterpret_cast<const f16 (*)[BV]>(in.v), um0, 0, r, kq);
       const float y[4] = {(float)vv[0] - in.gv[1][t] * ak[0], (float)vv[1] - in.gv[1][t + 1] * ak[1],
                           (float)vv[2] - in.gv[1][t + 2] * ak[2], (float)vv[3] - in.gv[1][t + 3] * ak[3]};
       store_pair4(&s.yh[r][t], &s.yl[r][t], y);
+    } else if (issuer && c + 2 < nch) {
+      fetch(c + 2, b2);
     }
-    __syncthreads();
-    if (wave < 2) {
+    bar();
+    if (!loader) {
       // u = T diag(beta) Y, rows 16 w .. (W S = T diag(beta) diag(gam) K S)
       const int um0 = 16 * wave;
       f32x4 au = {0.f, 0.f, 0.f, 0.f};
-      const f16x8 th = frag8(&in.th[um0 + r][8 * kq]), yh = frag8(&s.yh[r][8 * kq]);
+      const f16x8 th = frag8_s<C>(in.th, um0 + r, 8 * kq), yh = frag8(&s.yh[r][8 * kq]);
       au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, yh, au, 0, 0, 0);
       au = __builtin_amdgcn_mfma_f32_16x16x32_f16(th, frag8(&s.yl[r][8 * kq]), au, 0, 0, 0);
-      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8(&in.tl[um0 + r][8 * kq]), yh, au, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_s<C>(in.tl, um0 + r, 8 * kq), yh, au, 0, 0, 0);
       const int t = um0 + 4 * kq;
       float du[4];
-      float* const uo = p.uu + ri * (int64_t)C * p.V + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         du[i] = in.gv[2][t + i] * au[i];
-        uo[(int64_t)(t + i) * p.V + r] = au[i] * rsc.fs;
+        s.uf[t + i][r] = au[i] * rsc.fs;
       }
       store_pair4(&s.dh[r][t], &s.dl[r][t], du);
+    } else if (issuer) {
+      copy_state_rows<K, 64>(s.sh, reinterpret_cast<f16*>(p.ckS) + (ri * p.V + v0) * (int64_t)K, lane);
     }
-    __syncthreads();
+    bar();
     // S <- gam_C S + K^T diag(D) u
 #pragma unroll
     for (int j = 0; j < State<K>::NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        const f16x8 kt = frag8_t(in.k, 0, m0, r, kq);
+        const f16x8 kt = frag8_ts<K>(in.k, 0, m0, r, kq);
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
         a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dh[r][8 * kq]), a, 0, 0, 0);
         a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.dl[r][8 * kq]), a, 0, 0, 0);
@@ -1005,48 +1168,31 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-    nx.store(s.in[(c + 1) & 1], tid, rsc.v);
-    __syncthreads();
+    if (issuer) {
+      // u rows -> uu: 16 bytes a lane
+      static_assert(C * BV % (4 * 64) == 0, "whole u pieces per lane");
+#pragma unroll
+      for (int i = 0; i < C * BV / (4 * 64); ++i) {
+        const int e = lane + 64 * i, row = e / (BV / 4), c4 = 4 * (e % (BV / 4));
+        *reinterpret_cast<f32x4*>(p.uu + (ri * C + row) * (int64_t)p.V + v0 + c4) =
+            *reinterpret_cast<const f32x4*>(&s.uf[row][c4]);
+      }
+    } else if (loader && c + 1 < nch) {
+      settle(c + 1, b1);
+    }
+    bar();
   }
+  wait_dma();
 }
-
-// Next chunk's inputs of the backward walk, in registers.
-template <typename TIn, int K>
-struct RNext16 {
-  tiles16::HalfRows<C, C, NTP> th, tl, ph, pl;
-  tiles16::InRows<TIn, C, K, NTP> q, k;
-  tiles16::SlicePairs<TIn, C, BV, NTP> d;
-  float gate;
-  __device__ __forceinline__ void load(const BArgs& p, int tid, int64_t ri, const TIn* qg, const TIn* kg,
-                                       const TIn* dg, int t0, int nval) {
-    using R16 = Rec16;
-    const f16* const rh = p.r16 + ri * (int64_t)R16::SIZE;
-    th.load(tid, rh + R16::TBH, C);
-    tl.load(tid, rh + R16::TBL, C);
-    ph.load(tid, rh + R16::PH, C);
-    pl.load(tid, rh + R16::PL, C);
-    q.load(tid, qg + (int64_t)t0 * p.sq[1], p.sq[1], nval);
-    k.load(tid, kg + (int64_t)t0 * p.sk[1], p.sk[1], nval);
-    d.load(tid, dg + (int64_t)t0 * p.sdo[1], p.sdo[1], nval);
-    gate = p.rec[ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + (tid & (4 * C - 1))];
-  }
-  __device__ __forceinline__ void store(RIn<K>& s, int tid, float dsc) const {
-    th.store(tid, s.th);
-    tl.store(tid, s.tl);
-    ph.store(tid, s.ph);
-    pl.store(tid, s.pl);
-    q.store(tid, s.q);
-    k.store(tid, s.k);
-    d.store(tid, s.dot, dsc);
-    s.gv[tid / C][tid % C] = gate;
-  }
-};
 
 // Backward walk: dS' of each chunk -> ckD (fp16), du -> du, at the end dh0.
 // For bf16 inputs the walk runs on dO and d_final_state shifted into fp16's
 // range (every output of the walk is linear in them) and shifts du and dh0
 // back: small gradients keep their hi / lo precision.  ckD stays in the
 // shifted units; the factor that takes it back goes to scl[units + unit].
+// Waves 2 and 3 (the loaders) copy the previous chunk's inputs but its q
+// rows and store the chunk's dS' rows and du rows; waves 0 and 1 hold the
+// chain's products (du, z) and copy the q rows once their du is done.
 template <typename TIn, int K>
 __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, const RowSpan& rs, int bi, int hi,
                                                 int v0, int64_t slot0) {
@@ -1062,54 +1208,89 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       reinterpret_cast<const char*>(dg), p.sdo[1] * (int64_t)sizeof(TIn), rs.T, BV,
       p.dfs ? p.dfs + bi * p.sdfs[0] + hi * p.sdfs[1] + v0 * p.sdfs[3] : nullptr, p.sdfs[2], p.sdfs[3], K, 1.f);
   if (tid == 0) p.scl[p.units + ((int64_t)bi * p.H + hi) * p.nv + v0 / BV] = rsd.fs;
+  const bool loader = wave >= 2;
+  const int lw = wave - 2, ll = tid - 128;
+  // chunk cn's inputs -> in[cn & 1]: q rows from waves 0 and 1 (issued at
+  // the end of their first phase, where they wait for the loaders anyway),
+  // the rest from the loaders
+  auto fetch = [&](int cn) __attribute__((always_inline)) {
+    RIn<K>& d = s.in[cn & 1];
+    const int nval = min(C, rs.T - cn * C);
+    if (!loader) {
+      dma_rows<K, 2>(reinterpret_cast<const uint16_t*>(qg) + (int64_t)cn * C * p.sq[1], p.sq[1], nval, d.q, wave,
+                     lane);
+      return;
+    }
+    const int64_t ri = (slot0 + cn) * p.H + hi;
+    const uint16_t* const rh = reinterpret_cast<const uint16_t*>(p.r16 + ri * (int64_t)Rec16::SIZE);
+    dma_rows<K, 2>(reinterpret_cast<const uint16_t*>(kg) + (int64_t)cn * C * p.sk[1], p.sk[1], nval, d.k, lw, lane);
+    dma_rows<C, 2>(rh + Rec16::TBH, C, C, d.th, lw, lane);
+    dma_rows<C, 2>(rh + Rec16::TBL, C, C, d.tl, lw, lane);
+    dma_rows<C, 2>(rh + Rec16::PH, C, C, d.ph, lw, lane);
+    dma_rows<C, 2>(rh + Rec16::PL, C, C, d.pl, lw, lane);
+    dma_dot(reinterpret_cast<const uint16_t*>(dg) + (int64_t)cn * C * p.sdo[1], p.sdo[1], nval, d.dot, lw, lane);
+    if (lw == 0 && lane < C) dma16(p.rec + ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + 4 * lane, &d.gv[0][0]);
+  };
+  // every wave, before the barrier that publishes chunk cn: its own copies
+  auto settle = [&](int cn) __attribute__((always_inline)) {
+    wait_dma();
+    const int nval = min(C, rs.T - cn * C);
+    if (!std::is_same<TIn, f16>::value || nval < C) {
+      RIn<K>& d = s.in[cn & 1];
+      if (!loader) {
+        fix_rows<TIn, K, 2>(d.q, nval, wave, lane);
+      } else {
+        fix_rows<TIn, K, 2>(d.k, nval, lw, lane);
+        fix_dot<TIn>(d.dot, nval, rsd.v, lw, lane);
+      }
+    }
+  };
   State<K> S;
   S.load(p.dfs, p.sdfs, bi, hi, v0, wave, r, kq, rsd.v);
   S.put(s.sh, s.sl, wave, r, kq);
-  RNext16<TIn, K> nx;
   if (nch > 0) {
-    const int t0 = (nch - 1) * C;
-    nx.load(p, tid, (slot0 + nch - 1) * p.H + hi, qg, kg, dg, t0, rs.T - t0);
-    nx.store(s.in[(nch - 1) & 1], tid, rsd.v);
+    fetch(nch - 1);
+    settle(nch - 1);
   }
-  __syncthreads();
+  bar();
   for (int c = nch - 1; c >= 0; --c) {
     const int64_t ri = (slot0 + c) * p.H + hi;
     RIn<K>& in = s.in[c & 1];
-    // the previous chunk's inputs (chunk 0's again at the end)
-    const int cn = max(c - 1, 0);
-    nx.load(p, tid, (slot0 + cn) * p.H + hi, qg, kg, dg, cn * C, min(C, rs.T - cn * C));
-    copy_state_rows<K>(s.sh, reinterpret_cast<f16*>(p.ckD) + (ri * p.V + v0) * (int64_t)K, tid);
-    if (wave < 2) {
+    if (!loader) {
       // du = scale P^T dO + diag(D) K dS', rows 16 w ..
       const int um0 = 16 * wave;
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
-      const f16x8 df = frag8(&in.dot[r][8 * kq]);
-      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(in.ph, 0, um0, r, kq), df, a1, 0, 0, 0);
-      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_t(in.pl, 0, um0, r, kq), df, a1, 0, 0, 0);
+      const f16x8 df = dot_frag8(in.dot, r, kq);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_ts<C>(in.ph, 0, um0, r, kq), df, a1, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag8_ts<C>(in.pl, 0, um0, r, kq), df, a1, 0, 0, 0);
 #pragma unroll
       for (int kb = 0; kb < K; kb += 32) {
-        const f16x8 kf = frag8(&in.k[um0 + r][kb + 8 * kq]);
+        const f16x8 kf = frag8_s<K>(in.k, um0 + r, kb + 8 * kq);
         a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sh[r][kb + 8 * kq]), a2, 0, 0, 0);
         a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, frag8(&s.sl[r][kb + 8 * kq]), a2, 0, 0, 0);
       }
       const int t = um0 + 4 * kq;
       float du[4];
-      float* const duo = p.du + ri * (int64_t)C * p.V + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         du[i] = scale * a1[i] + in.gv[2][t + i] * a2[i];
-        duo[(int64_t)(t + i) * p.V + r] = du[i] * rsd.fs;
+        s.duf[t + i][r] = du[i] * rsd.fs;
       }
       store_pair4(&s.uh[r][t], &s.ul[r][t], du);
+      if (c >= 1) fetch(c - 1);
     } else {
-      // (diag(gam) dO)^T as pairs: lane -> column tid % 16, rows 4 (tid / 16) ..
-      const int l = tid - 128, col = l & 15, t4 = 4 * (l >> 4);
-      const f16x4 dv = *reinterpret_cast<const f16x4*>(&in.dot[col][t4]);
+      // the previous chunk's copies first: they have until the chunk's end
+      if (c >= 1) fetch(c - 1);
+      // (diag(gam) dO)^T as pairs: lane (r, kq) of loader wave lw -> column
+      // r, rows t4 .. t4 + 3 (a 32-lane pass reads rows 0..3, 8..11 + 16 lw)
+      const int t4 = 16 * lw + ((kq & 1) << 3) + ((kq & 2) << 1);
+      const f16x4 dv = read_tr4(in.dot + dperm(t4 + (r >> 2)) * BV + 4 * (r & 3));
       const float x[4] = {in.gv[1][t4] * (float)dv[0], in.gv[1][t4 + 1] * (float)dv[1],
                           in.gv[1][t4 + 2] * (float)dv[2], in.gv[1][t4 + 3] * (float)dv[3]};
-      store_pair4(&s.gh[col][t4], &s.gl[col][t4], x);
+      store_pair4(&s.gh[r][t4], &s.gl[r][t4], x);
+      copy_state_rows<K, 128>(s.sh, reinterpret_cast<f16*>(p.ckD) + (ri * p.V + v0) * (int64_t)K, ll);
     }
-    __syncthreads();
+    bar();
     // W^T du = K^T diag(beta gam) T^T du = K^T (diag(gam) (T diag(beta))^T du):
     // z on waves 0-1 (rows 16 w .. of z, T diag(beta) transposed by the
     // reads) while waves 2-3 form their Q^T diag(gam) dO term
@@ -1120,15 +1301,15 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
         const int m0 = 16 * (wave + 4 * j);
         aq[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (m0 < K) {
-          const f16x8 qt = frag8_t(in.q, 0, m0, r, kq);
+          const f16x8 qt = frag8_ts<K>(in.q, 0, m0, r, kq);
           aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gh[r][8 * kq]), aq[j], 0, 0, 0);
           aq[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qt, frag8(&s.gl[r][8 * kq]), aq[j], 0, 0, 0);
         }
       }
     };
-    if (wave < 2) {
+    if (!loader) {
       const int um0 = 16 * wave;
-      const f16x8 tth = frag8_t(in.th, 0, um0, r, kq), ttl = frag8_t(in.tl, 0, um0, r, kq);
+      const f16x8 tth = frag8_ts<C>(in.th, 0, um0, r, kq), ttl = frag8_ts<C>(in.tl, 0, um0, r, kq);
       const f16x8 uh = frag8(&s.uh[r][8 * kq]);
       f32x4 az = {0.f, 0.f, 0.f, 0.f};
       az = __builtin_amdgcn_mfma_f32_16x16x32_f16(tth, uh, az, 0, 0, 0);
@@ -1140,15 +1321,20 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       store_pair4(&s.zh[r][t], &s.zl[r][t], z);
     } else {
       q_term();
+      // du rows -> du: 16 bytes a loader lane
+      static_assert(C * BV == 4 * 128, "four du entries per loader lane");
+      const int row = ll / (BV / 4), c4 = 4 * (ll % (BV / 4));
+      *reinterpret_cast<f32x4*>(p.du + (ri * C + row) * (int64_t)p.V + v0 + c4) =
+          *reinterpret_cast<const f32x4*>(&s.duf[row][c4]);
     }
-    __syncthreads();
-    if (wave < 2) q_term();
+    bar();
+    if (!loader) q_term();
     // dS <- scale Q^T diag(gam) dO + gam_C dS' - K^T z
 #pragma unroll
     for (int j = 0; j < State<K>::NST; ++j) {
       const int m0 = 16 * (wave + 4 * j);
       if (m0 < K) {
-        const f16x8 kt = frag8_t(in.k, 0, m0, r, kq);
+        const f16x8 kt = frag8_ts<K>(in.k, 0, m0, r, kq);
         f32x4 b = {0.f, 0.f, 0.f, 0.f};
         b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zh[r][8 * kq]), b, 0, 0, 0);
         b = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt, frag8(&s.zl[r][8 * kq]), b, 0, 0, 0);
@@ -1157,9 +1343,10 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
       }
     }
     S.put(s.sh, s.sl, wave, r, kq);
-    nx.store(s.in[(c + 1) & 1], tid, rsd.v);
-    __syncthreads();
+    if (c >= 1) settle(c - 1);
+    bar();
   }
+  wait_dma();
   if (p.dh0 != nullptr) {
 #pragma unroll
     for (int j = 0; j < State<K>::NST; ++j) {
