@@ -69,10 +69,14 @@ def test_bwd_fp32_vs_autograd(pkg, cuda, T, K, V, gate):
     _compare(got, want, torch.float32, f"fp32 T={T} K={K} V={V}")
 
 
-@pytest.mark.parametrize("T,K,V", [(200, 128, 32), (77, 64, 48), (33, 32, 16)])
+@pytest.mark.parametrize("T,K,V", [(200, 128, 32), (77, 64, 48), (33, 32, 16),
+                                   (1, 64, 16), (32, 128, 16), (96, 128, 32), (97, 32, 48)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_bwd_lowp_vs_autograd(pkg, cuda, dtype, T, K, V):
-    """16-bit q, k, v and dO: the recurrences run on fp16 hi / lo pairs."""
+    """16-bit q, k, v and dO: the recurrences run on fp16 hi / lo pairs.
+    Chunk counts 1 to 7, whole and partial last chunks: the walks copy their
+    inputs one (backward) or two (forward) chunks ahead and zero a partial
+    chunk's rows in LDS."""
     B, H = 1, 3
     q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=5)
     d = lambda t: t.to(cuda)
