@@ -792,7 +792,9 @@ __global__ __launch_bounds__(NTP) void recur_kernel(const BArgs p) {
 //     lo copy of its transpose in LDS feeds the products through it.  K^T,
 //     Q^T, P^T and W^T are read from row-major LDS copies by transposing
 //     reads.  Per chunk: the u (du) tiles on waves 0-1, then the state
-//     update on all four waves, then the next chunk's inputs are staged.
+//     update on all four waves; the inputs of the chunks ahead arrive in
+//     LDS by LDS-DMA copies that waves 2-3 (and, for q, waves 0-1) issue
+//     and drain themselves.
 // ---------------------------------------------------------------------------
 
 namespace w16 {
