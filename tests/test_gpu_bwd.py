@@ -277,3 +277,31 @@ def test_bwd_bf16_extreme_scales(pkg, cuda, v_scale, d_scale):
     want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=1.0)
     got = (got[0], got[1], got[2], got[4], got[3], got[5])   # -> dq dk dv dbeta dg dh0
     _compare(got, want, torch.bfloat16, f"bf16 v*{v_scale:g} dO*{d_scale:g}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_bwd_do_row_offsets(pkg, cuda, dtype):
+    """dO as a view into a wider buffer: rows 4-byte aligned (the 16-bit
+    walks copy dO slices 4 bytes a lane) give the same bits as a dense dO;
+    rows only 2-byte aligned take the fp32 recurrences and still match the
+    oracle."""
+    B, T, H, K, V = 1, 77, 2, 64, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=23)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] {dtype} dO row offsets T={T} K={K} V={V}", flush=True)
+    dense = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=1.0)
+    wide = torch.zeros(B, T, H, V + 8, dtype=dtype)
+    for off in (2, 1):   # elements: 4 bytes, then 2 bytes
+        wide.zero_()
+        wide[..., off:off + V] = do
+        view = d(wide)[..., off:off + V]
+        assert view.stride(-1) == 1 and (view.data_ptr() % 4 == 0) == (off == 2)
+        got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), view, d(dfin), scale=1.0)
+        torch.cuda.synchronize()
+        if off == 2:
+            for a, b in zip(got, dense):
+                if a is not None:
+                    assert torch.equal(a, b)
+        else:
+            want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin)
+            _compare((got[0], got[1], got[2], got[4], got[3], got[5]), want, dtype, f"{dtype} dO offset {off}")
