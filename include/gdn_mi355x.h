@@ -46,7 +46,11 @@
 extern "C" {
 #endif
 
-#define GDN_MI355X_ABI_VERSION 4
+/* 5: C = 32 with fp16 / bf16 inputs runs on per-chunk records in the
+ * caller's workspace (gdn_fwd_workspace_size is non-zero there, and a
+ * workspace smaller than one record per sequence and head is
+ * GDN_ERR_WORKSPACE); 64-row records are laid out per sequence segment. */
+#define GDN_MI355X_ABI_VERSION 5
 
 /* Element types of the tensors crossing the boundary. */
 enum GdnDtype {
@@ -57,7 +61,9 @@ enum GdnDtype {
 
 /* Status codes.  0 is success; values below 1000 are hipError_t values
  * passed through from the HIP runtime; values from 1000 are argument
- * errors detected before launch (nothing is enqueued). */
+ * errors detected before launch (nothing is enqueued).  A launch error
+ * (a hipError_t) can come after earlier segments of the same call were
+ * enqueued, so o and final_state may then be partly written. */
 enum GdnStatus {
   GDN_OK = 0,
   GDN_ERR_NULL_POINTER = 1001,
@@ -149,14 +155,18 @@ int gdn_fwd_launch(const GdnFwdParams* params, void* stream);
  *   - 32-row chunks (fp16, bf16): the sequence runs in segments of as many
  *     chunks as the array holds (B * H records per chunk, of 3 KB for fp16
  *     and 3 KB + 2 C K bytes for bf16, which also carry the chunk's k rows
- *     in fp16); if one chunk per sequence does not fit (fp16:
- *     B * H > 10922; bf16 at K = 128: B * H > 2978), bf16 runs on the fused
- *     kernel and fp16 fails with GDN_ERR_SCRATCH_LIMIT.
+ *     in fp16).  If one chunk per sequence does not fit (fp16:
+ *     B * H > 10922; bf16 at K = 128: B * H > 2978), the call runs on the
+ *     fused kernel, which needs no workspace.
  *   - 64-row chunks: likewise in segments (records of 33 KB per chunk and
- *     head for 16-bit inputs, 66 KB for fp32 at K = 128); GDN_ERR_SCRATCH_LIMIT
- *     only if one chunk per sequence does not fit (B * H > 992 for 16-bit
- *     inputs).
- *   - Nothing is enqueued when a status other than GDN_OK is returned.
+ *     head for 16-bit inputs, 66 KB for fp32 at K = 128).  If one chunk
+ *     per sequence does not fit (B * H > 992 for 16-bit inputs), the call
+ *     runs on the phased kernel, which needs no workspace;
+ *     GDN_ERR_SCRATCH_LIMIT only where that kernel does not support the
+ *     shape either.
+ *   - The first call on a device fetches the array's device address
+ *     (hipGetSymbolAddress) and keeps it: make one call on each device
+ *     before capturing a call into a HIP graph.
  * Every call on a device shares that device's array: calls that overlap
  * on one device (on different streams, or from different host threads)
  * race and must be serialised by the caller. */

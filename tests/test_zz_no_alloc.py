@@ -147,3 +147,75 @@ def test_noalloc_bf16_beyond_scratch_runs_fused(pkg, cuda):
     o_ref, h_ref = ref.recurrent(qc, kc, vc, bc, gc, ref.to_vk(hc), dtype=torch.float64)
     assert ref.rel_err(0.8 * o_ref, o.cpu()) <= 1e-3
     assert ref.rel_err(ref.to_kv(h_ref), fs.cpu()) <= 1e-3
+
+
+@pytest.mark.parametrize("dtype,chunk,H", [(torch.float16, 32, 10923), (torch.float16, 64, 1000)])
+def test_noalloc_beyond_scratch_falls_back(pkg, cuda, dtype, chunk, H):
+    """fp16 at 32-row chunks (10923 heads x 3 KB) and 64-row chunks (1000
+    heads x 33 KB) whose records do not fit the scratch array even one chunk
+    per sequence-head run on a kernel without workspace (the fused kernel,
+    the phased kernel) instead of failing: checked against the fp64
+    recurrence."""
+    B, T, K, V = 1, 40 if chunk == 32 else 100, 64, 16
+    q, k, v, g, beta, h0 = _inputs(cuda, B, T, H, K, V, dtype, 90 + chunk)
+    L = pkg._lib
+    lib = L.load_library()
+    o = torch.full((B, T, H, V), float("nan"), dtype=torch.float32, device=cuda)
+    fs = torch.full((B, H, K, V), float("nan"), dtype=torch.float32, device=cuda)
+    P = _params(L, q, k, v, g, beta, h0, o, fs, chunk)
+    print(f"[no_alloc] {dtype} C={chunk} B={B} T={T} H={H} beyond the scratch array", flush=True)
+    rc = lib.gdn_fwd_launch_noalloc(ctypes.byref(P), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, L.status_string(rc)
+    qc, kc, vc, gc, bc, hc = (t.cpu() for t in (q, k, v, g, beta, h0))
+    o_ref, h_ref = ref.recurrent(qc, kc, vc, bc, gc, ref.to_vk(hc), dtype=torch.float64)
+    assert ref.rel_err(0.8 * o_ref, o.cpu()) <= 1e-3
+    assert ref.rel_err(ref.to_kv(h_ref), fs.cpu()) <= 1e-3
+
+
+@pytest.mark.parametrize("dtype,chunk", [(torch.float16, 32), (torch.bfloat16, 32), (torch.float16, 64)])
+def test_noalloc_under_graph_capture(pkg, cuda, dtype, chunk):
+    """The use the entry point exists for: after one eager call on the
+    device, a call captured into a HIP graph (torch.cuda.graph) replays with
+    outputs equal bit for bit to gdn_fwd_launch's, replay after replay, with
+    eager work and synchronisations between the replays; and a warmed eager
+    call takes no device memory (free bytes unchanged)."""
+    B, T, H, K, V = 2, 333, 256, 128, 64   # 512 heads: 3 segments of 21 chunks at C = 32 (fp16)
+    (o1, fs1), _ = _both(pkg, cuda, B, T, H, K, V, dtype, chunk, seed=97)
+    L = pkg._lib
+    lib = L.load_library()
+    q, k, v, g, beta, h0 = _inputs(cuda, B, T, H, K, V, dtype, 97)
+    o = torch.full((B, T, H, V), float("nan"), dtype=dtype, device=cuda)
+    fs = torch.full((B, H, K, V), float("nan"), dtype=torch.float32, device=cuda)
+    P = _params(L, q, k, v, g, beta, h0, o, fs, chunk)
+    # warmed eager call: no allocation
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = lib.gdn_fwd_launch_noalloc(ctypes.byref(P), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, L.status_string(rc)
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.equal(o, o1) and torch.equal(fs, fs1)
+    print(f"[no_alloc] graph capture {dtype} C={chunk} B={B} T={T} H={H}", flush=True)
+    o.fill_(float("nan"))
+    fs.fill_(float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = lib.gdn_fwd_launch_noalloc(ctypes.byref(P), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert rc == 0, L.status_string(rc)
+    for rep in range(3):
+        o.fill_(float("nan"))
+        fs.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o1), f"replay {rep}: o differs"
+        assert torch.equal(fs, fs1), f"replay {rep}: final state differs"
+        # eager work between replays
+        (_, _), (o3, fs3) = _both(pkg, cuda, 1, 100, 3, K, V, dtype, chunk, seed=98 + rep)
+        assert torch.isfinite(o3.float()).all()

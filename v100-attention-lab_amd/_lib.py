@@ -9,7 +9,7 @@ import threading
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libgdn_mi355x.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enum GdnDtype
 DTYPE_F32 = 0

@@ -109,7 +109,7 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   if (P.T > 0 && (P.q == nullptr || P.k == nullptr || P.v == nullptr || P.g == nullptr ||
                   P.beta == nullptr || P.o == nullptr))
     return GDN_ERR_NULL_POINTER;
-  const bool c64 = uses_c64(P);
+  bool c64 = uses_c64(P);
   int bv = c64 ? 16 : P.block_v;
   if (bv == 0) bv = auto_block_v(P.B, P.H, P.K, P.V, P.chunk_size, P.qkv_dtype);
   if (!c64 && (bv <= 0 || P.V % bv != 0 || !supported(P.qkv_dtype, P.K, P.chunk_size, bv)))
@@ -128,24 +128,32 @@ static int launch_impl(const GdnFwdParams& P, hipStream_t s, int64_t scratch_byt
   const long long units = (long long)P.B * P.H * (P.V / bv);
   if (units > 0x7fffffffLL) return GDN_ERR_BAD_SHAPE;
   bool scan32 = uses_scan32(P, bv) && (scratch_bytes > 0 || P.workspace != nullptr);
-  // bf16 runs on the fused kernel (no workspace) when the static scratch
-  // cannot hold its records
-  if (scan32 && scratch_bytes > 0 && P.qkv_dtype == GDN_DTYPE_BF16 &&
-      (int64_t)P.B * P.H * scan32_record_bytes(P.qkv_dtype, P.K) > scratch_bytes)
-    scan32 = false;
-  // workspace: the caller's, or the static scratch array when it holds
-  // what the path needs
+  if (scratch_bytes > 0 && P.T > 0) {
+    // The static scratch must hold one chunk's records per sequence and
+    // head (longer sequences run in segments).  Where it cannot, the call
+    // runs on a kernel that needs no workspace: the fused kernel for
+    // 32-row chunks (it supports every shape the records path does), the
+    // phased kernel for 64-row chunks.
+    const int64_t bh = (int64_t)P.B * P.H;
+    if (scan32 && bh * scan32_record_bytes(P.qkv_dtype, P.K) > scratch_bytes) scan32 = false;
+    if (c64 && bh * c64_record_bytes(P.K, P.qkv_dtype) > scratch_bytes) {
+      if (!supported(P.qkv_dtype, P.K, P.chunk_size, bv)) return GDN_ERR_SCRATCH_LIMIT;
+      c64 = false;
+    }
+  }
+  // workspace: the caller's, or the static scratch array
   GdnFwdParams W = P;
   if (scratch_bytes > 0 && (c64 || scan32) && P.T > 0) {
-    // one chunk per sequence and head (longer sequences run in segments)
-    const int64_t need = (int64_t)P.B * P.H * (c64 ? c64_record_bytes(P.K, P.qkv_dtype) : scan32_record_bytes(P.qkv_dtype, P.K));
-    if (need > scratch_bytes) return GDN_ERR_SCRATCH_LIMIT;
     void* ptr = nullptr;
     const int st = scratch_address(&ptr);
     if (st != 0) return st;
     W.workspace = ptr;
     W.workspace_bytes = scratch_bytes;
   }
+  // Launch errors are read back with hipGetLastError after each launch:
+  // clear one left by unrelated earlier work so that it is not reported
+  // as this call's.
+  (void)hipGetLastError();
   if (c64) {
     // segment length: as many chunks per sequence as the workspace holds
     const int64_t per_chunk = (int64_t)P.B * P.H * c64_record_bytes(P.K, P.qkv_dtype);

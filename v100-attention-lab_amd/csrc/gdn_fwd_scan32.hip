@@ -56,7 +56,7 @@ constexpr int D = 4;  // chunks loaded ahead by the LOAD wave
 constexpr int REC_BYTES = 3072;
 // record layout (byte offsets)
 constexpr int R_TU = 0;     // f16x8 [2][64]: Tu rows 16 mt + (lane & 15), columns pi(lane >> 4, s)
-constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b (flat past the sequence end)
+constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b times log2(e) (flat past the sequence end)
 constexpr int R_EB = 2176;  // float [32]: e^b
 constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
 constexpr int R_EBC = 2432; // float: e^{bC}
@@ -98,7 +98,7 @@ struct SArgs {
   int g_dtype, beta_dtype, o_dtype;
   const int64_t* cu;
   int xcd_remap;
-  int o_vec;           // o rows take 16-byte stores (base and strides aligned)
+  int o_vec;           // o takes 16-byte stores (base and strides aligned for them)
 };
 
 // One barrier of the workgroup.  Written out (rather than __syncthreads)
@@ -116,6 +116,25 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// The fp16 rounding residual of two accumulator tiles given their fp16
+// rounding h: lo = (f16)(x - (float)h), as split_lo, but written as
+// fma(h, -one, x) so that each element is one v_fma_mix (h read as fp16
+// from its half of the packed register, the result rounded to fp16).  x - h
+// is exact in fp32, so the rounding is the same.  `one` is 1.0 held in a
+// register the compiler cannot see through (opaque_one); with a literal 1
+// the product is folded into a subtraction and the conversions return.
+__device__ __forceinline__ float opaque_one() {
+  float one = 1.0f;
+  asm volatile("" : "+v"(one));
+  return one;
+}
+__device__ __forceinline__ f16x8 split_lo_mix(const f32x4& lo, const f32x4& hi, const f16x8& h, float one) {
+  return f16x8{(f16)__builtin_fmaf((float)h[0], -one, lo[0]), (f16)__builtin_fmaf((float)h[1], -one, lo[1]),
+               (f16)__builtin_fmaf((float)h[2], -one, lo[2]), (f16)__builtin_fmaf((float)h[3], -one, lo[3]),
+               (f16)__builtin_fmaf((float)h[4], -one, hi[0]), (f16)__builtin_fmaf((float)h[5], -one, hi[1]),
+               (f16)__builtin_fmaf((float)h[6], -one, hi[2]), (f16)__builtin_fmaf((float)h[7], -one, hi[3])};
+}
 
 // 16 bytes per lane from global memory into LDS at base + 16 * lane.
 __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
@@ -285,7 +304,7 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   s_b[wave][half][c] = b;
   if (nval[half] > 0) {
     char* rr = rp[half];
-    reinterpret_cast<float*>(rr + R_B)[c] = b;
+    reinterpret_cast<float*>(rr + R_B)[c] = b * 1.4426950408889634f;
     reinterpret_cast<float*>(rr + R_EB)[c] = fexp(b);
     reinterpret_cast<float*>(rr + R_EC)[c] = fexp(bC - b);
     if (c == 0) *reinterpret_cast<float*>(rr + R_EBC) = fexp(bC);
@@ -423,8 +442,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
 // 2. the scan
 // ---------------------------------------------------------------------------
 
-constexpr int OT_PITCH = 20;  // floats per row of an o staging tile (16 + 4: rows 4 apart hit other banks)
-
 template <int K, int BV>
 struct alignas(16) ScanSmem {
   static constexpr int NSW = BV / 16;
@@ -437,24 +454,32 @@ struct alignas(16) ScanSmem {
   f16x8 p[2][2][64];                // P operand fragments, hi
   f16x8 plo[2][2][64];              // and the fp16 residual
   f16x8 so[2][NSW][K / 32][64];     // chunk-start state as B operand fragments
-  f16x8 uo[2][NSW][2][64];          // u as hi + lo
-  float ot[NSW][C][OT_PITCH];       // o tile of each OUT wave, for row-contiguous stores
+  f32x4 uo[2][NSW][2][64];          // u in fp32 (accumulator layout)
 };
 
-// 8 consecutive o elements (two f32x4) at o + off, aligned for a 16-byte
-// (16-bit o) or two 16-byte (fp32 o) stores.
+// Two floats as packed fp16 (round to nearest even, as (f16) x).
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  typedef f16 f16x2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, f16x2v{(f16)a, (f16)b});
+}
+
+// 4 consecutive o elements at o + off: one 16-byte store (fp32 o, when
+// `vec`: base and strides aligned for it), else one store per element.
 template <typename TOut>
-__device__ __forceinline__ void store_o8(void* o, int64_t off, const f32x4& w0, const f32x4& w1) {
-  if constexpr (std::is_same<TOut, f16>::value) {
-    *reinterpret_cast<f16x8*>(static_cast<f16*>(o) + off) =
-        f16x8{(f16)w0[0], (f16)w0[1], (f16)w0[2], (f16)w0[3], (f16)w1[0], (f16)w1[1], (f16)w1[2], (f16)w1[3]};
-  } else if constexpr (std::is_same<TOut, bf16_t>::value) {
-    auto pk = [](float a, float b) { return (uint32_t)float_to_bf16_bits(a) | ((uint32_t)float_to_bf16_bits(b) << 16); };
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(o) + off) =
-        uint4{pk(w0[0], w0[1]), pk(w0[2], w0[3]), pk(w1[0], w1[1]), pk(w1[2], w1[3])};
+__device__ __forceinline__ void store_o4(void* o, int64_t off, const f32x4& w, int vec) {
+  if (vec) {
+    if constexpr (std::is_same<TOut, f16>::value) {
+      typedef f16 f16x4v __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<f16x4v*>(static_cast<f16*>(o) + off) = f16x4v{(f16)w[0], (f16)w[1], (f16)w[2], (f16)w[3]};
+    } else if constexpr (std::is_same<TOut, bf16_t>::value) {
+      auto pk = [](float a, float b) { return (uint32_t)float_to_bf16_bits(a) | ((uint32_t)float_to_bf16_bits(b) << 16); };
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(o) + off) = uint2{pk(w[0], w[1]), pk(w[2], w[3])};
+    } else {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = w;
+    }
   } else {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = w0;
-    *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off + 4) = w1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) put<TOut>(o, off + i, w[i]);
   }
 }
 
@@ -690,11 +715,8 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
         __builtin_amdgcn_sched_group_barrier(SG_DSR, 2, 0);
       }
-      {
-        const f16x8 uh = M::from_acc(u[0], u[1]);
-        s.uo[it & 1][cb][0][lane] = uh;
-        s.uo[it & 1][cb][1][lane] = split_lo(u[0], u[1], uh);
-      }
+      s.uo[it & 1][cb][0][lane] = u[0];
+      s.uo[it & 1][cb][1][lane] = u[1];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
       PS_END_A(sB[0], sB[KB - 1]);
@@ -721,124 +743,187 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     return;
   } else if (role == SR_OUT) {
     // ================================================================ OUT
+    // o is formed transposed: o^T = u^T P^T + (Q S)^T diag(e^b).  The
+    // operand fragments are the same registers as for P u and Q S with A
+    // and B exchanged (an A fragment holds row lane % 16 over contraction
+    // slots, a B fragment column lane % 16 over the same slots), and the
+    // accumulator then holds 4 consecutive o columns (v) of one row (t) per
+    // lane: o goes out with one 4-element store per lane and tile.
     const int c2 = ridx;
-    f32x4 oq[2] = {z4, z4};
+    const float one = opaque_one();
+    f32x4 oq[2] = {z4, z4};  // (Q S)^T: lane (n, gq) holds v = 4 gq + i of row t = 16 mt + n
+    // 16-bit o after the exchange: lane (n, gq) stores columns 8 (gq / 2) ..
+    // + 7 of row orow (of each chunk)
+    const int orow = n + 16 * (gq & 1);
+    const int64_t o_eb = p.o_dtype == GDN_DTYPE_F32 ? 4 : 2;
+    const int64_t o_row_bytes = p.so[1] * o_eb;
+    char* const o_lane = static_cast<char*>(p.o) +
+                         (head_base(rs, hi, p.so) + (int64_t)orow * p.so[1] + v0 + 16 * c2 + 8 * (gq >> 1)) * o_eb;
     PS_DECL;
-    auto store_chunk = [&](int it) {
-      f16x8 uh = s.uo[it & 1][c2][0][lane];
-      f16x8 ul = s.uo[it & 1][c2][1][lane];
-      const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
-      const f32x4 ebv[2] = {*reinterpret_cast<const f32x4*>(ebr + 4 * gq),
-                            *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq)};
-      f32x4 ov[2];
+    // Operands of o for chunk it (u, P, e^b), read at the start of
+    // iteration it + 1 before anything waits on them.
+    struct OutOps {
+      f32x4 u0, u1;
       f16x8 pAs[2], pLs[2];
+      float ebt[2];
+    };
+    auto load_o = [&](int it, OutOps& o) __attribute__((always_inline)) {
+      o.u0 = s.uo[it & 1][c2][0][lane];
+      o.u1 = s.uo[it & 1][c2][1][lane];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        pAs[mt] = s.p[it & 1][mt][lane];
-        pLs[mt] = s.plo[it & 1][mt][lane];
+        o.pAs[mt] = s.p[it & 1][mt][lane];
+        o.pLs[mt] = s.plo[it & 1][mt][lane];
       }
-      PS_BEGIN(uh, ul, pAs[1], pLs[1]);
+      const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
+      o.ebt[0] = ebr[n];
+      o.ebt[1] = ebr[16 + n];
+    };
+    auto store_chunk = [&](int it, const OutOps& o) __attribute__((always_inline)) {
+      const f16x8 uh = M::from_acc(o.u0, o.u1);
+      const f16x8 ul = split_lo_mix(o.u0, o.u1, uh, one);
+      f32x4 ov[2];
+      PS_BEGIN(uh, ul, o.pAs[1], o.pLs[1]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        f32x4 pu = M::mma(pAs[mt], ul, z4);
-        pu = M::mma(pLs[mt], uh, pu);
-        pu = M::mma(pAs[mt], uh, pu);
-        ov[mt] = (pu + ebv[mt] * oq[mt]) * rsc.o;
+        f32x4 pu = M::mma(ul, o.pAs[mt], z4);
+        pu = M::mma(uh, o.pLs[mt], pu);
+        pu = M::mma(uh, o.pAs[mt], pu);
+        ov[mt] = (pu + o.ebt[mt] * oq[mt]) * rsc.o;
       }
       PS_END_B(ov[0], ov[1]);
       const int t0 = (p.c0 + it) * C;
-      const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2;
-      if (p.o_vec) {
-        // through this wave's LDS tile: lane -> row lane / 2, 8 columns
-        float(*const ot)[OT_PITCH] = s.ot[c2];
+      if (p.o_vec && p.o_dtype != GDN_DTYPE_F32) {
+        // 16-bit o: the lanes of 16-lane groups gq and gq ^ 1 exchange a
+        // tile (v_permlane16_swap), so that each lane holds 8 consecutive
+        // columns of one row: row n of tile 0 in even groups, of tile 1 in
+        // odd groups.  One 16-byte store per lane.
+        uint32_t w0[2], w1[2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ot[16 * mt + 4 * gq + i][n] = ov[mt][i];
-        const int r = lane >> 1, c8 = 8 * (lane & 1);
-        const f32x4 w0 = *reinterpret_cast<const f32x4*>(&ot[r][c8]);
-        const f32x4 w1 = *reinterpret_cast<const f32x4*>(&ot[r][c8 + 4]);
-        if (t0 + r < T) {
-          const int64_t off = o_col + (int64_t)(t0 + r) * p.so[1] + c8;
-          if (p.o_dtype == GDN_DTYPE_F16)
-            store_o8<f16>(p.o, off, w0, w1);
-          else if (p.o_dtype == GDN_DTYPE_BF16)
-            store_o8<bf16_t>(p.o, off, w0, w1);
-          else
-            store_o8<float>(p.o, off, w0, w1);
+        for (int h = 0; h < 2; ++h) {
+          if (p.o_dtype == GDN_DTYPE_F16) {
+            w0[h] = pack_f16x2(ov[0][2 * h], ov[0][2 * h + 1]);
+            w1[h] = pack_f16x2(ov[1][2 * h], ov[1][2 * h + 1]);
+          } else {
+            w0[h] = (uint32_t)float_to_bf16_bits(ov[0][2 * h]) | ((uint32_t)float_to_bf16_bits(ov[0][2 * h + 1]) << 16);
+            w1[h] = (uint32_t)float_to_bf16_bits(ov[1][2 * h]) | ((uint32_t)float_to_bf16_bits(ov[1][2 * h + 1]) << 16);
+          }
+          const auto sw = __builtin_amdgcn_permlane16_swap(w0[h], w1[h], false, false);
+          w0[h] = sw[0];
+          w1[h] = sw[1];
         }
-      } else if (p.o_dtype == GDN_DTYPE_F16) {
-        store_o<f16>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
-      } else if (p.o_dtype == GDN_DTYPE_BF16) {
-        store_o<bf16_t>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
+        if (t0 + orow < T)
+          *reinterpret_cast<uint4*>(o_lane + (int64_t)t0 * o_row_bytes) = uint4{w0[0], w0[1], w1[0], w1[1]};
       } else {
-        store_o<float>(p.o, o_col + n, p.so[1], t0, T, gq, ov);
+        const int64_t o_col = head_base(rs, hi, p.so) + v0 + 16 * c2 + 4 * gq;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int t = t0 + 16 * mt + n;
+          if (t < T) {
+            const int64_t off = o_col + (int64_t)t * p.so[1];
+            if (p.o_dtype == GDN_DTYPE_F16)
+              store_o4<f16>(p.o, off, ov[mt], p.o_vec);
+            else if (p.o_dtype == GDN_DTYPE_BF16)
+              store_o4<bf16_t>(p.o, off, ov[mt], p.o_vec);
+            else
+              store_o4<float>(p.o, off, ov[mt], p.o_vec);
+          }
+        }
       }
     };
-    wg_barrier();
-    for (int it = 0; it < nloc; ++it) {
-      if (it >= 1) store_chunk(it - 1);
+    // q rows of chunk it + 1 are read during chunk it (published two ahead)
+    auto load_q = [&](int it, f16x8 (&qA)[2][KB]) __attribute__((always_inline)) {
       const int sl = it % R;
-      f16x8 qA[2][KB];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) qA[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+    };
+    auto chunk = [&](int it, f16x8 (&qA)[2][KB], f16x8 (&qN)[2][KB]) __attribute__((always_inline)) {
+      OutOps oo;
+      if (it >= 1) load_o(it - 1, oo);
       f16x8 sOp[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sOp[kb] = s.so[it & 1][c2][kb][lane];
+      load_q(min(it + 1, nloc - 1), qN);
+      if (it >= 1) store_chunk(it - 1, oo);
       PS_BEGIN(qA[0][0], qA[1][0], sOp[0], sOp[KB - 1]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         f32x4 acc = z4;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) acc = M::mma(qA[mt][kb], sOp[kb], acc);
+        for (int kb = 0; kb < KB; ++kb) acc = M::mma(sOp[kb], qA[mt][kb], acc);
         oq[mt] = acc;
       }
       PS_END_A(oq[0], oq[1]);
       wg_barrier();
+    };
+    f16x8 qa[2][KB], qb[2][KB];
+    wg_barrier();
+    load_q(0, qa);
+    for (int it = 0; it < nloc; it += 2) {
+      chunk(it, qa, qb);
+      if (it + 1 < nloc) chunk(it + 1, qb, qa);
     }
-    store_chunk(nloc - 1);
+    {
+      OutOps oo;
+      load_o(nloc - 1, oo);
+      store_chunk(nloc - 1, oo);
+    }
     PS_RECORD(2, nloc, 2 * KB, 6);
   } else if (role == SR_PQK) {
     // ================================================================ PQK
+    // Chunk it + 1's q and k rows and gates are read into a second register
+    // set while chunk it computes (the LOAD wave publishes chunks two
+    // ahead), so no product waits on LDS.
+    const float one = opaque_one();
     PS_DECL;
-    wg_barrier();
-    for (int it = 0; it < nloc; ++it) {
+    struct PqkOps {
+      f16x8 qf[2][KB], kf[2][KB];
+      float bt[2];   // b log2(e) of rows t = 16 mt + n
+      f32x4 bj[2];   // of rows j = 16 a + 4 gq + i
+    };
+    auto read_ops = [&](int it, PqkOps& o) __attribute__((always_inline)) {
       const int sl = it % R;
       const float* bb = reinterpret_cast<const float*>(s.rec[it % RR] + R_B);
-      f16x8 qf[2][KB], kf[2][KB];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          qf[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
-          kf[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+          o.qf[mt][kb] = staged(s.rq[sl], 16 * mt + n, 4 * kb + gq);
+          o.kf[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
         }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        o.bt[mt] = bb[16 * mt + n];
+        o.bj[mt] = *reinterpret_cast<const f32x4*>(bb + 16 * mt + 4 * gq);
+      }
+    };
+    auto chunk = [&](int it, PqkOps& o, PqkOps& nx) __attribute__((always_inline)) {
+      read_ops(min(it + 1, nloc - 1), nx);  // the last chunk's again at the end
       // P^T tiles (rows j, columns t) = K Q^T: the tiles of rows j in
       // [0,16) and [16,32) of one column tile form one P operand
-      PS_BEGIN(qf[0][0], qf[1][0], kf[0][0], kf[1][0]);
+      PS_BEGIN(o.qf[0][0], o.qf[1][0], o.kf[0][0], o.kf[1][0]);
       f16x8 phs[2], pls[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         const int t = 16 * mt + n;
-        const float bt = bb[t];
         f32x4 pt[2] = {z4, z4};
 #pragma unroll
         for (int a = 0; a <= mt; ++a) {
           f32x4 acc = z4;
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) acc = M::mma(kf[a][kb], qf[mt][kb], acc);
-          const f32x4 bj4 = *reinterpret_cast<const f32x4*>(bb + 16 * a + 4 * gq);
+          for (int kb = 0; kb < KB; ++kb) acc = M::mma(o.kf[a][kb], o.qf[mt][kb], acc);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // mask folded into the exponent: 2^-inf = 0
-            const float x = t >= 16 * a + 4 * gq + i ? bt - bj4[i] : -__builtin_inff();
-            pt[a][i] = pin(acc[i] * fexp(x));
+            // e^{b_t - b_j} = 2^{(b_t - b_j) log2 e}; the mask folded into
+            // the exponent: 2^-inf = 0
+            const float x = t >= 16 * a + 4 * gq + i ? o.bt[mt] - o.bj[a][i] : -__builtin_inff();
+            pt[a][i] = pin(acc[i] * __builtin_amdgcn_exp2f(x));
           }
         }
         phs[mt] = M::from_acc(pt[0], pt[1]);
-        pls[mt] = split_lo(pt[0], pt[1], phs[mt]);
+        pls[mt] = split_lo_mix(pt[0], pt[1], phs[mt], one);
       }
       PS_END_A(phs[0], phs[1], pls[0], pls[1]);
 #pragma unroll
@@ -847,6 +932,13 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
         s.plo[it & 1][mt][lane] = pls[mt];
       }
       wg_barrier();
+    };
+    PqkOps oa, ob;
+    wg_barrier();
+    read_ops(0, oa);
+    for (int it = 0; it < nloc; it += 2) {
+      chunk(it, oa, ob);
+      if (it + 1 < nloc) chunk(it + 1, ob, oa);
     }
     PS_RECORD(3, nloc, 3 * KB, 0);
   } else {
@@ -996,9 +1088,12 @@ int scan32_launch(const GdnFwdParams& P, int bv, int seg_chunks, hipStream_t str
   const int64_t units = (int64_t)P.B * P.H * a.nv;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
   {
-    const int64_t eb = P.o_dtype == GDN_DTYPE_F32 ? 4 : 2;
-    a.o_vec = reinterpret_cast<uintptr_t>(P.o) % 16 == 0 && (P.o_stride[0] * eb) % 16 == 0 &&
-              (P.o_stride[1] * eb) % 16 == 0 && (P.o_stride[2] * eb) % 16 == 0;
+    // 16-byte stores of o: 8 consecutive 16-bit elements or 4 fp32 ones
+    // per lane (base 16-byte aligned, every stride a multiple of that many
+    // elements)
+    const int64_t per = P.o_dtype == GDN_DTYPE_F32 ? 4 : 8;
+    a.o_vec = reinterpret_cast<uintptr_t>(P.o) % 16 == 0 && P.o_stride[0] % per == 0 &&
+              P.o_stride[1] % per == 0 && P.o_stride[2] % per == 0;
   }
   // every sequence has at most ceil(T / C) chunks (the offsets are not read here)
   const int nchmax = (P.T + s32::C - 1) / s32::C;

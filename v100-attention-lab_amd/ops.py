@@ -307,7 +307,7 @@ def gdn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     """
     if _needs_grad(q, k, v, g, beta, h0):
         return _GdnFunction.apply(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype,
-                                  kernel, False, cu_seqlens, False)
+                                  kernel, False, cu_seqlens, False, max_segment_chunks)
     return _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel, False,
                 cu_seqlens, False, max_segment_chunks)
 
@@ -612,9 +612,9 @@ class _GdnFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
-                fs_vk, cu_seqlens, o_hf):
+                fs_vk, cu_seqlens, o_hf, seg_chunks=None):
         o, fs = _run(q, k, v, g, beta, h0, scale, chunk_size, block_v, output_dtype, kernel,
-                     fs_vk, cu_seqlens, o_hf)
+                     fs_vk, cu_seqlens, o_hf, seg_chunks)
         ctx.save_for_backward(q, k, v, g, beta, h0, cu_seqlens)
         ctx.scale, ctx.fs_vk, ctx.o_hf = scale, fs_vk, o_hf
         return o, fs
@@ -632,7 +632,7 @@ class _GdnFunction(torch.autograd.Function):
         need_dh0 = h0 is not None and ctx.needs_input_grad[5]
         dq, dk, dv, dg, dbeta, dh0 = gdn_bwd(q, k, v, g, beta, h0, do_bthv, dfs_kv, ctx.scale,
                                              cu_seqlens=cu, need_dh0=need_dh0)
-        return dq, dk, dv, dg, dbeta, dh0, None, None, None, None, None, None, None, None
+        return dq, dk, dv, dg, dbeta, dh0, None, None, None, None, None, None, None, None, None
 
 
 def _needs_grad(*ts) -> bool:
