@@ -243,8 +243,9 @@ int gdn_prep_launch(const GdnPrepParams* params, void* stream);
  *     dtype), dg, dbeta (g's / beta's dtypes): any strides.  dh0 [B,H,K,V]
  *     fp32 (nullable: not written).
  *   - d_final_state nullable (zero).  h0 nullable (zero).
- *   - workspace: device memory of at least gdn_bwd_workspace_size(...)
- *     bytes, 256-byte aligned, owned by the caller; its contents need no
+ *   - workspace: device memory of at least gdn_bwd_workspace_size_params()
+ *     bytes (gdn_bwd_workspace_size() is always enough), 256-byte aligned,
+ *     owned by the caller; its contents need no
  *     initialisation and are undefined afterwards.
  *   - Enqueues three kernels on `stream` (per-chunk record, the two state
  *     recurrences, per-chunk gradients); no allocation, no synchronisation. */
@@ -291,9 +292,18 @@ typedef struct GdnBwdParams {
   int64_t workspace_bytes;
 } GdnBwdParams;
 
-/* Bytes of workspace gdn_bwd_launch needs for these sizes (n_seq: the
- * number of sequences with cu_seqlens, else 0); -1 if unsupported. */
+/* Bytes of workspace that gdn_bwd_launch needs for these sizes whatever
+ * the dtypes (n_seq: the number of sequences with cu_seqlens, else 0); -1
+ * if unsupported. */
 int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq);
+
+/* Bytes of workspace gdn_bwd_launch needs for exactly these params (their
+ * sizes, dtypes, d_o alignment and cu_seqlens; pointers other than d_o and
+ * cu_seqlens are not read); -1 if unsupported.  With 16-bit q, k, v and dO
+ * of the same type, 4-byte aligned, the walks keep the chunk states in
+ * fp16 and their records hold T and the gates only: about 55 % of
+ * gdn_bwd_workspace_size at K = V = 128. */
+int64_t gdn_bwd_workspace_size_params(const GdnBwdParams* params);
 
 /* Enqueue the backward on `stream`; returns a GdnStatus / hipError_t. */
 int gdn_bwd_launch(const GdnBwdParams* params, void* stream);

@@ -346,13 +346,12 @@ def test_fla_surface_and_prep_reject_cpu_tensors(pkg):
 # --------------------------------------------------------------------------
 
 def test_bwd_workspace_size(lib):
-    # cfg2, per (chunk, head): the record (T, P, K K^T as C x C, W as C x K,
-    # four gate rows), S and dS' (K x V), u and du (C x V), all fp32 (the
-    # 16-bit walks store S and dS' in fp16 in the same space); then T
-    # diag(beta) and P (C x C) as fp16 pairs; then two state scales per walk
+    # cfg2, per (chunk, head), the larger layout (the fp32 walks): the
+    # record (T, P, K K^T as C x C, W as C x K, four gate rows), S and dS'
+    # (K x V), u and du (C x V), all fp32; then two state scales per walk
     # unit (sequence, head, 16-column slice)
     C, K, V, nrec = 32, 128, 128, 2 * (4096 // 32) * 16
-    want = nrec * 4 * ((3 * C * C + C * K + 4 * C) + 2 * K * V + 2 * C * V) + nrec * 2 * (4 * C * C)
+    want = nrec * 4 * ((3 * C * C + C * K + 4 * C) + 2 * K * V + 2 * C * V)
     want += 2 * (2 * 16 * V // 16) * 4
     got = lib.gdn_bwd_workspace_size(2, 4096, 16, 128, 128, 0)
     assert want <= got <= want + 7 * 256
@@ -360,6 +359,27 @@ def test_bwd_workspace_size(lib):
     assert lib.gdn_bwd_workspace_size(2, 4096, 16, 128, 120, 0) == -1
     # packed sequences: chunk slots ceil(T / C) + N
     assert lib.gdn_bwd_workspace_size(3, 100, 2, 64, 32, 3) > 0
+
+
+def test_bwd_workspace_size_params(lib, pkg):
+    """The workspace of the path the params select: the 16-bit walks keep
+    T and the gates in the record (C*C + 4C floats), S and dS' in fp16, and
+    add T diag(beta) and P as fp16 pairs; fp32 inputs (or a dO of another
+    dtype, or one not 4-byte aligned) take the general size."""
+    C, K, V, H = 32, 128, 128, 16
+    nrec = 2 * (4096 // C) * H
+    want16 = nrec * (4 * (C * C + 4 * C) + 2 * 2 * K * V + 4 * 2 * C * V + 2 * 4 * C * C) + 2 * (2 * H * V // 16) * 4
+    general = lib.gdn_bwd_workspace_size(2, 4096, H, K, V, 0)
+    P = _bwd_params(pkg._lib, B=2, T=4096, H=H, K=K, V=V, qkv_dtype=1, do_dtype=1)
+    got = lib.gdn_bwd_workspace_size_params(ctypes.byref(P))
+    assert want16 <= got <= want16 + 8 * 256
+    assert got < 0.6 * general
+    for kw in (dict(qkv_dtype=0, do_dtype=0), dict(qkv_dtype=1, do_dtype=0), dict(qkv_dtype=1, do_dtype=1, d_o=0x3002)):
+        P = _bwd_params(pkg._lib, B=2, T=4096, H=H, K=K, V=V, **kw)
+        assert lib.gdn_bwd_workspace_size_params(ctypes.byref(P)) == general
+    P = _bwd_params(pkg._lib, B=2, T=4096, H=H, K=256, V=V)
+    assert lib.gdn_bwd_workspace_size_params(ctypes.byref(P)) == -1
+    assert lib.gdn_bwd_workspace_size_params(None) == -1
 
 
 def _bwd_params(L, **kw):

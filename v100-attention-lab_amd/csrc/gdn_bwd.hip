@@ -108,6 +108,12 @@ struct Rec {
   static constexpr int SIZE = G + 4 * C;
 };
 inline int64_t rec_size(int K) { return 3 * C * C + (int64_t)C * K + 4 * C; }
+// The 16-bit walks' per-(slot, head) record, in floats: T as [C][C], then
+// the gates as in Rec (their products take P, K K^T and W from elsewhere).
+struct RecT {
+  static constexpr int T = 0, G = C * C;
+  static constexpr int SIZE = G + 4 * C;
+};
 // The same chunk's operands of the 16-bit recurrences, in halves: T diag(beta)
 // and P as [C][C], each an fp16 pair hi + lo.
 struct Rec16 {
@@ -296,7 +302,7 @@ constexpr int NRW = 2;  // records per wave
 
 template <typename TIn, int K>
 __global__ __launch_bounds__(256) void prep16_kernel(const BArgs p, int64_t nrec) {
-  using R = Rec<K>;
+  using R = RecT;
   constexpr int KB = K / 32;
   __shared__ __attribute__((aligned(16))) float s_at[4][NRW][C * C];  // A^T row-major
   __shared__ __attribute__((aligned(16))) float s_beta[4][NRW][C];
@@ -1093,7 +1099,7 @@ __device__ __forceinline__ void walk_forward16(const BArgs& p, FMem<K>& s, const
     dma_rows<C, 1>(rh + Rec16::TBH, C, C, d.th, 0, lane);
     dma_rows<C, 1>(rh + Rec16::TBL, C, C, d.tl, 0, lane);
     dma_v(reinterpret_cast<const uint16_t*>(vg) + (int64_t)cn * C * p.sv[1], p.sv[1], nval, d.v, lane);
-    if (lane < C) dma16(p.rec + ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + 4 * lane, &d.gv[0][0]);
+    if (lane < C) dma16(p.rec + ri * (int64_t)RecT::SIZE + RecT::G + 4 * lane, &d.gv[0][0]);
   };
   // the loader that fetched chunk cn, before the barrier that publishes it
   auto settle = [&](int cn, int b) __attribute__((always_inline)) {
@@ -1231,7 +1237,7 @@ __device__ __forceinline__ void walk_backward16(const BArgs& p, RMem<K>& s, cons
     dma_rows<C, 2>(rh + Rec16::PH, C, C, d.ph, lw, lane);
     dma_rows<C, 2>(rh + Rec16::PL, C, C, d.pl, lw, lane);
     dma_dot(reinterpret_cast<const uint16_t*>(dg) + (int64_t)cn * C * p.sdo[1], p.sdo[1], nval, d.dot, lw, lane);
-    if (lw == 0 && lane < C) dma16(p.rec + ri * (int64_t)Rec<K>::SIZE + Rec<K>::G + 4 * lane, &d.gv[0][0]);
+    if (lw == 0 && lane < C) dma16(p.rec + ri * (int64_t)RecT::SIZE + RecT::G + 4 * lane, &d.gv[0][0]);
   };
   // every wave, before the barrier that publishes chunk cn: its own copies
   auto settle = [&](int cn) __attribute__((always_inline)) {
@@ -1456,7 +1462,7 @@ struct alignas(16) GSmem {
 // whose waits cover exactly the step being staged.
 template <typename TIn, int K, int VS, bool ST16, int NVS>
 __global__ __launch_bounds__(NTG) void grad_kernel(const BArgs p) {
-  using R = Rec<K>;
+  using R = typename std::conditional<ST16, RecT, Rec<K>>::type;
   constexpr int RL = NTG / C;
   // fp16 inputs with fp16 states (no range shift): the V walk's products on
   // v_mfma_f32_16x16x32_f16, one 32-column step per product
@@ -2120,24 +2126,26 @@ struct Layout {
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-inline Layout layout(int B, int T, int H, int K, int V, int n_seq) {
+// w16: the 16-bit walks (T and the gates in the record, fp16 S and dS').
+inline Layout layout(int B, int T, int H, int K, int V, int n_seq, bool w16) {
   Layout L;
   const int64_t nch = (T + C - 1) / C;
   L.nslot = n_seq > 0 ? nch + n_seq : (int64_t)B * nch;
   const int64_t nr = L.nslot * H;
   int64_t off = 0;
   L.rec = off;
-  off = align256(off + nr * rec_size(K) * 4);
+  off = align256(off + nr * (w16 ? RecT::SIZE : rec_size(K)) * 4);
+  const int64_t sb = w16 ? 2 : 4;  // bytes per element of S and dS'
   L.ckS = off;
-  off = align256(off + nr * K * V * 4);
+  off = align256(off + nr * K * V * sb);
   L.ckD = off;
-  off = align256(off + nr * K * V * 4);
+  off = align256(off + nr * K * V * sb);
   L.uu = off;
   off = align256(off + nr * C * V * 4);
   L.du = off;
   off = align256(off + nr * C * V * 4);
   L.r16 = off;
-  off = align256(off + nr * rec16_size(K) * 2);
+  if (w16) off = align256(off + nr * rec16_size(K) * 2);
   L.scl = off;  // two floats per walk unit (B sequences x H x V / BV)
   off = align256(off + 2 * (int64_t)B * H * (V / BV) * 4);
   L.total = off;
@@ -2195,10 +2203,28 @@ int launch_t(const BArgs& a, int K, int64_t nrec, hipStream_t s) {
 
 using namespace gdn;
 
+// The 16-bit walks: 16-bit q, k, v with dO of the same type, whose rows
+// take 4-byte element-pair loads.
+static bool bwd_w16(const GdnBwdParams& P) {
+  return P.qkv_dtype != GDN_DTYPE_F32 && P.do_dtype == P.qkv_dtype &&
+         reinterpret_cast<uintptr_t>(P.d_o) % 4 == 0 && P.do_stride[0] % 2 == 0 && P.do_stride[1] % 2 == 0 &&
+         P.do_stride[2] % 2 == 0;
+}
+
 extern "C" int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq) {
   if (B <= 0 || T < 0 || H <= 0 || V <= 0 || V % bwd::BV != 0 || n_seq < 0) return -1;
   if (K != 32 && K != 64 && K != 128) return -1;
-  return bwd::layout(B, T, H, K, V, n_seq).total;
+  const int64_t a = bwd::layout(B, T, H, K, V, n_seq, false).total, b = bwd::layout(B, T, H, K, V, n_seq, true).total;
+  return a > b ? a : b;  // enough for either path
+}
+
+extern "C" int64_t gdn_bwd_workspace_size_params(const GdnBwdParams* prm) {
+  if (prm == nullptr) return -1;
+  const GdnBwdParams& P = *prm;
+  if (P.B <= 0 || P.T < 0 || P.H <= 0 || P.V <= 0 || P.V % bwd::BV != 0) return -1;
+  if (P.K != 32 && P.K != 64 && P.K != 128) return -1;
+  if (!valid_dtype(P.qkv_dtype) || !valid_dtype(P.do_dtype)) return -1;
+  return bwd::layout(P.B, P.T, P.H, P.K, P.V, P.cu_seqlens ? P.B : 0, bwd_w16(P)).total;
 }
 
 extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
@@ -2226,7 +2252,8 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   }
   const int64_t units = (int64_t)P.B * P.H * (P.V / bwd::BV);
   // B is the number of sequences when cu_seqlens is given (one packed batch)
-  const bwd::Layout L = bwd::layout(P.B, P.T, P.H, P.K, P.V, P.cu_seqlens ? P.B : 0);
+  const bool w16 = bwd_w16(P);
+  const bwd::Layout L = bwd::layout(P.B, P.T, P.H, P.K, P.V, P.cu_seqlens ? P.B : 0, w16);
   const int64_t nrec = L.nslot * P.H;
   if (2 * units > 0x7fffffffLL || nrec > 0x7fffffffLL || (int64_t)P.B * P.T * P.H * P.K >= (1LL << 40))
     return GDN_ERR_BAD_SHAPE;
@@ -2263,11 +2290,8 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   a.g_dtype = P.g_dtype; a.beta_dtype = P.beta_dtype; a.do_dtype = P.do_dtype;
   a.cu = P.cu_seqlens;
   a.xcd_remap = (units % 8 == 0) ? 1 : 0;
-  // fp16 pair recurrences: 16-bit q, k, v with dO of the same type, whose
-  // rows take 4-byte element-pair loads
-  a.w16 = P.qkv_dtype != GDN_DTYPE_F32 && P.do_dtype == P.qkv_dtype &&
-          reinterpret_cast<uintptr_t>(P.d_o) % 4 == 0 && P.do_stride[0] % 2 == 0 && P.do_stride[1] % 2 == 0 &&
-          P.do_stride[2] % 2 == 0;
+  // fp16 pair recurrences (the 16-bit walks)
+  a.w16 = w16;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nrec_launch = P.T > 0 ? nrec : 0;

@@ -567,16 +567,12 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
         do = do.contiguous()
     dev = q.device
     lib = _lib.load_library()
-    ws_bytes = lib.gdn_bwd_workspace_size(B, T, H, K, V, n_seq or 0)
-    if ws_bytes < 0:
-        raise ValueError(f"backward does not support B={B} T={T} H={H} K={K} V={V}")
     dq = torch.empty(q.shape, dtype=q.dtype, device=dev)
     dk = torch.empty(k.shape, dtype=k.dtype, device=dev)
     dv = torch.empty(v.shape, dtype=v.dtype, device=dev)
     dg = torch.empty(g.shape, dtype=g.dtype, device=dev)
     dbeta = torch.empty(beta.shape, dtype=beta.dtype, device=dev)
     dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=dev) if need_dh0 else None
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     P = _lib.GdnBwdParams()
     P.q, P.k, P.v, P.g, P.beta = q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr()
     P.h0 = h0.data_ptr() if h0 is not None else None
@@ -584,7 +580,6 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     P.d_final_state = dfinal.data_ptr() if dfinal is not None else None
     P.dq, P.dk, P.dv, P.dg, P.dbeta = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr()
     P.dh0 = dh0.data_ptr() if dh0 is not None else None
-    P.workspace, P.workspace_bytes = ws.data_ptr(), ws.numel()
     for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("dq", dq), ("dk", dk), ("dv", dv)):
         getattr(P, f"{name}_stride")[:] = t.stride()[:3]
     for name, t in (("g", g), ("beta", beta), ("dg", dg), ("dbeta", dbeta)):
@@ -599,6 +594,12 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     P.beta_dtype = _DTYPE_CODE[beta.dtype]
     P.do_dtype = _DTYPE_CODE[do.dtype]
     P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
+    # the workspace this call's path takes (the 16-bit walks need less)
+    ws_bytes = lib.gdn_bwd_workspace_size_params(ctypes.byref(P))
+    if ws_bytes < 0:
+        raise ValueError(f"backward does not support B={B} T={T} H={H} K={K} V={V}")
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    P.workspace, P.workspace_bytes = ws.data_ptr(), ws.numel()
     with torch.cuda.device(dev):
         status = lib.gdn_bwd_launch(ctypes.byref(P), torch.cuda.current_stream(dev).cuda_stream)
     if status != 0:
