@@ -48,7 +48,17 @@ CONFIGS = {
     # exploration only: the configs[4] shape in fp16 (64 heads on the
     # two-launch path)
     "cfg4_f16": (4, 4096, 16, 128, 128, torch.float16, 32, True),
+    # sweep only: the reference's own autotune shape (bench_gdn.py:120-121,
+    # B2 T2048 H8) and a K = V = 64 shape, both with fewer (b, h, 16-column)
+    # units than the 256 CUs
+    "ref_sweep": (2, 2048, 8, 128, 128, torch.float16, 32, False),
+    "k64": (2, 4096, 16, 64, 64, torch.float16, 32, False),
+    "k64_bf16": (2, 4096, 16, 64, 64, torch.bfloat16, 32, False),
+    # sweep only: the headline shape in bf16 (where the 16-bit input
+    # conversion weighs most)
+    "cfg2_bf16": (2, 4096, 16, 128, 128, torch.bfloat16, 32, False),
 }
+SWEEP_CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg4_f16", "ref_sweep", "k64", "k64_bf16", "cfg2_bf16")
 
 DTYPE_NAME = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
 
@@ -381,21 +391,38 @@ def phase_stamps(pkg, config):
                                    "window_cycles": float(r[:, 1].sum())}
     for ph in phases.values():
         ph["util"] = round(ph["busy_cycles"] / ph["window_cycles"], 4)
+        # the same against the nominal 16 cycles per v_mfma_f32_16x16x32_f16
+        # (2.5 PFLOP/s dense fp16 on 256 CUs x 4 SIMDs at 2.4 GHz)
+        ph["util_nominal16"] = round(ph["mfma"] * 16.0 / ph["window_cycles"], 4)
     scan_names = [n for n in phases if not n.startswith("records")]
     busy = sum(phases[n]["busy_cycles"] for n in scan_names)
     win = sum(phases[n]["window_cycles"] for n in scan_names)
     busy_all = busy + phases["records: K K^T, A"]["busy_cycles"]
     win_all = win + phases["records: K K^T, A"]["window_cycles"]
+    mfma_scan = sum(phases[n]["mfma"] for n in scan_names)
+    mfma_all = mfma_scan + phases["records: K K^T, A"]["mfma"]
     for ph in phases.values():
         ph["busy_cycles"] = round(ph["busy_cycles"])
         ph["window_cycles"] = round(ph["window_cycles"])
+    # per role of the scan: cycles in barriers (the LDS drain before each
+    # s_barrier and the wait for the other waves) and the loop's cycles, per
+    # chunk, averaged over the waves of the role
+    roles = {}
+    for role, name in ((1, "SCAN"), (2, "OUT"), (3, "PQK"), (4, "LOAD")):
+        d = scan[(scan[:, :, 0] == role) & (scan[:, :, 1] > 0)]
+        if len(d):
+            nch = float(d[:, 1].sum())
+            roles[name] = {"waves": int(len(d)), "barrier_cycles_per_chunk": round(float(d[:, 6].sum()) / nch, 1),
+                           "loop_cycles_per_chunk": round(float(d[:, 7].sum()) / nch, 1)}
     print(json.dumps({"metric": "MFMA utilisation of the contraction phases (s_memtime phase windows)",
                       "config": config, "B": B, "T": T, "H": H, "K": K, "V": V, "chunk_size": C,
                       "mfma_cycles_per_instruction": round(cyc_mfma, 3),
                       "stamped_ms_per_step": round(ms, 5),
                       "scan_contraction_util": round(busy / win, 4),
                       "all_contraction_util": round(busy_all / win_all, 4),
-                      "phases": phases}), flush=True)
+                      "scan_contraction_util_nominal16": round(mfma_scan * 16.0 / win, 4),
+                      "all_contraction_util_nominal16": round(mfma_all * 16.0 / win_all, 4),
+                      "phases": phases, "roles": roles}), flush=True)
 
 
 # (C, BV) combinations of the sweep: 32-row chunks take BV 16 or 32 on the
@@ -404,12 +431,12 @@ def phase_stamps(pkg, config):
 SWEEP = ((32, 16), (32, 32), (32, 64), (64, 16))
 
 
-def sweep(pkg, steps, warmup):
+def sweep(pkg, steps, warmup, names=SWEEP_CONFIGS):
     """Times every (C, BV) of SWEEP at every config (configs[2] with C = 64 is
     configs[2] as well) and prints one JSON line per config with the times
     and the launcher's automatic BV for 32-row chunks."""
     dev = torch.device("cuda:0")
-    for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg4_f16"):
+    for name in names:
         B, T, H, K, V, dtype, _, with_h0 = CONFIGS[name]
         q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, dtype, with_h0, dev)
         res = {}
@@ -437,6 +464,8 @@ def main():
                          "preparation; bwd: only the backward (gdn_bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the C=64 and cold-cache lines")
+    ap.add_argument("--sweep-configs", default=None,
+                    help="comma-separated configs for --sweep (default: all of SWEEP_CONFIGS)")
     ap.add_argument("--sweep", action="store_true",
                     help="time every (chunk, block_v) at every config (one JSON line per config)")
     ap.add_argument("--phase-stamps", action="store_true",
@@ -480,7 +509,8 @@ def main():
         phase_stamps(pkg, args.config)
         return
     if args.sweep:
-        sweep(pkg, min(args.steps, 50), min(args.warmup, 10))
+        sweep(pkg, min(args.steps, 50), min(args.warmup, 10),
+              args.sweep_configs.split(",") if args.sweep_configs else SWEEP_CONFIGS)
         return
     dev = torch.device("cuda:0")
     B, T, H, K, V, dtype, C, with_h0 = CONFIGS[args.config]

@@ -195,6 +195,21 @@ __device__ __forceinline__ void ps_record(int wave, int lane, unsigned long long
     d[0] = role; d[1] = n; d[2] = wa; d[3] = wb; d[4] = ma; d[5] = mb;
   }
 }
+// slots 6 and 7: the cycles this wave spent in its barriers (from just
+// before the LDS drain that precedes each s_barrier to its release) and the
+// cycles from its first barrier's release to the end of its chunk loop
+__device__ __forceinline__ void ps_record_bar(int wave, int lane, unsigned long long role, unsigned long long n,
+                                              unsigned long long bar, unsigned long long loop) {
+  if (lane == 0 && blockIdx.x < PS_WG && wave < PS_WAVES) {
+    unsigned long long* d = g_phase_scan + ((int64_t)blockIdx.x * PS_WAVES + wave) * PS_SLOTS;
+    d[0] = role; d[1] = n; d[6] = bar; d[7] = loop;
+  }
+}
+__device__ __forceinline__ unsigned long long ps_now() {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) :: "memory");
+  return t;
+}
 #define PS_DECL unsigned long long ps_a = 0, ps_b = 0, ps_t0 = 0
 #define PS_BEGIN(...) ps_t0 = ps_stamp(__VA_ARGS__)
 #define PS_END_A(...) ps_a += ps_stamp(__VA_ARGS__) - ps_t0
@@ -513,6 +528,25 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#ifdef GDN_PHASE_STAMPS
+  // the workgroup barrier, timed (stamps build only): the time in each
+  // barrier after the first, and the loop's cycles from the first
+  // barrier's release
+  unsigned long long ps_bar = 0, ps_loop0 = 0;
+  int ps_nb = 0;
+  auto wg_barrier = [&]() __attribute__((always_inline)) {
+    const unsigned long long t0 = ps_now();
+    s32::wg_barrier();
+    const unsigned long long t1 = ps_now();
+    if (ps_nb++ == 0)
+      ps_loop0 = t1;
+    else
+      ps_bar += t1 - t0;
+  };
+#define PS_RECORD_BAR(role) ps_record_bar(wave, tid & 63, role, nloc, ps_bar, ps_now() - ps_loop0)
+#else
+#define PS_RECORD_BAR(role)
+#endif
   const int lane = tid & 63;
   const int n = lane & 15;
   const int gq = lane >> 4;
@@ -734,6 +768,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       if (it + 1 < nloc) chunk(it + 1, ob, oa);
     }
     PS_RECORD(1, nloc, 2 * KB + 2 + KT, 0);
+    PS_RECORD_BAR(1);
     float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
 #pragma unroll
     for (int r = 0; r < KT; ++r)
@@ -780,10 +815,10 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       o.ebt[1] = ebr[16 + n];
     };
     auto store_chunk = [&](int it, const OutOps& o) __attribute__((always_inline)) {
-      const f16x8 uh = M::from_acc(o.u0, o.u1);
-      const f16x8 ul = split_lo_mix(o.u0, o.u1, uh, one);
+      f16x8 uh = M::from_acc(o.u0, o.u1);
+      f16x8 ul = split_lo_mix(o.u0, o.u1, uh, one);
       f32x4 ov[2];
-      PS_BEGIN(uh, ul, o.pAs[1], o.pLs[1]);
+      PS_BEGIN(uh, ul);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         f32x4 pu = M::mma(ul, o.pAs[mt], z4);
@@ -871,6 +906,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       store_chunk(nloc - 1, oo);
     }
     PS_RECORD(2, nloc, 2 * KB, 6);
+    PS_RECORD_BAR(2);
   } else if (role == SR_PQK) {
     // ================================================================ PQK
     // Chunk it + 1's q and k rows and gates are read into a second register
@@ -941,6 +977,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       if (it + 1 < nloc) chunk(it + 1, ob, oa);
     }
     PS_RECORD(3, nloc, 3 * KB, 0);
+    PS_RECORD_BAR(3);
   } else {
     // =============================================================== LOAD
     // chunk j -> slots j % R (q, k, v) and j % RR (record).  Rows past the
@@ -1032,6 +1069,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       convert(it + 2);
       wg_barrier();
     }
+    PS_RECORD_BAR(4);
   }
 }
 
