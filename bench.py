@@ -251,18 +251,21 @@ def cpu_baseline(B, T, H, K, V, dtype, C, budget_s=12.0):
 
 # The sources the 32-row forward's two launches are built from (the record
 # and scan kernels, the headers they include, the dispatch that launches
-# them): the code a forward traffic profile measures.
+# them): the code a forward traffic profile measures.  64-row chunks run the
+# record and scan kernels of gdn_fwd_c64.hip (FWD_SOURCES_C64).
 FWD_SOURCES = ("gdn_fwd_api.hip", "gdn_fwd_kernel.h", "gdn_fwd_pipe.h", "gdn_fwd_scan32.hip")
+FWD_SOURCES_C64 = ("gdn_fwd_api.hip", "gdn_fwd_kernel.h", "gdn_tiles_f16.h", "gdn_fwd_c64.hip")
 
 
-def sources_digest():
-    """sha256 (first 16 hex digits) over the forward's HIP sources
-    (FWD_SOURCES), names and bytes: it identifies the build a traffic profile
-    was measured on, also on a machine without the git history."""
+def sources_digest(config="cfg2"):
+    """sha256 (first 16 hex digits) over the HIP sources of the forward path
+    that `config` runs (FWD_SOURCES, or FWD_SOURCES_C64 for 64-row chunks),
+    names and bytes: it identifies the build a traffic profile was measured
+    on, also on a machine without the git history."""
     import hashlib
     d = os.path.join(REPO, "v100-attention-lab_amd", "csrc")
     h = hashlib.sha256()
-    for name in FWD_SOURCES:
+    for name in FWD_SOURCES_C64 if CONFIGS[config][6] == 64 else FWD_SOURCES:
         h.update(name.encode())
         with open(os.path.join(d, name), "rb") as f:
             h.update(f.read())
@@ -278,7 +281,7 @@ def load_traffic(config):
     (profiles/gdn_fwd_<config>_traffic.json) and a note on where they come
     from.  The bytes are None when no profile exists or when it was taken on
     other kernel sources than the ones present (its ``sources`` digest differs
-    from ``sources_digest()``): a stale figure is not reported as this
+    from ``sources_digest(config)``): a stale figure is not reported as this
     build's."""
     try:
         with open(traffic_path(config)) as f:
@@ -286,9 +289,25 @@ def load_traffic(config):
     except (OSError, ValueError):
         return None, "no traffic profile for this config"
     where = f"profiles/gdn_fwd_{config}_traffic.json, commit {rec.get('commit', '?')}"
-    if rec.get("sources") != sources_digest():
+    if rec.get("sources") != sources_digest(config):
         return None, f"stale: {where} measured other kernel sources"
     return rec.get("hbm_bytes_per_launch"), where
+
+
+def is_library_kernel(name):
+    """A kernel of this library, as rocprofv3 names it (mangled or
+    demangled)."""
+    return name.startswith("_ZN3gdn") or name.startswith("void gdn::")
+
+
+def segments_per_launch(config):
+    """Segments one forward call at `config` runs in (each launches the
+    record and the scan kernel once): the records of at most 256 chunks of
+    32 rows, or 64 chunks of 64 rows, per sequence and head
+    (gdn_fwd_api.hip kSegChunks, gdn_fwd_kernel.h kSegC64)."""
+    B, T, H, K, V, dtype, C, with_h0 = CONFIGS[config]
+    nch = -(-T // C)
+    return -(-nch // (256 if C == 32 else 64))
 
 
 def write_traffic(config, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
@@ -296,9 +315,11 @@ def write_traffic(config, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
     ``--pmc`` CSVs: FETCH_SIZE and WRITE_SIZE of a ``bench.py --steps 5
     --warmup 1 --no-extras --no-cpu-baseline`` run, and the same two counters
     of ``bench.py --calibrate-copy`` (a 256 MiB copy, which gives each
-    counter's scale).  Every library kernel (``gdn::`` names) of the run is
-    one launch's share: per kernel the median KiB per dispatch, summed over
-    the kernels, scaled.  Run where the git history is, after the GPU run."""
+    counter's scale).  Each library kernel (``gdn::`` names, mangled or not)
+    runs once per segment of a launch: per kernel the median KiB per
+    dispatch times the segments per launch (segments_per_launch), summed
+    over the kernels, scaled.  Run where the git history is, after the GPU
+    run."""
     import csv
     import subprocess
 
@@ -314,17 +335,18 @@ def write_traffic(config, fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
         return (256 << 10) / max(copy)  # the 256 MiB copy in KiB / the counter's KiB
 
     fetch, write = medians(fetch_csv), medians(write_csv)
-    kernels = sorted(k for k in fetch if k.startswith("_ZN3gdn"))
+    kernels = sorted(k for k in fetch if is_library_kernel(k))
     fs, ws = scale(copy_fetch_csv), scale(copy_write_csv)
+    nseg = segments_per_launch(config)
     per_kernel = {k: {"fetch_kib": fetch[k], "write_kib": write.get(k)} for k in kernels}
-    rd = sum(fetch[k] for k in kernels) * 1024 * fs
-    wr = sum(write[k] for k in kernels) * 1024 * ws
+    rd = sum(fetch[k] for k in kernels) * nseg * 1024 * fs
+    wr = sum(write[k] for k in kernels) * nseg * 1024 * ws
     B, T, H, K, V, dtype, C, with_h0 = CONFIGS[config]
     alg = algorithmic_bytes(B, T, H, K, V, torch.finfo(dtype).bits // 8, with_h0)
     git = lambda *a: subprocess.run(["git", *a], cwd=REPO, capture_output=True, text=True).stdout.strip()
     rec = {"config": config, "commit": git("rev-parse", "--short", "HEAD"),
            "uncommitted_changes": bool(git("status", "--porcelain", "--", "v100-attention-lab_amd/csrc")),
-           "sources": sources_digest(), "kernels": per_kernel,
+           "sources": sources_digest(config), "kernels": per_kernel, "dispatches_per_kernel_per_launch": nseg,
            "fetch_scale": round(fs, 6), "write_scale": round(ws, 6),
            "bytes_read_per_launch": round(rd), "bytes_written_per_launch": round(wr),
            "hbm_bytes_per_launch": round(rd + wr), "algorithmic_bytes_per_launch": alg,

@@ -465,15 +465,19 @@ def test_traffic_profile_tracks_sources(monkeypatch):
     spec = importlib.util.spec_from_file_location("_bench", os.path.join(REPO, "bench.py"))
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    with open(bench.traffic_path("cfg2")) as f:
-        rec = json.load(f)
-    assert rec["sources"] and rec["commit"] and rec["kernels"]
-    assert all(k.startswith("_ZN3gdn") for k in rec["kernels"])
-    nbytes, note = bench.load_traffic("cfg2")
-    if rec["sources"] == bench.sources_digest():
-        assert nbytes == rec["hbm_bytes_per_launch"] and rec["commit"] in note
-    else:
-        assert nbytes is None and note.startswith("stale")
-    monkeypatch.setattr(bench, "sources_digest", lambda: "0" * 16)
+    for config in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg2_c64"):
+        with open(bench.traffic_path(config)) as f:
+            rec = json.load(f)
+        assert rec["config"] == config and rec["sources"] and rec["commit"] and rec["kernels"]
+        assert rec["kernels"] and all(bench.is_library_kernel(k) for k in rec["kernels"])
+        assert rec["dispatches_per_kernel_per_launch"] == bench.segments_per_launch(config)
+        nbytes, note = bench.load_traffic(config)
+        if rec["sources"] == bench.sources_digest(config):
+            assert nbytes == rec["hbm_bytes_per_launch"] and rec["commit"] in note
+        else:
+            assert nbytes is None and note.startswith("stale")
+    # the 64-row path's digest covers its own kernel file, not the 32-row one's
+    assert bench.sources_digest("cfg2_c64") != bench.sources_digest("cfg2")
+    monkeypatch.setattr(bench, "sources_digest", lambda config: "0" * 16)
     nbytes, note = bench.load_traffic("cfg2")
     assert nbytes is None and note.startswith("stale")
