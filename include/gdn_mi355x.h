@@ -247,8 +247,17 @@ int gdn_prep_launch(const GdnPrepParams* params, void* stream);
  *     bytes (gdn_bwd_workspace_size() is always enough), 256-byte aligned,
  *     owned by the caller; its contents need no
  *     initialisation and are undefined afterwards.
- *   - Enqueues three kernels on `stream` (per-chunk record, the two state
- *     recurrences, per-chunk gradients); no allocation, no synchronisation. */
+ *   - One pass enqueues three kernels on `stream` (per-chunk record, the two
+ *     state recurrences, per-chunk gradients); no allocation, no
+ *     synchronisation.  It keeps every chunk's state and state gradient in
+ *     the workspace (about 108 KB per chunk and head with 16-bit inputs at
+ *     K = V = 128).  A batch without cu_seqlens whose workspace holds fewer
+ *     chunks runs in segments of as many chunks as it holds, last segment
+ *     first: one forward call per earlier segment (gdn_fwd_launch, o into
+ *     the workspace) leaves the fp32 state at each segment start, and each
+ *     segment's backward passes the gradient of its initial state to the
+ *     segment before.  The default sizes hold 256 chunks per sequence, so
+ *     the workspace is bounded in T. */
 typedef struct GdnBwdParams {
   const void* q;
   const void* k;
@@ -294,7 +303,8 @@ typedef struct GdnBwdParams {
 
 /* Bytes of workspace that gdn_bwd_launch needs for these sizes whatever
  * the dtypes (n_seq: the number of sequences with cu_seqlens, else 0); -1
- * if unsupported. */
+ * if unsupported.  Without cu_seqlens, at most 256 chunks (8192 rows) per
+ * sequence at a time. */
 int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq);
 
 /* Bytes of workspace gdn_bwd_launch needs for exactly these params (their
@@ -302,8 +312,15 @@ int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq);
  * cu_seqlens are not read); -1 if unsupported.  With 16-bit q, k, v and dO
  * of the same type, 4-byte aligned, the walks keep the chunk states in
  * fp16 and their records hold T and the gates only: about 55 % of
- * gdn_bwd_workspace_size at K = V = 128. */
+ * gdn_bwd_workspace_size at K = V = 128.  Without cu_seqlens, at most 256
+ * chunks per sequence at a time. */
 int64_t gdn_bwd_workspace_size_params(const GdnBwdParams* params);
+
+/* As gdn_bwd_workspace_size_params, for segments of at most seg_chunks
+ * chunks (>= 1; ignored with cu_seqlens).  No counterpart in the reference
+ * (no backward there); for callers that trade time (one more forward pass
+ * over all but the last segment) for memory. */
+int64_t gdn_bwd_segment_workspace_size(const GdnBwdParams* params, int seg_chunks);
 
 /* Enqueue the backward on `stream`; returns a GdnStatus / hipError_t. */
 int gdn_bwd_launch(const GdnBwdParams* params, void* stream);

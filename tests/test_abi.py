@@ -382,6 +382,35 @@ def test_bwd_workspace_size_params(lib, pkg):
     assert lib.gdn_bwd_workspace_size_params(None) == -1
 
 
+def test_bwd_workspace_bounded_in_t(lib, pkg):
+    """Without cu_seqlens the default workspace holds at most 256 chunks per
+    sequence: at cfg3's length (T = 16384, 512 chunks) it is the 8192-row
+    layout plus three fp32 states (the checkpoint at the second segment's
+    start and the two carried state gradients); the one-pass layout grows
+    with T.  Packed sequences keep the one-pass layout."""
+    H, K, V = 16, 128, 128
+    state = 2 * H * K * V * 4
+    sz = lambda **kw: lib.gdn_bwd_workspace_size_params(ctypes.byref(_bwd_params(pkg._lib, **kw)))
+    seg = lambda n, **kw: lib.gdn_bwd_segment_workspace_size(ctypes.byref(_bwd_params(pkg._lib, **kw)), n)
+    w8 = sz(B=2, T=8192, H=H, K=K, V=V)
+    assert sz(B=2, T=16384, H=H, K=K, V=V) == w8 + 3 * state
+    assert sz(B=2, T=65536, H=H, K=K, V=V) == w8 + 9 * state
+    assert seg(10 ** 6, B=2, T=16384, H=H, K=K, V=V) > 1.99 * w8
+    assert seg(256, B=2, T=16384, H=H, K=K, V=V) == w8 + 3 * state
+    # shorter segments take less, until the checkpoints (one state per
+    # segment) outweigh the layout
+    assert seg(64, B=2, T=16384, H=H, K=K, V=V) < seg(128, B=2, T=16384, H=H, K=K, V=V) < w8
+    assert seg(4, B=2, T=16384, H=H, K=K, V=V) > seg(8, B=2, T=16384, H=H, K=K, V=V)
+    assert seg(0, B=2, T=16384, H=H, K=K, V=V) == -1
+    # the dtype-free size is bounded the same way
+    assert lib.gdn_bwd_workspace_size(2, 65536, H, K, V, 0) < 1.03 * lib.gdn_bwd_workspace_size(2, 8192, H, K, V, 0)
+    # packed sequences (B of them in T rows): one pass, whatever the
+    # segment length asked for
+    packed = sz(B=2, T=16384, H=H, K=K, V=V, cu_seqlens=0x2000)
+    assert packed > 1.99 * sz(B=1, T=8192, H=H, K=K, V=V)
+    assert seg(4, B=2, T=16384, H=H, K=K, V=V, cu_seqlens=0x2000) == packed
+
+
 def _bwd_params(L, **kw):
     P = L.GdnBwdParams()
     fake = 0x1000  # never dereferenced: every case below returns before a launch

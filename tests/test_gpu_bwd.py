@@ -171,6 +171,76 @@ def test_bwd_full_size_one_head(pkg, cuda):
     _compare(mine, want, torch.float16, "cfg2 head (1,5)")
 
 
+@pytest.mark.parametrize("dtype,seg", [(torch.float32, 1), (torch.float32, 3), (torch.float16, 2),
+                                       (torch.float16, 4), (torch.bfloat16, 3)])
+def test_bwd_segments_vs_autograd(pkg, cuda, dtype, seg):
+    """A workspace of `seg` chunks per sequence: T = 300 (10 chunks, the
+    last partial) runs as ceil(10 / seg) segments, the states at their
+    starts from forward calls and the state gradient carried backwards.
+    The gradients match the oracle at the one-pass tolerances, and the
+    one-pass call within the same bound."""
+    B, H, T, K, V = 2, 2, 300, 64, 32
+    q, k, v, g, beta, h0, do, dfin = _inputs(B, T, H, K, V, dtype, seed=11 + seg)
+    d = lambda t: t.to(cuda)
+    print(f"[bwd] segments of {seg} chunks, {dtype}", flush=True)
+    got = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=0.8,
+                      max_segment_chunks=seg)
+    one = pkg.gdn_bwd(d(q), d(k), d(v), d(g), d(beta), d(h0), d(do), d(dfin), scale=0.8)
+    torch.cuda.synchronize()
+    want = ref.recurrent_grads(q, k, v, beta, g, h0, do, dfin, scale=0.8)
+    order = lambda r: (r[0], r[1], r[2], r[4], r[3], r[5])   # -> dq dk dv dbeta dg dh0
+    _compare(order(got), want, dtype, f"{dtype} segments of {seg}")
+    _compare(order(got), tuple(t.cpu().double() for t in order(one)), dtype, f"{dtype} segments vs one pass")
+
+
+def test_bwd_cfg3_length_segmented(pkg, cuda):
+    """cfg3's length (fp16 B2 H16 T16384 K=V=128, 512 chunks): the default
+    workspace holds 256 chunks per sequence, so the backward runs as two
+    segments.  That workspace is the 8192-row one plus three fp32 states,
+    under half the one-pass size; the allocator grows by no more than the
+    outputs and that workspace over the call; head (1, 5) matches the
+    oracle's fp64 chunked backward."""
+    import ctypes
+    B, T, H, K, V = 2, 16384, 16, 128, 128
+    q, k, v, g, beta, _ = ref.make_inputs_baseline(B, T, H, K, V, seed=0)
+    gen = torch.Generator().manual_seed(2)
+    do = torch.randn(B, T, H, V, generator=gen).half()
+    dq_, dk_, dv_, dg_, db_, do_ = (t.to(cuda) for t in (q, k, v, g, beta, do))
+    L = pkg._lib
+    lib = L.load_library()
+
+    def ws(rows, seg=None):
+        P = L.GdnBwdParams()
+        P.B, P.T, P.H, P.K, P.V = B, rows, H, K, V
+        P.qkv_dtype, P.g_dtype, P.beta_dtype, P.do_dtype = 1, 0, 0, 1
+        P.d_o = do_.data_ptr()
+        P.do_stride[:] = do_.stride()[:3]
+        if seg is None:
+            return lib.gdn_bwd_workspace_size_params(ctypes.byref(P))
+        return lib.gdn_bwd_segment_workspace_size(ctypes.byref(P), seg)
+
+    state = B * H * K * V * 4
+    bound = ws(8192) + 3 * state
+    assert ws(T) == bound and bound < 0.51 * ws(T, 10 ** 6)
+    print(f"[bwd] cfg3 length, workspace {bound / 2**20:.0f} MiB", flush=True)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(cuda)
+    base = torch.cuda.memory_allocated(cuda)
+    got = pkg.gdn_bwd(dq_, dk_, dv_, dg_, db_, None, do_, None, scale=1.0, need_dh0=False)
+    torch.cuda.synchronize()
+    grown = torch.cuda.max_memory_allocated(cuda) - base
+    outs = sum(t.numel() * t.element_size() for t in got if t is not None)
+    assert grown <= outs + bound + (2 << 20), (grown, outs, bound)
+    for t in got[:5]:
+        assert torch.isfinite(t.float()).all()
+    b, h = 1, 5
+    sel = lambda t: t[b:b + 1, :, h:h + 1]
+    want = ref.chunked_bwd(sel(q), sel(k), sel(v), sel(beta), sel(g), None, sel(do), None)
+    mine = (sel(got[0].cpu()), sel(got[1].cpu()), sel(got[2].cpu()), sel(got[4].cpu()),
+            sel(got[3].cpu()), None)
+    _compare(mine, want, torch.float16, "cfg3 length head (1,5)")
+
+
 def test_autograd_fla_varlen_bf16(pkg, cuda):
     """loss.backward() through FLA's varlen call (bf16, initial_state and
     final-state gradient): every sequence's gradients match the oracle's."""

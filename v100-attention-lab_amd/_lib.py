@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "gdn_prep_launch",
     "gdn_bwd_workspace_size",
     "gdn_bwd_workspace_size_params",
+    "gdn_bwd_segment_workspace_size",
     "gdn_bwd_launch",
     "gdn_fwd_launch_noalloc",
     "gdn_fwd_scratch_bytes",
@@ -176,6 +177,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         lib.gdn_bwd_workspace_size.restype = ctypes.c_int64
         lib.gdn_bwd_workspace_size_params.argtypes = [ctypes.POINTER(GdnBwdParams)]
         lib.gdn_bwd_workspace_size_params.restype = ctypes.c_int64
+        lib.gdn_bwd_segment_workspace_size.argtypes = [ctypes.POINTER(GdnBwdParams), ctypes.c_int]
+        lib.gdn_bwd_segment_workspace_size.restype = ctypes.c_int64
         lib.gdn_fwd_abi_version.argtypes = []
         lib.gdn_fwd_abi_version.restype = ctypes.c_int
         ver = lib.gdn_fwd_abi_version()

@@ -2211,25 +2211,159 @@ static bool bwd_w16(const GdnBwdParams& P) {
          P.do_stride[2] % 2 == 0;
 }
 
+namespace gdn {
+namespace bwd {
+
+// Segments.  The workspace of one pass holds every chunk's S, dS', u and du
+// (about 108 KB per (chunk, head) with the 16-bit walks at K = V = 128), so
+// it grows with T.  A dense batch of more than kSegChunks chunks per
+// sequence runs in segments of L chunks instead, last segment first:
+//   1. a forward pass over segments 0 .. n-2 (gdn_fwd_launch, one call per
+//      segment, o into scratch) leaves the fp32 state at the start of every
+//      later segment (the checkpoints);
+//   2. segment j's backward starts from checkpoint j (h0 for j = 0) and takes
+//      as the gradient of its final state the gradient of its successor's
+//      initial state (d_final_state for the last segment); its dh0 is
+//      carried to segment j - 1 (the caller's dh0 for j = 0).
+// The chunk gradients are independent given S and dS' at the segment ends,
+// so the segments add up to the one-pass backward.  The workspace is one
+// segment's layout (the forward pass's records and o scratch reuse it) plus
+// n + 1 states of B H K V floats.  The segment length is what the caller's
+// workspace holds, as for the forward.
+constexpr int64_t kSegChunks = 256;
+
+struct SegPlan {
+  int64_t L = 0, nseg = 0;  // chunks per segment, segments
+  int64_t region = 0;       // one segment's layout, or the forward pass's scratch
+  int64_t fwd_ws = 0;       // forward workspace, at offset 0 of the region
+  int64_t fwd_o = 0;        // forward o scratch offset
+  int64_t state_bytes = 0;  // one fp32 [B, H, K, V] state, 256-byte aligned
+  int64_t ckpt = 0;         // nseg - 1 checkpoints
+  int64_t carry = 0;        // two state gradients (in, out)
+  int64_t total = 0;
+};
+
+// Forward params over rows [t0, t0 + Tn) of P's inputs, o into `o` (dense,
+// the input dtype), the state from h0 (h0_stride) into fs (dense).
+inline GdnFwdParams fwd_params(const GdnBwdParams& P, int64_t t0, int Tn, const float* h0, const int64_t* h0s,
+                               float* fs, void* o) {
+  GdnFwdParams f = {};
+  const int eq = elem_bytes(P.qkv_dtype), eg = elem_bytes(P.g_dtype), eb = elem_bytes(P.beta_dtype);
+  auto off = [](const void* p, int64_t t0, const int64_t* st, int e) {
+    return p ? static_cast<const void*>(static_cast<const char*>(p) + t0 * st[1] * e) : nullptr;
+  };
+  f.q = off(P.q, t0, P.q_stride, eq);
+  f.k = off(P.k, t0, P.k_stride, eq);
+  f.v = off(P.v, t0, P.v_stride, eq);
+  f.g = off(P.g, t0, P.g_stride, eg);
+  f.beta = off(P.beta, t0, P.beta_stride, eb);
+  f.h0 = h0;
+  f.o = o;
+  f.final_state = fs;
+  for (int d = 0; d < 3; ++d) {
+    f.q_stride[d] = P.q_stride[d];
+    f.k_stride[d] = P.k_stride[d];
+    f.v_stride[d] = P.v_stride[d];
+    f.g_stride[d] = P.g_stride[d];
+    f.beta_stride[d] = P.beta_stride[d];
+  }
+  f.o_stride[0] = (int64_t)Tn * P.H * P.V;
+  f.o_stride[1] = (int64_t)P.H * P.V;
+  f.o_stride[2] = P.V;
+  for (int d = 0; d < 4; ++d) f.h0_stride[d] = h0s ? h0s[d] : 0;
+  f.fs_stride[0] = (int64_t)P.H * P.K * P.V;
+  f.fs_stride[1] = (int64_t)P.K * P.V;
+  f.fs_stride[2] = P.V;
+  f.fs_stride[3] = 1;
+  f.B = P.B;
+  f.T = Tn;
+  f.H = P.H;
+  f.K = P.K;
+  f.V = P.V;
+  f.scale = 1.f;
+  f.chunk_size = C;
+  f.qkv_dtype = P.qkv_dtype;
+  f.g_dtype = P.g_dtype;
+  f.beta_dtype = P.beta_dtype;
+  f.o_dtype = P.qkv_dtype;
+  return f;
+}
+
+// The workspace of a dense call run in segments of L chunks (L >= the
+// call's chunk count: one pass, the plain layout).
+inline SegPlan seg_plan(const GdnBwdParams& P, bool w16, int64_t L) {
+  SegPlan sp;
+  const int64_t nch = (P.T + C - 1) / C;
+  sp.L = L < nch ? L : nch;
+  if (sp.L < 1) sp.L = 1;
+  sp.nseg = nch > 0 ? (nch + sp.L - 1) / sp.L : 1;
+  const int Tseg = (int)(sp.nseg > 1 ? sp.L * C : P.T);
+  const int64_t lay = layout(P.B, Tseg, P.H, P.K, P.V, 0, w16).total;
+  if (sp.nseg == 1) {
+    sp.region = sp.total = lay;
+    return sp;
+  }
+  GdnFwdParams f = fwd_params(P, 0, Tseg, nullptr, nullptr, nullptr, nullptr);
+  sp.fwd_ws = align256(gdn_fwd_workspace_size(&f));
+  sp.fwd_o = sp.fwd_ws;
+  const int64_t need = sp.fwd_o + align256((int64_t)P.B * Tseg * P.H * P.V * elem_bytes(P.qkv_dtype));
+  sp.region = lay > need ? lay : need;
+  sp.state_bytes = align256((int64_t)P.B * P.H * P.K * P.V * 4);
+  sp.ckpt = sp.region;
+  sp.carry = sp.ckpt + (sp.nseg - 1) * sp.state_bytes;
+  sp.total = sp.carry + 2 * sp.state_bytes;
+  return sp;
+}
+
+}  // namespace bwd
+}  // namespace gdn
+
 extern "C" int64_t gdn_bwd_workspace_size(int B, int T, int H, int K, int V, int n_seq) {
   if (B <= 0 || T < 0 || H <= 0 || V <= 0 || V % bwd::BV != 0 || n_seq < 0) return -1;
   if (K != 32 && K != 64 && K != 128) return -1;
-  const int64_t a = bwd::layout(B, T, H, K, V, n_seq, false).total, b = bwd::layout(B, T, H, K, V, n_seq, true).total;
-  return a > b ? a : b;  // enough for either path
+  const int64_t nch = ((int64_t)T + bwd::C - 1) / bwd::C;
+  if (n_seq > 0 || nch <= bwd::kSegChunks) {
+    const int64_t a = bwd::layout(B, T, H, K, V, n_seq, false).total, b = bwd::layout(B, T, H, K, V, n_seq, true).total;
+    return a > b ? a : b;  // enough for either path
+  }
+  // segments of kSegChunks chunks: the largest plan over the dtypes
+  int64_t best = 0;
+  for (int dt : {GDN_DTYPE_F32, GDN_DTYPE_F16, GDN_DTYPE_BF16}) {
+    GdnBwdParams P = {};
+    P.B = B; P.T = T; P.H = H; P.K = K; P.V = V;
+    P.qkv_dtype = dt; P.g_dtype = GDN_DTYPE_F32; P.beta_dtype = GDN_DTYPE_F32;
+    for (bool w16 : {false, true}) {
+      if (w16 && dt == GDN_DTYPE_F32) continue;
+      const int64_t t = bwd::seg_plan(P, w16, bwd::kSegChunks).total;
+      if (t < 0) return -1;
+      best = t > best ? t : best;
+    }
+  }
+  return best;
 }
 
-extern "C" int64_t gdn_bwd_workspace_size_params(const GdnBwdParams* prm) {
+// The workspace of a call run in segments of at most `seg_chunks` chunks.
+static int64_t bwd_workspace_bytes(const GdnBwdParams* prm, int64_t seg_chunks) {
   if (prm == nullptr) return -1;
   const GdnBwdParams& P = *prm;
   if (P.B <= 0 || P.T < 0 || P.H <= 0 || P.V <= 0 || P.V % bwd::BV != 0) return -1;
   if (P.K != 32 && P.K != 64 && P.K != 128) return -1;
   if (!valid_dtype(P.qkv_dtype) || !valid_dtype(P.do_dtype)) return -1;
-  return bwd::layout(P.B, P.T, P.H, P.K, P.V, P.cu_seqlens ? P.B : 0, bwd_w16(P)).total;
+  if (P.cu_seqlens) return bwd::layout(P.B, P.T, P.H, P.K, P.V, P.B, bwd_w16(P)).total;
+  return bwd::seg_plan(P, bwd_w16(P), seg_chunks).total;
 }
 
-extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
-  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
-  const GdnBwdParams& P = *prm;
+extern "C" int64_t gdn_bwd_workspace_size_params(const GdnBwdParams* prm) {
+  return bwd_workspace_bytes(prm, bwd::kSegChunks);
+}
+
+extern "C" int64_t gdn_bwd_segment_workspace_size(const GdnBwdParams* prm, int seg_chunks) {
+  if (seg_chunks < 1) return -1;
+  return bwd_workspace_bytes(prm, seg_chunks);
+}
+
+// Arguments every path checks: shapes, dtypes, pointers, alignment.
+static int bwd_check(const GdnBwdParams& P) {
   if (P.B <= 0 || P.H <= 0 || P.T < 0 || P.V <= 0 || P.V % bwd::BV != 0) return GDN_ERR_BAD_SHAPE;
   if (P.K != 32 && P.K != 64 && P.K != 128) return GDN_ERR_UNSUPPORTED;
   if (!valid_dtype(P.qkv_dtype) || !valid_dtype(P.g_dtype) || !valid_dtype(P.beta_dtype) ||
@@ -2250,6 +2384,11 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
         if ((strides[i][d] * eb) % 16 != 0) return GDN_ERR_MISALIGNED;
     }
   }
+  return GDN_OK;
+}
+
+// One pass over the whole of P (the kernels' workspace at P.workspace).
+static int bwd_launch_one(const GdnBwdParams& P, hipStream_t s) {
   const int64_t units = (int64_t)P.B * P.H * (P.V / bwd::BV);
   // B is the number of sequences when cu_seqlens is given (one packed batch)
   const bool w16 = bwd_w16(P);
@@ -2293,11 +2432,93 @@ extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
   // fp16 pair recurrences (the 16-bit walks)
   a.w16 = w16;
 
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nrec_launch = P.T > 0 ? nrec : 0;
   switch (P.qkv_dtype) {
     case GDN_DTYPE_F16: return bwd::launch_t<f16>(a, P.K, nrec_launch, s);
     case GDN_DTYPE_BF16: return bwd::launch_t<bf16_t>(a, P.K, nrec_launch, s);
     default: return bwd::launch_t<float>(a, P.K, nrec_launch, s);
   }
+}
+
+extern "C" int gdn_bwd_launch(const GdnBwdParams* prm, void* stream) {
+  if (prm == nullptr) return GDN_ERR_NULL_POINTER;
+  const GdnBwdParams& P = *prm;
+  const int chk = bwd_check(P);
+  if (chk != GDN_OK) return chk;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nch = ((int64_t)P.T + bwd::C - 1) / bwd::C;
+  const bool w16 = bwd_w16(P);
+  // one pass: packed sequences, or a workspace that holds every chunk
+  if (P.cu_seqlens != nullptr || nch <= 1 || P.workspace == nullptr ||
+      P.workspace_bytes >= bwd::layout(P.B, P.T, P.H, P.K, P.V, 0, w16).total)
+    return bwd_launch_one(P, s);
+  if (reinterpret_cast<uintptr_t>(P.workspace) % 256 != 0) return GDN_ERR_WORKSPACE;
+  // the longest segments whose layout fits, then shorter ones until the
+  // checkpoints fit beside it
+  int64_t lo = 0, hi = nch - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (bwd::seg_plan(P, w16, mid).region <= P.workspace_bytes)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  int64_t L = lo;
+  while (L >= 1 && bwd::seg_plan(P, w16, L).total > P.workspace_bytes) --L;
+  if (L < 1) return GDN_ERR_WORKSPACE;
+  const bwd::SegPlan sp = bwd::seg_plan(P, w16, L);
+  char* ws = static_cast<char*>(P.workspace);
+  const int64_t dense[4] = {(int64_t)P.H * P.K * P.V, (int64_t)P.K * P.V, P.V, 1};
+  auto ckpt = [&](int64_t j) { return reinterpret_cast<float*>(ws + sp.ckpt + j * sp.state_bytes); };
+  auto carry = [&](int64_t j) { return reinterpret_cast<float*>(ws + sp.carry + (j & 1) * sp.state_bytes); };
+  const int64_t R = sp.L * bwd::C;  // rows per segment
+  // 1. the state at the start of segments 1 .. n-1
+  for (int64_t j = 0; j + 1 < sp.nseg; ++j) {
+    GdnFwdParams f = bwd::fwd_params(P, j * R, (int)R, j == 0 ? P.h0 : ckpt(j - 1), j == 0 ? P.h0_stride : dense,
+                                     ckpt(j), ws + sp.fwd_o);
+    f.workspace = sp.fwd_ws > 0 ? ws : nullptr;
+    f.workspace_bytes = sp.fwd_ws;
+    const int st = gdn_fwd_launch(&f, stream);
+    if (st != GDN_OK) return st;
+  }
+  // 2. the segments' backward, last first, the state gradient carried
+  const int eq = elem_bytes(P.qkv_dtype), eg = elem_bytes(P.g_dtype), eb = elem_bytes(P.beta_dtype),
+            ed = elem_bytes(P.do_dtype);
+  for (int64_t j = sp.nseg - 1; j >= 0; --j) {
+    const int64_t t0 = j * R;
+    GdnBwdParams Q = P;
+    auto in = [t0](const void* p, const int64_t* st, int e) {
+      return static_cast<const void*>(static_cast<const char*>(p) + t0 * st[1] * e);
+    };
+    auto out = [t0](void* p, const int64_t* st, int e) {
+      return static_cast<void*>(static_cast<char*>(p) + t0 * st[1] * e);
+    };
+    Q.q = in(P.q, P.q_stride, eq);
+    Q.k = in(P.k, P.k_stride, eq);
+    Q.v = in(P.v, P.v_stride, eq);
+    Q.g = in(P.g, P.g_stride, eg);
+    Q.beta = in(P.beta, P.beta_stride, eb);
+    Q.d_o = in(P.d_o, P.do_stride, ed);
+    Q.dq = out(P.dq, P.dq_stride, eq);
+    Q.dk = out(P.dk, P.dk_stride, eq);
+    Q.dv = out(P.dv, P.dv_stride, eq);
+    Q.dg = out(P.dg, P.dg_stride, eg);
+    Q.dbeta = out(P.dbeta, P.dbeta_stride, eb);
+    Q.T = (int)(P.T - t0 < R ? P.T - t0 : R);
+    if (j > 0) {
+      Q.h0 = ckpt(j - 1);
+      for (int d = 0; d < 4; ++d) Q.h0_stride[d] = dense[d];
+      Q.dh0 = carry(j);
+      for (int d = 0; d < 4; ++d) Q.dh0_stride[d] = dense[d];
+    }
+    if (j + 1 < sp.nseg) {
+      Q.d_final_state = carry(j + 1);
+      for (int d = 0; d < 4; ++d) Q.dfs_stride[d] = dense[d];
+    }
+    Q.workspace = ws;
+    Q.workspace_bytes = sp.region;
+    const int st = bwd_launch_one(Q, s);
+    if (st != GDN_OK) return st;
+  }
+  return GDN_OK;
 }

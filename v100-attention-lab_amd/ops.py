@@ -534,7 +534,8 @@ BWD_SUPPORTED_K = (32, 64, 128)
 def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
             beta: torch.Tensor, h0: Optional[torch.Tensor], do: torch.Tensor,
             dfinal: Optional[torch.Tensor] = None, scale: float = 1.0,
-            cu_seqlens: Optional[torch.Tensor] = None, need_dh0: bool = True):
+            cu_seqlens: Optional[torch.Tensor] = None, need_dh0: bool = True,
+            max_segment_chunks: Optional[int] = None):
     """Gradients of ``gdn_fwd`` (the recurrence gdn_ref.py:3-9) with respect to
     ``q, k, v, g, beta, h0``, given ``do`` (the gradient of ``o``, ``[B,T,H,V]``)
     and ``dfinal`` (the gradient of ``final_state``, ``[B,H,K,V]`` fp32, or
@@ -545,7 +546,11 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     same strides, dtypes and ``cu_seqlens`` convention as the forward.  One
     call enqueues the backward's three kernels on the current stream; the
     workspace (per-chunk records, chunk-start states and their gradients,
-    u and du) is allocated here and released when the call returns.
+    u and du) is allocated here and released when the call returns.  It
+    holds at most ``max_segment_chunks`` chunks of 32 rows per sequence
+    (default 256): a longer batch runs in segments, with one forward pass
+    over all but the last segment for the states at their starts
+    (``gdn_bwd_launch``).  Packed sequences run in one pass.
     """
     n_seq = None
     if cu_seqlens is not None:
@@ -595,7 +600,12 @@ def gdn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
     P.do_dtype = _DTYPE_CODE[do.dtype]
     P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
     # the workspace this call's path takes (the 16-bit walks need less)
-    ws_bytes = lib.gdn_bwd_workspace_size_params(ctypes.byref(P))
+    if max_segment_chunks is None:
+        ws_bytes = lib.gdn_bwd_workspace_size_params(ctypes.byref(P))
+    else:
+        if int(max_segment_chunks) < 1:
+            raise ValueError(f"max_segment_chunks must be >= 1, got {max_segment_chunks}")
+        ws_bytes = lib.gdn_bwd_segment_workspace_size(ctypes.byref(P), int(max_segment_chunks))
     if ws_bytes < 0:
         raise ValueError(f"backward does not support B={B} T={T} H={H} K={K} V={V}")
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
