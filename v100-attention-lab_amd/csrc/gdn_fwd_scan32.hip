@@ -682,7 +682,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     // MFMA, placed by sched_group_barrier): issued all at once they would
     // fill the wave's LDS queue and hold the first MFMA back until most had
     // returned.
-    constexpr int SG_MFMA = 0x8, SG_DSR = 0x100;
+    constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100;
     auto chunk = [&](int it, ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
       const int itn = min(it + 1, nloc - 1);  // the last chunk's again at the end
       const int sl = itn % R;
@@ -691,6 +691,11 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       // chunk's k rows in between
       f32x4 ks[2] = {z4, z4};
       PS_BEGIN(o.kR[0][0], o.kR[1][0], sB[0], o.kA[0]);
+      // e^{b_C} S, in place: the multiplies fill the VALU slots between the
+      // K S products (sB already holds this chunk's S) instead of delaying
+      // the state update at the end of the chain
+#pragma unroll
+      for (int r = 0; r < KT; ++r) st[r] = st[r] * o.ebC;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -702,6 +707,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       for (int g = 0; g < 2 * KB; ++g) {
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
         __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
       }
       f32x4 y0, y1;
 #pragma unroll
@@ -738,7 +744,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
 #pragma unroll
       for (int r = 0; r < KT; ++r) {
-        st[r] = M::mma(o.kA[r], utB, st[r] * o.ebC);
+        st[r] = M::mma(o.kA[r], utB, st[r]);
         const int piece = 4 * (r >> 1) + (n & 3);
         const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
         const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
