@@ -1,6 +1,7 @@
 // The forward for 32-row chunks as two launches: a per-chunk record of the
 // state-independent work, then a scan over the chunks that keeps the state
-// on chip (the default path for fp16 inputs, C = 32, K in {64, 128}).
+// on chip (the default path for fp16 and bf16 inputs, C = 32, K in {64,
+// 128}).
 //
 // Per chunk (C = 32 rows, b = in-chunk cumsum of g, as in gdn_ref.py:51-99):
 //   A  = tril_-1(beta_t e^{b_t - b_j} K K^T),   T = (I + A)^-1,
@@ -23,11 +24,13 @@
 //      (no chunk state is written).  Waves have fixed roles and pass one
 //      barrier per iteration:
 //        SCAN x BV/16  chunk it: K S, Y = V - diag(e^b) K S, u = Tu Y,
-//                      S <- e^{bC} S + K^T diag(e^{bC-b}) u (16 columns each)
+//                      S <- e^{bC} S + K^T diag(e^{bC-b}) u (16 columns each;
+//                      fp16 at BV = 16, K = 128: two waves, each updating
+//                      half of the state rows)
 //        OUT  x BV/16  chunk it: Q S with the chunk-start state;
-//                      chunk it-1: o = scale (P u + diag(e^b) Q S), staged
-//                      through LDS so that each lane stores 8 elements of
-//                      one row
+//                      chunk it-1: o = scale (P u + diag(e^b) Q S), formed
+//                      transposed so that each lane stores 8 consecutive
+//                      elements of one row
 //        PQK           chunk it: P = e^{b_t-b_j} Q K^T (t >= j) as hi + lo
 //                      fp16 operand fragments
 //        LOAD          chunk it+D: q, k, the v slice and the record, copied
@@ -498,9 +501,20 @@ __device__ __forceinline__ void store_o4(void* o, int64_t off, const f32x4& w, i
   }
 }
 
-template <int BV>
+// fp16 at BV = 16 and K = 128 can split the slice's SCAN work over two
+// waves, each updating half of the state rows (five waves): SCAN is the
+// longest role there.  The launch takes the split for segments of at most
+// kSplitChunks chunks; longer ones run faster on one SCAN wave, and at
+// K = 64 the split costs more than it saves.
+template <typename TIn, int K, int BV>
+constexpr bool scan_split_ok() {
+  return std::is_same<TIn, f16>::value && BV == 16 && K == 128;
+}
+constexpr int kSplitChunks = 192;
+
+template <int BV, bool SPL>
 constexpr int scan_waves() {
-  return 2 * (BV / 16) + 2;
+  return 2 * (BV / 16) + 2 + (SPL ? 1 : 0);
 }
 
 enum ScanRole { SR_SCAN, SR_OUT, SR_PQK, SR_LOAD };
@@ -511,11 +525,12 @@ constexpr int dma_per_chunk() {
   return 2 * (C * K * 2 / 1024) + (C * BV * 2 + 1023) / 1024 + REC_BYTES / 1024;
 }
 
-template <typename TIn, int K, int BV>
-__global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SArgs p) {
+template <typename TIn, int K, int BV, bool SPLIT>
+__global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(const SArgs p) {
   using M = Mma<f16>;
   using S = ScanSmem<K, BV>;
   constexpr int NSW = BV / 16;
+  static_assert(!SPLIT || scan_split_ok<TIn, K, BV>(), "split SCAN: fp16, K = 128, BV = 16");
   constexpr int KB = K / 32, KT = K / 16;
   constexpr int R = S::R, RR = S::RR;
   constexpr int ND = dma_per_chunk<K, BV>();
@@ -586,7 +601,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     __shared__ uint32_t red[8];
     uint32_t m = state_absmax_bits(st_src ? st_src + bi * st_sd[0] + hi * st_sd[1] + v0 * st_sd[3] : nullptr,
                                    st_sd[2], st_sd[3], K, BV);
-    for (int i = tid; i < nloc * NSW; i += 64 * scan_waves<BV>()) {
+    for (int i = tid; i < nloc * NSW; i += 64 * scan_waves<BV, SPLIT>()) {
       const float* vm = reinterpret_cast<const float*>(rech + (int64_t)(i / NSW) * RS + R_VMAX);
       m = max(m, __float_as_uint(vm[v0 / 16 + i % NSW]));
     }
@@ -597,9 +612,17 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 
   // Waves w and w + 4 share SIMD w % 4.  At BV = 32 (six waves) the SCAN
   // waves take waves 2 and 3, alone on their SIMDs, and the OUT waves share
-  // theirs with PQK and LOAD.
+  // theirs with PQK and LOAD.  Split SCAN (five waves): the two SCAN waves
+  // and PQK each alone on a SIMD, OUT with LOAD (of the five placements
+  // timed, the fastest: a SCAN or PQK wave beside LOAD or each other is
+  // slower).
   int role, ridx;
-  if constexpr (NSW == 2) {
+  if constexpr (SPLIT) {
+    constexpr int roles[5] = {SR_OUT, SR_PQK, SR_SCAN, SR_SCAN, SR_LOAD};
+    constexpr int idx[5] = {0, 0, 0, 1, 0};
+    role = roles[wave];
+    ridx = idx[wave];
+  } else if constexpr (NSW == 2) {
     constexpr int roles[6] = {SR_OUT, SR_OUT, SR_SCAN, SR_SCAN, SR_PQK, SR_LOAD};
     constexpr int idx[6] = {0, 1, 0, 1, 0, 0};
     role = roles[wave];
@@ -611,175 +634,217 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
 
   if (role == SR_SCAN) {
     // ================================================================ SCAN
-    const int cb = ridx;
-    const int vcol = 16 * cb + n;
-    // accumulator element (r, i) is state row rho = 16 r + 4 gq + i
-    auto key_of = [&](int r, int i) { return 32 * (r >> 1) + 8 * gq + 4 * (r & 1) + i; };
-    f32x4 st[KT];
-    {
-      const float* src = st_src;
-      const int64_t* sd = st_sd;
+    // NH state waves per 16-column slice.  NH = 2 (fp16 at BV = 16): wave h
+    // keeps the state rows of key blocks h KB / 2 .. (h + 1) KB / 2 - 1 and
+    // updates them; both form the whole K S, reading the other half of S
+    // from the chunk-start copy in LDS (written before the last barrier),
+    // and the whole u.  NH = 1: one wave per slice (cb: the slice at BV = 32).
+    auto scan = [&](auto HH, auto NHH) __attribute__((always_inline)) {
+      constexpr int h = decltype(HH)::value, NH = decltype(NHH)::value;
+      constexpr int KBO = KB / NH, KTO = KT / NH;  // own 32-key blocks, own 16-key state tiles
+      constexpr int kb0 = h * KBO, r0 = h * KTO;
+      constexpr int KBP = NH == 2 ? KB - KBO : 1;  // the other wave's blocks
+      constexpr int kbp0 = (1 - h) * KBO;
+      const int cb = NH == 1 ? ridx : 0;
+      const float one = opaque_one();
+      const int vcol = 16 * cb + n;
+      // accumulator element (r, i) is state row rho = 16 r + 4 gq + i
+      auto key_of = [&](int r, int i) { return 32 * (r >> 1) + 8 * gq + 4 * (r & 1) + i; };
+      f32x4 st[KTO];
+      {
+        const float* src = st_src;
+        const int64_t* sd = st_sd;
 #pragma unroll
-      for (int r = 0; r < KT; ++r) st[r] = z4;
-      if (src != nullptr) {
-        const float* s0 = src + bi * sd[0] + hi * sd[1] + (v0 + vcol) * sd[3];
+        for (int rl = 0; rl < KTO; ++rl) st[rl] = z4;
+        if (src != nullptr) {
+          const float* s0 = src + bi * sd[0] + hi * sd[1] + (v0 + vcol) * sd[3];
 #pragma unroll
-        for (int r = 0; r < KT; ++r)
+          for (int rl = 0; rl < KTO; ++rl)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) st[r][i] = s0[key_of(r, i) * sd[2]] * rsc.v;
+            for (int i = 0; i < 4; ++i) st[rl][i] = s0[key_of(r0 + rl, i) * sd[2]] * rsc.v;
+        }
       }
-    }
-    f16x8 sB[KB];
+      f16x8 sB[KBO];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
-      s.so[0][cb][kb][lane] = sB[kb];
-    }
-    PS_DECL;
-    // One chunk's operands of the chain, in registers.  Chunk it + 1's are
-    // read from LDS while chunk it computes (the LOAD wave publishes chunks
-    // two ahead), so the chain K S -> u -> S waits on no LDS read.
-    struct ScanOps {
-      f16x8 kR[2][KB], kA[KT];
-      f16x4 va, vb;
-      f16x8 tu0, tu1;
-      f32x4 eb_lo, eb_hi, ec_lo, ec_hi;
-      float ebC;
-    };
-    const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
-    const int vc = (16 * cb + 4 * (n & 3)) * 2;
-    auto read_ops = [&](int it, ScanOps& o) __attribute__((always_inline)) {
-      const int sl = it % R;
-      const char* rc = s.rec[it % RR];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) o.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
-      const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
-#pragma unroll
-      for (int r = 0; r < KT; ++r) {
+      for (int kl = 0; kl < KBO; ++kl) {
+        sB[kl] = M::from_acc(st[2 * kl], st[2 * kl + 1]);
+        s.so[0][cb][kb0 + kl][lane] = sB[kl];
+      }
+      PS_DECL;
+      // One chunk's operands of the chain, in registers.  Chunk it + 1's are
+      // read from LDS while chunk it computes (the LOAD wave publishes chunks
+      // two ahead), so the chain K S -> u -> S waits on no LDS read.
+      struct ScanOps {
+        f16x8 kR[2][KB], kA[KTO];
+        f16x4 va, vb;
+        f16x8 tu0, tu1;
+        f32x4 eb_lo, eb_hi, ec_lo, ec_hi;
+        float ebC;
+      };
+      const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
+      const int vc = (16 * cb + 4 * (n & 3)) * 2;
+      auto read_kA = [&](const char* kbase, int rl) __attribute__((always_inline)) {
+        const int r = r0 + rl;
         const int piece = 4 * (r >> 1) + (n & 3);
         const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
         const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
-        o.kA[r] = cat8(lo, hi4);
-      }
-      // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
-      const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
-      o.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
-      o.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
-      const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
-      o.tu0 = tu[lane];
-      o.tu1 = tu[64 + lane];
-      const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
-      const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
-      o.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
-      o.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
-      o.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
-      o.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
-      o.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
-    };
-    // The next chunk's reads go out between the chain's MFMAs (a few per
-    // MFMA, placed by sched_group_barrier): issued all at once they would
-    // fill the wave's LDS queue and hold the first MFMA back until most had
-    // returned.
-    constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100;
-    auto chunk = [&](int it, ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
-      const int itn = min(it + 1, nloc - 1);  // the last chunk's again at the end
-      const int sl = itn % R;
-      const char* rc = s.rec[itn % RR];
-      // K S: rows t, so its two row tiles form a B operand over t; the next
-      // chunk's k rows in between
-      f32x4 ks[2] = {z4, z4};
-      PS_BEGIN(o.kR[0][0], o.kR[1][0], sB[0], o.kA[0]);
-      // e^{b_C} S, in place: the multiplies fill the VALU slots between the
-      // K S products (sB already holds this chunk's S) instead of delaying
-      // the state update at the end of the chain
+        return cat8(lo, hi4);
+      };
+      auto read_ops = [&](int it, ScanOps& o) __attribute__((always_inline)) {
+        const int sl = it % R;
+        const char* rc = s.rec[it % RR];
 #pragma unroll
-      for (int r = 0; r < KT; ++r) st[r] = st[r] * o.ebC;
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+          for (int kb = 0; kb < KB; ++kb) o.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+        const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          ks[mt] = M::mma(o.kR[mt][kb], sB[kb], ks[mt]);
-          nx.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
-        }
-#pragma unroll
-      for (int g = 0; g < 2 * KB; ++g) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
-      }
-      f32x4 y0, y1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
-        y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
-      }
-      const f16x8 yB = M::from_acc(y0, y1);
-      f32x4 u[2];
-      u[0] = M::mma(o.tu0, yB, z4);
-      u[1] = M::mma(o.tu1, yB, z4);
-      {
-        // the next chunk's v column and record fields
+        for (int rl = 0; rl < KTO; ++rl) o.kA[rl] = read_kA(kbase, rl);
+        // v rows 4 gq + i and 16 + 4 gq + i of column vcol (accumulator layout)
         const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
-        nx.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
-        nx.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+        o.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+        o.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
         const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
-        nx.tu0 = tu[lane];
-        nx.tu1 = tu[64 + lane];
+        o.tu0 = tu[lane];
+        o.tu1 = tu[64 + lane];
         const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
         const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
-        nx.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
-        nx.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
-        nx.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
-        nx.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
-        nx.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
-      }
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DSR, 5, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DSR, 4, 0);
-      const f16x8 utB = M::from_acc(u[0] * o.ec_lo, u[1] * o.ec_hi);
-      // state update; the next chunk's transposed k fragments in between
-      const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
+        o.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+        o.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+        o.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+        o.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+        o.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+      };
+      // The next chunk's reads go out between the chain's MFMAs (a few per
+      // MFMA, placed by sched_group_barrier): issued all at once they would
+      // fill the wave's LDS queue and hold the first MFMA back until most had
+      // returned.
+      constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100;
+      auto chunk = [&](int it, ScanOps& o, ScanOps& nx) __attribute__((always_inline)) {
+        const int itn = min(it + 1, nloc - 1);  // the last chunk's again at the end
+        const int sl = itn % R;
+        const char* rc = s.rec[itn % RR];
+        // the other wave's half of this chunk's start state
+        f16x8 sP[KBP];
+        if constexpr (NH == 2) {
 #pragma unroll
-      for (int r = 0; r < KT; ++r) {
-        st[r] = M::mma(o.kA[r], utB, st[r]);
-        const int piece = 4 * (r >> 1) + (n & 3);
-        const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
-        const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
-        nx.kA[r] = cat8(lo, hi4);
-      }
+          for (int j = 0; j < KBP; ++j) sP[j] = s.so[it & 1][cb][kbp0 + j][lane];
+        }
+        // K S: rows t, so its two row tiles form a B operand over t; own
+        // key blocks first, the next chunk's k rows in between
+        f32x4 ks[2] = {z4, z4};
+        PS_BEGIN(o.kR[0][0], o.kR[1][0], sB[0], o.kA[0]);
+        // e^{b_C} S, in place: the multiplies fill the VALU slots between
+        // the K S products (sB already holds this chunk's S) instead of
+        // delaying the state update at the end of the chain
 #pragma unroll
-      for (int r = 0; r < KT; ++r) {
+        for (int rl = 0; rl < KTO; ++rl) st[rl] = st[rl] * o.ebC;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+          const int kb = NH == 2 ? (j < KBO ? kb0 + j : kbp0 + j - KBO) : j;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const f16x8 sop = (NH == 1 || j < KBO) ? sB[min(j, KBO - 1)] : sP[max(j - KBO, 0) % KBP];
+            ks[mt] = M::mma(o.kR[mt][kb], sop, ks[mt]);
+            nx.kR[mt][kb] = staged(s.rk[sl], 16 * mt + n, 4 * kb + gq);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 2 * KB; ++g) {
+          __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
+        }
+        f32x4 y0, y1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
+          y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
+        }
+        const f16x8 yB = M::from_acc(y0, y1);
+        f32x4 u[2];
+        u[0] = M::mma(o.tu0, yB, z4);
+        u[1] = M::mma(o.tu1, yB, z4);
+        {
+          // the next chunk's v column and record fields
+          const char* vbase = reinterpret_cast<const char*>(s.rv[sl]);
+          nx.va = lds_tr16(vbase + t0 * (BV * 2) + vc);
+          nx.vb = lds_tr16(vbase + t1 * (BV * 2) + vc);
+          const f16x8* tu = reinterpret_cast<const f16x8*>(rc + R_TU);
+          nx.tu0 = tu[lane];
+          nx.tu1 = tu[64 + lane];
+          const float* ebr = reinterpret_cast<const float*>(rc + R_EB);
+          const float* ecr = reinterpret_cast<const float*>(rc + R_EC);
+          nx.eb_lo = *reinterpret_cast<const f32x4*>(ebr + 4 * gq);
+          nx.eb_hi = *reinterpret_cast<const f32x4*>(ebr + 16 + 4 * gq);
+          nx.ec_lo = *reinterpret_cast<const f32x4*>(ecr + 4 * gq);
+          nx.ec_hi = *reinterpret_cast<const f32x4*>(ecr + 16 + 4 * gq);
+          nx.ebC = *reinterpret_cast<const float*>(rc + R_EBC);
+        }
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_DSR, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DSR, 5, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DSR, 4, 0);
+        const f16x8 utB = M::from_acc(u[0] * o.ec_lo, u[1] * o.ec_hi);
+        // state update of the own rows; the next chunk's transposed k
+        // fragments in between
+        const char* kbase = reinterpret_cast<const char*>(s.rk[sl]);
+#pragma unroll
+        for (int rl = 0; rl < KTO; ++rl) {
+          st[rl] = M::mma(o.kA[rl], utB, st[rl]);
+          nx.kA[rl] = read_kA(kbase, rl);
+        }
+#pragma unroll
+        for (int rl = 0; rl < KTO; ++rl) {
+          __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(SG_DSR, 2, 0);
+        }
+        if constexpr (NH == 2) {
+          // u for OUT as fp16 hi and residual operand fragments, in the two
+          // 16-byte slots of the fp32 copy, from wave 0 (wave 1 sums K S
+          // in another order: its u may differ in the last fp32 bit, which
+          // only its own state rows see)
+          if (h == 0) {
+            const f16x8 uhi = M::from_acc(u[0], u[1]);
+            reinterpret_cast<f16x8*>(&s.uo[it & 1][cb][0][0])[lane] = uhi;
+            reinterpret_cast<f16x8*>(&s.uo[it & 1][cb][1][0])[lane] = split_lo_mix(u[0], u[1], uhi, one);
+          }
+        } else {
+          s.uo[it & 1][cb][0][lane] = u[0];
+          s.uo[it & 1][cb][1][lane] = u[1];
+        }
+#pragma unroll
+        for (int kl = 0; kl < KBO; ++kl) sB[kl] = M::from_acc(st[2 * kl], st[2 * kl + 1]);
+        PS_END_A(sB[0], sB[KBO - 1]);
+#pragma unroll
+        for (int kl = 0; kl < KBO; ++kl) s.so[(it + 1) & 1][cb][kb0 + kl][lane] = sB[kl];
+        wg_barrier();
+      };
+      ScanOps oa, ob;
+      if (nloc > 0) {
+        wg_barrier();
+        read_ops(0, oa);
       }
-      s.uo[it & 1][cb][0][lane] = u[0];
-      s.uo[it & 1][cb][1][lane] = u[1];
+      for (int it = 0; it < nloc; it += 2) {
+        chunk(it, oa, ob);
+        if (it + 1 < nloc) chunk(it + 1, ob, oa);
+      }
+      PS_RECORD(1, nloc, 2 * KB + 2 + KTO, 0);
+      PS_RECORD_BAR(1);
+      float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sB[kb] = M::from_acc(st[2 * kb], st[2 * kb + 1]);
-      PS_END_A(sB[0], sB[KB - 1]);
+      for (int rl = 0; rl < KTO; ++rl)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) s.so[(it + 1) & 1][cb][kb][lane] = sB[kb];
-      wg_barrier();
+        for (int i = 0; i < 4; ++i) fs[key_of(r0 + rl, i) * p.sfs[2]] = st[rl][i] * rsc.fs;
     };
-    ScanOps oa, ob;
-    if (nloc > 0) {
-      wg_barrier();
-      read_ops(0, oa);
+    if constexpr (SPLIT) {
+      if (ridx == 0)
+        scan(std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{});
+      else
+        scan(std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
+    } else {
+      scan(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
     }
-    for (int it = 0; it < nloc; it += 2) {
-      chunk(it, oa, ob);
-      if (it + 1 < nloc) chunk(it + 1, ob, oa);
-    }
-    PS_RECORD(1, nloc, 2 * KB + 2 + KT, 0);
-    PS_RECORD_BAR(1);
-    float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
-#pragma unroll
-    for (int r = 0; r < KT; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fs[key_of(r, i) * p.sfs[2]] = st[r][i] * rsc.fs;
   } else if (nloc == 0) {
     return;
   } else if (role == SR_OUT) {
@@ -810,7 +875,7 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
     };
     auto load_o = [&](int it, OutOps& o) __attribute__((always_inline)) {
       o.u0 = s.uo[it & 1][c2][0][lane];
-      o.u1 = s.uo[it & 1][c2][1][lane];
+      o.u1 = s.uo[it & 1][c2][1][lane];  // split SCAN: u as fp16 hi, residual
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         o.pAs[mt] = s.p[it & 1][mt][lane];
@@ -821,8 +886,14 @@ __global__ __launch_bounds__(64 * scan_waves<BV>()) void scan32_kernel(const SAr
       o.ebt[1] = ebr[16 + n];
     };
     auto store_chunk = [&](int it, const OutOps& o) __attribute__((always_inline)) {
-      f16x8 uh = M::from_acc(o.u0, o.u1);
-      f16x8 ul = split_lo_mix(o.u0, o.u1, uh, one);
+      f16x8 uh, ul;
+      if constexpr (SPLIT) {
+        uh = __builtin_bit_cast(f16x8, o.u0);
+        ul = __builtin_bit_cast(f16x8, o.u1);
+      } else {
+        uh = M::from_acc(o.u0, o.u1);
+        ul = split_lo_mix(o.u0, o.u1, uh, one);
+      }
       f32x4 ov[2];
       PS_BEGIN(uh, ul);
 #pragma unroll
@@ -1087,7 +1158,13 @@ template <typename TIn, int K, int BV>
 int launch_kb(const SArgs& a, int units, hipStream_t s) {
   static_assert(sizeof(ScanSmem<K, BV>) <= kLdsLimit, "LDS budget");
   if (a.nrec > 0) hipLaunchKernelGGL((rec32_kernel<TIn, K>), dim3((a.nrec + 7) / 8), dim3(256), 0, s, a);
-  hipLaunchKernelGGL((scan32_kernel<TIn, K, BV>), dim3(units), dim3(64 * scan_waves<BV>()), 0, s, a);
+  if constexpr (scan_split_ok<TIn, K, BV>()) {
+    if (a.L <= kSplitChunks) {
+      hipLaunchKernelGGL((scan32_kernel<TIn, K, BV, true>), dim3(units), dim3(64 * scan_waves<BV, true>()), 0, s, a);
+      return (int)hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((scan32_kernel<TIn, K, BV, false>), dim3(units), dim3(64 * scan_waves<BV, false>()), 0, s, a);
   return (int)hipGetLastError();
 }
 
