@@ -115,7 +115,7 @@ def test_fwd_workspace_size(lib, pkg):
     # bf16: the record, then the chunk's k rows in fp16
     assert size(qkv_dtype=2) == 2 * H * 128 * (3072 + 32 * 128 * 2)
     assert size(qkv_dtype=2, K=64) == 2 * H * 128 * (3072 + 32 * 64 * 2)
-    assert size(qkv_dtype=2, V=2512) == 0                # bf16, V / 16 > 156: fused kernel, none
+    assert size(qkv_dtype=2, V=2512) == 2 * H * 128 * (3072 + 32 * 128 * 2)  # any V
     assert size(qkv_dtype=0) == 0                        # fp32: phased kernel, none
     assert size(K=32) == 0 and size(K=256) == 0          # phased kernel, none
     assert size(chunk_size=64, K=256) == 0               # phased kernel, none

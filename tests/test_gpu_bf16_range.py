@@ -92,3 +92,53 @@ def test_bf16_in_range_unchanged(pkg, cuda, kernel):
                            output_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(o_b.cpu(), o_h.cpu()) and torch.equal(f_b.cpu(), f_h.cpu())
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("rising", [True, False])
+def test_bf16_scale_changes_along_t(pkg, cuda, case, rising):
+    """v's magnitude changes by eleven decades at row 100 (1e-6 then 1e5, or
+    the reverse), inside the fourth 32-row chunk.
+
+    Rising: every kernel meets the max-norm bound on o and the final state.
+    The record + scan launches at C = 32 choose their shift chunk by chunk
+    (it only goes down along the sequence), so there the first three
+    chunks' outputs also meet it against their own magnitude; the other
+    kernels take one shift per slice for the whole sequence, which sinks
+    those rows into fp16's subnormals.
+    Falling: o meets the max-norm bound.  The decayed final state is eleven
+    decades below the state's earlier magnitude, the one that set the shift
+    (a shift that went down stays down, and a single shift cannot serve
+    both), so it is held to that earlier magnitude: max |error| <= 1e-3
+    max |h0|."""
+    name, chunk, kernel, K = CASES[case]
+    T, t_sw = 200, 100
+    lo, hi = 1e-6, 1e5
+    prof = torch.full((T,), hi if rising else lo)
+    prof[:t_sw] = lo if rising else hi
+    q, k, v, g, beta, h0 = ref.make_inputs_baseline(1, T, 2, K, 32, seed=99 + case, dtype=torch.float32,
+                                                    with_h0=True)
+    v = v * prof.view(1, T, 1, 1)
+    h0 = h0 * (lo if rising else hi)
+    bf = lambda t: t.to(torch.bfloat16)
+    q, k, v = bf(q), bf(k), bf(v)
+    d = lambda t: t.to(cuda)
+    print(f"[bf16 range] {name} v 1e-6/1e5 {'rising' if rising else 'falling'}", flush=True)
+    o, fs = pkg.gdn_fwd(d(q), d(k), d(v), d(g), d(beta), d(h0), chunk_size=chunk, kernel=kernel,
+                        output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o, fs = o.cpu(), fs.cpu()
+    assert torch.isfinite(o).all() and torch.isfinite(fs).all()
+    o_ref, h_ref = ref.recurrent(q, k, v, beta, g, ref.to_vk(h0), dtype=torch.float64)
+    h_ref = ref.to_kv(h_ref)
+    eo = ref.rel_err(o_ref, o)
+    if rising:
+        eh = ref.rel_err(h_ref, fs)
+    else:
+        eh = ((h_ref - fs.double()).abs().max() / h0.abs().max()).item()
+    print(f"[bf16 range] {name}: o rel={eo:.3e} state err={eh:.3e}", flush=True)
+    assert eo <= TOL and eh <= TOL
+    if rising and chunk == 32 and kernel == "auto":
+        e = ref.rel_err(o_ref[:, :96], o[:, :96])
+        print(f"[bf16 range] {name} rows before the change: o rel={e:.3e}", flush=True)
+        assert e <= TOL

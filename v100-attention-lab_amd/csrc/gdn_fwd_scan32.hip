@@ -63,16 +63,14 @@ constexpr int R_B = 2048;   // float [32]: in-chunk cumsum b times log2(e) (flat
 constexpr int R_EB = 2176;  // float [32]: e^b
 constexpr int R_EC = 2304;  // float [32]: e^{bC - b}
 constexpr int R_EBC = 2432; // float: e^{bC}
-constexpr int R_VMAX = 2448; // float [V / 16] (bf16 inputs): largest |v| of each 16-column slice of the rows
-constexpr int kMaxVSlices = (REC_BYTES - R_VMAX) / 4;
-// bf16 inputs: the record is followed by the chunk's k and q rows in fp16
-// (C x K each, in frag_piece order, rows past the end holding the last
-// row), which the scan copies instead of the inputs.
+// bf16 inputs: the record is followed by the chunk's k rows in fp16 (C x K,
+// in frag_piece order, rows past the end holding the last row), which the
+// scan copies instead of the input.
 template <typename TIn, int K>
 constexpr int rec_stride() {
   return std::is_same<TIn, bf16_t>::value ? REC_BYTES + C * K * 2 : REC_BYTES;
 }
-constexpr int R_K16 = REC_BYTES;  // then q at R_K16 + C K 2
+constexpr int R_K16 = REC_BYTES;
 // 16-byte piece c (columns 8 c ..) of row r of those copies, in the order
 // the record kernel's lanes hold them (lane (n, gq) of operand (mt, kb) is
 // row 16 mt + n, piece 4 kb + gq): each of its stores is 1 KB contiguous.
@@ -257,8 +255,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
   // the two records of this wave: geometry (wave-uniform)
   int nval[2];
   const char* kh[2];
-  const char* qh[2];
-  const char* vh[2];
   char* rp[2];
   uint32_t skb[2];
 #pragma unroll
@@ -266,8 +262,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
     const int r = (blockIdx.x * 4 + wave) * 2 + e;
     nval[e] = 0;
     kh[e] = nullptr;
-    qh[e] = nullptr;
-    vh[e] = nullptr;
     rp[e] = nullptr;
     skb[e] = 0;
     if (r < p.nrec) {
@@ -279,8 +273,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
         nval[e] = min(C, rs.T - t0);
         kh[e] = static_cast<const char*>(p.k) + (head_base(rs, hi, p.sk) + (int64_t)t0 * p.sk[1]) * EB;
         skb[e] = (uint32_t)p.sk[1] * EB;
-        vh[e] = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + (int64_t)t0 * p.sv[1]) * EB;
-        qh[e] = static_cast<const char*>(p.q) + (head_base(rs, hi, p.sq) + (int64_t)t0 * p.sq[1]) * EB;
         rp[e] = p.rec + (int64_t)r * rec_stride<TIn, K>();
       }
     }
@@ -423,37 +415,6 @@ __global__ __launch_bounds__(256) void rec32_kernel(const SArgs p) {
       tu[mt * 64 + 16 * g4 + nl] = fu;
     }
   }
-  // bf16 inputs: the largest |v| of each 16-column slice of the record's
-  // rows (rows past the end re-read the last row), from which the scan
-  // takes its range scale.  Lane (rg, sl8): rows 4 rg .. 4 rg + 3 of slice
-  // sb + sl8, reduced over rg.
-  if constexpr (std::is_same<TIn, bf16_t>::value) {
-    const int nsl = p.V / 16, sl8 = lane & 7, rg = lane >> 3;
-    const int64_t svb = p.sv[1] * (int64_t)EB;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      if (nval[e] == 0) continue;
-      for (int sb = 0; sb < nsl; sb += 8) {
-        const int slc = sb + sl8;
-        uint32_t m = 0;
-        if (slc < nsl) {
-          uint4 x[8];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const char* row = vh[e] + (int64_t)min(4 * rg + i, nval[e] - 1) * svb + slc * 32;
-            x[2 * i] = *reinterpret_cast<const uint4*>(row);
-            x[2 * i + 1] = *reinterpret_cast<const uint4*>(row + 16);
-          }
-#pragma unroll
-          for (int i = 0; i < 8; ++i) m = max(m, bf16x8_absmax_bits(x[i]));
-        }
-        m = max(m, (uint32_t)__shfl_xor((int)m, 8));
-        m = max(m, (uint32_t)__shfl_xor((int)m, 16));
-        m = max(m, (uint32_t)__shfl_xor((int)m, 32));
-        if (rg == 0 && slc < nsl) reinterpret_cast<float*>(rp[e] + R_VMAX)[slc] = __uint_as_float(m);
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -473,7 +434,67 @@ struct alignas(16) ScanSmem {
   f16x8 plo[2][2][64];              // and the fp16 residual
   f16x8 so[2][NSW][K / 32][64];     // chunk-start state as B operand fragments
   f32x4 uo[2][NSW][2][64];          // u in fp32 (accumulator layout)
+  float usc[2][NSW][2];             // bf16: u's range factors for OUT (Q S ratio, o scale)
 };
+
+// bf16 inputs: the range shift of a 16-column state slice, chosen chunk by
+// chunk.  Each SCAN wave runs its columns on v and the state times 2^sh, a
+// power of two (exact in fp32, and carried unchanged through fp16 rounding
+// away from fp16's limits), and o and final_state come out times 2^-sh.
+// The shift only goes down along the sequence: sh_c = min(sh_{c-1},
+// cap(chunk c's v)), starting from cap(incoming state), so that every
+// operand already folded into the state stays in range; going down, the
+// state is multiplied by 2^(sh_c - sh_{c-1}) with the chunk's decay.  o and
+// the state are linear in (v, state) and each column evolves on its own,
+// which makes this exact up to the roundings the unscaled values would see.
+// cap(m), for a largest magnitude with float bits m (wave-uniform): none
+// (kNoCap) when m is zero, 0 when m is not finite or lies in [2^-6, 2^10],
+// else 127 - e for m's biased exponent e, which puts m 2^cap in [1, 2);
+// clamped to [-126, 126].
+constexpr int kNoCap = 127;
+__device__ __forceinline__ int shift_cap(uint32_t m) {
+  if (m == 0) return kNoCap;
+  const int e = (int)(m >> 23);
+  if (e >= 255 || (m >= 0x3c800000u && m <= 0x44800000u)) return 0;
+  return min(max(127 - e, -126), 126);
+}
+
+// 2^n for n in [-126, 127], built from its bits (scalar for uniform n).
+__device__ __forceinline__ float pow2i(int n) { return __int_as_float((n + 127) << 23); }
+
+// Largest of m over the wave (as unsigned), wave-uniform: DPP within rows
+// of 16 lanes, then the four row results.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t m) {
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xf, 0xf, false));  // row_mirror
+  const uint32_t a = __builtin_amdgcn_readlane(m, 0), b = __builtin_amdgcn_readlane(m, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(m, 32), d = __builtin_amdgcn_readlane(m, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Whether the largest of m over the lanes set in `lanes` (m: float bits
+// of magnitudes) lies in [2^-6, 2^10], where shift_cap is 0: two compares,
+// no cross-lane reduction (the usual case).
+__device__ __forceinline__ bool cap0_lanes(uint32_t m, uint64_t lanes) {
+  const uint64_t big = __builtin_amdgcn_ballot_w64(m > 0x44800000u) & lanes;
+  const uint64_t mid = __builtin_amdgcn_ballot_w64(m >= 0x3c800000u) & lanes;
+  return big == 0 && mid != 0;
+}
+
+// shift_cap of the largest of m over the wave.
+__device__ __forceinline__ int wave_cap(uint32_t m) {
+  return cap0_lanes(m, ~0ull) ? 0 : shift_cap(wave_max_u32(m));
+}
+
+// A 16-bit element holding bf16 bits: its value, and |value| as fp32 bits.
+__device__ __forceinline__ float bf16_bits_f32(f16 x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, x) << 16);
+}
+__device__ __forceinline__ uint32_t bf16_abs_bits(f16 x) {
+  return ((uint32_t)__builtin_bit_cast(uint16_t, x) & 0x7fffu) << 16;
+}
 
 // Two floats as packed fp16 (round to nearest even, as (f16) x).
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
@@ -588,34 +609,22 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
   const char* vh = static_cast<const char*>(p.v) + (head_base(rs, hi, p.sv) + v0) * EB;
   constexpr int RS = rec_stride<TIn, K>();
   const char* rech = p.rec + (int64_t)(bi * p.H + hi) * p.L * RS;
-  // bf16: this slice's v and initial state scaled by a power of two into
-  // fp16's range (from their absolute maximum over the whole sequence), o
-  // and the final state scaled back; identity for fp16
+  // the incoming state: h0 (nullable) on the first segment, else the
+  // previous segment's final state
   const float* const st_src = p.first ? p.h0 : p.fs;
   const int64_t* const st_sd = p.first ? p.sh0 : p.sfs;
-  RangeScale rsc;
-  rsc.o = p.scale;
-  if constexpr (std::is_same<TIn, bf16_t>::value) {
-    // the largest |v| of this slice over the segment's records and of the
-    // incoming state
-    __shared__ uint32_t red[8];
-    uint32_t m = state_absmax_bits(st_src ? st_src + bi * st_sd[0] + hi * st_sd[1] + v0 * st_sd[3] : nullptr,
-                                   st_sd[2], st_sd[3], K, BV);
-    for (int i = tid; i < nloc * NSW; i += 64 * scan_waves<BV, SPLIT>()) {
-      const float* vm = reinterpret_cast<const float*>(rech + (int64_t)(i / NSW) * RS + R_VMAX);
-      m = max(m, __float_as_uint(vm[v0 / 16 + i % NSW]));
-    }
-    rsc = range_scale_of(__uint_as_float(block_max_bits(m, red)), p.scale);
-  }
+  constexpr bool BF = std::is_same<TIn, bf16_t>::value;  // range shifts (shift_cap)
 
   auto staged = [&](const f16x8 (&tile)[C][K / 8], int r, int cc) { return tile[r][swz<K>(r, cc)]; };
 
-  // Waves w and w + 4 share SIMD w % 4.  At BV = 32 (six waves) the SCAN
-  // waves take waves 2 and 3, alone on their SIMDs, and the OUT waves share
-  // theirs with PQK and LOAD.  Split SCAN (five waves): the two SCAN waves
-  // and PQK each alone on a SIMD, OUT with LOAD (of the five placements
-  // timed, the fastest: a SCAN or PQK wave beside LOAD or each other is
-  // slower).
+  // Waves w and w + 4 share SIMD w % 4.  At BV = 32 (six waves) LOAD and
+  // the second OUT wave are alone on their SIMDs; the first SCAN wave shares
+  // its SIMD with PQK, the second with the first OUT wave, each the older
+  // wave of its pair (of twelve placements timed: bf16 7-10 % faster than
+  // with the SCAN waves alone and LOAD beside an OUT wave, fp16 the same).
+  // Split SCAN (five waves): the two SCAN waves and PQK each alone on a
+  // SIMD, OUT with LOAD (of the five placements timed, the fastest: a SCAN
+  // or PQK wave beside LOAD or each other is slower).
   int role, ridx;
   if constexpr (SPLIT) {
     constexpr int roles[5] = {SR_OUT, SR_PQK, SR_SCAN, SR_SCAN, SR_LOAD};
@@ -623,8 +632,8 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
     role = roles[wave];
     ridx = idx[wave];
   } else if constexpr (NSW == 2) {
-    constexpr int roles[6] = {SR_OUT, SR_OUT, SR_SCAN, SR_SCAN, SR_PQK, SR_LOAD};
-    constexpr int idx[6] = {0, 1, 0, 1, 0, 0};
+    constexpr int roles[6] = {SR_SCAN, SR_OUT, SR_LOAD, SR_OUT, SR_PQK, SR_SCAN};
+    constexpr int idx[6] = {0, 0, 0, 1, 0, 1};
     role = roles[wave];
     ridx = idx[wave];
   } else {
@@ -661,8 +670,23 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
 #pragma unroll
           for (int rl = 0; rl < KTO; ++rl)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) st[rl][i] = s0[key_of(r0 + rl, i) * sd[2]] * rsc.v;
+            for (int i = 0; i < 4; ++i) st[rl][i] = s0[key_of(r0 + rl, i) * sd[2]];
         }
+      }
+      // bf16: the shift bound (sc) and the shift in use (sh), from the
+      // incoming state's columns
+      int sc = kNoCap, sh = 0;
+      if constexpr (BF) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int rl = 0; rl < KTO; ++rl)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) m = max(m, __float_as_uint(st[rl][i]) & 0x7fffffffu);
+        sc = wave_cap(m);
+        sh = sc == kNoCap ? 0 : sc;
+        const float f = pow2i(sh);
+#pragma unroll
+        for (int rl = 0; rl < KTO; ++rl) st[rl] = st[rl] * f;
       }
       f16x8 sB[KBO];
 #pragma unroll
@@ -681,6 +705,13 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
         f32x4 eb_lo, eb_hi, ec_lo, ec_hi;
         float ebC;
       };
+      // the cap of a chunk's v column from the operands in registers
+      auto own_cap = [&](const ScanOps& x) __attribute__((always_inline)) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = max(m, max(bf16_abs_bits(x.va[i]), bf16_abs_bits(x.vb[i])));
+        return wave_cap(m);
+      };
       const int t0 = 4 * gq + (n >> 2), t1 = t0 + 16;
       const int vc = (16 * cb + 4 * (n & 3)) * 2;
       auto read_kA = [&](const char* kbase, int rl) __attribute__((always_inline)) {
@@ -689,6 +720,17 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
         const f16x4 lo = lds_tr16(kbase + t0 * (K * 2) + swz<K>(t0, piece) * 16 + (r & 1) * 8);
         const f16x4 hi4 = lds_tr16(kbase + t1 * (K * 2) + swz<K>(t1, piece) * 16 + (r & 1) * 8);
         return cat8(lo, hi4);
+      };
+      // bf16: a chunk's shift from the cap of its v column, taken at the
+      // chunk's start (the usual cap 0 costs two compares, off the K S
+      // products' path); dsh is the change from the previous chunk's shift
+      // (< 0, or > 0 only while the state is zero)
+      int dsh = 0;
+      auto take_cap = [&](int cap) __attribute__((always_inline)) {
+        sc = min(sc, cap);
+        const int shn = sc == kNoCap ? 0 : sc;
+        dsh = shn - sh;
+        sh = shn;
       };
       auto read_ops = [&](int it, ScanOps& o) __attribute__((always_inline)) {
         const int sl = it % R;
@@ -730,6 +772,15 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
 #pragma unroll
           for (int j = 0; j < KBP; ++j) sP[j] = s.so[it & 1][cb][kbp0 + j][lane];
         }
+        // bf16: the state (and K S, Q S of the chunk-start state) change
+        // units by 2^dsh
+        float ebC = o.ebC, rat = 1.f, vmul = 1.f;
+        if constexpr (BF) {
+          take_cap(own_cap(o));
+          rat = pow2i(max(dsh, -126));
+          ebC = dsh >= -126 ? ebC * rat : ldexpf(ebC, dsh);
+          vmul = pow2i(sh);
+        }
         // K S: rows t, so its two row tiles form a B operand over t; own
         // key blocks first, the next chunk's k rows in between
         f32x4 ks[2] = {z4, z4};
@@ -738,7 +789,7 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
         // the K S products (sB already holds this chunk's S) instead of
         // delaying the state update at the end of the chain
 #pragma unroll
-        for (int rl = 0; rl < KTO; ++rl) st[rl] = st[rl] * o.ebC;
+        for (int rl = 0; rl < KTO; ++rl) st[rl] = st[rl] * ebC;
 #pragma unroll
         for (int j = 0; j < KB; ++j) {
           const int kb = NH == 2 ? (j < KBO ? kb0 + j : kbp0 + j - KBO) : j;
@@ -756,10 +807,28 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
           __builtin_amdgcn_sched_group_barrier(SG_VALU, 4, 0);
         }
         f32x4 y0, y1;
+        if constexpr (BF) {
+          // v from its bf16 bits, times 2^sh (the multiplies only where a
+          // shift is in use)
+          if (sh == 0 && dsh == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
-          y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
+            for (int i = 0; i < 4; ++i) {
+              y0[i] = bf16_bits_f32(o.va[i]) - o.eb_lo[i] * ks[0][i];
+              y1[i] = bf16_bits_f32(o.vb[i]) - o.eb_hi[i] * ks[1][i];
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              y0[i] = bf16_bits_f32(o.va[i]) * vmul - (o.eb_lo[i] * rat) * ks[0][i];
+              y1[i] = bf16_bits_f32(o.vb[i]) * vmul - (o.eb_hi[i] * rat) * ks[1][i];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            y0[i] = (float)o.va[i] - o.eb_lo[i] * ks[0][i];
+            y1[i] = (float)o.vb[i] - o.eb_hi[i] * ks[1][i];
+          }
         }
         const f16x8 yB = M::from_acc(y0, y1);
         f32x4 u[2];
@@ -812,6 +881,13 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
         } else {
           s.uo[it & 1][cb][0][lane] = u[0];
           s.uo[it & 1][cb][1][lane] = u[1];
+          if constexpr (BF) {
+            // OUT: Q S of the chunk-start state times rat, o times 2^-sh
+            if (lane == 0) {
+              s.usc[it & 1][cb][0] = rat;
+              s.usc[it & 1][cb][1] = p.scale * pow2i(-sh);
+            }
+          }
         }
 #pragma unroll
         for (int kl = 0; kl < KBO; ++kl) sB[kl] = M::from_acc(st[2 * kl], st[2 * kl + 1]);
@@ -832,10 +908,11 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
       PS_RECORD(1, nloc, 2 * KB + 2 + KTO, 0);
       PS_RECORD_BAR(1);
       float* fs = p.fs + bi * p.sfs[0] + hi * p.sfs[1] + (v0 + vcol) * p.sfs[3];
+      const float fsc = pow2i(-sh);
 #pragma unroll
       for (int rl = 0; rl < KTO; ++rl)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fs[key_of(r0 + rl, i) * p.sfs[2]] = st[rl][i] * rsc.fs;
+        for (int i = 0; i < 4; ++i) fs[key_of(r0 + rl, i) * p.sfs[2]] = st[rl][i] * fsc;
     };
     if constexpr (SPLIT) {
       if (ridx == 0)
@@ -872,6 +949,7 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
       f32x4 u0, u1;
       f16x8 pAs[2], pLs[2];
       float ebt[2];
+      float rat, osc;  // bf16: Q S's factor and o's scale (with the shift)
     };
     auto load_o = [&](int it, OutOps& o) __attribute__((always_inline)) {
       o.u0 = s.uo[it & 1][c2][0][lane];
@@ -884,6 +962,10 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
       const float* ebr = reinterpret_cast<const float*>(s.rec[it % RR] + R_EB);
       o.ebt[0] = ebr[n];
       o.ebt[1] = ebr[16 + n];
+      if constexpr (BF) {
+        o.rat = s.usc[it & 1][c2][0];
+        o.osc = s.usc[it & 1][c2][1];
+      }
     };
     auto store_chunk = [&](int it, const OutOps& o) __attribute__((always_inline)) {
       f16x8 uh, ul;
@@ -901,7 +983,10 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
         f32x4 pu = M::mma(ul, o.pAs[mt], z4);
         pu = M::mma(uh, o.pLs[mt], pu);
         pu = M::mma(uh, o.pAs[mt], pu);
-        ov[mt] = (pu + o.ebt[mt] * oq[mt]) * rsc.o;
+        if constexpr (BF)
+          ov[mt] = (pu + (o.ebt[mt] * o.rat) * oq[mt]) * o.osc;
+        else
+          ov[mt] = (pu + o.ebt[mt] * oq[mt]) * p.scale;
       }
       PS_END_B(ov[0], ov[1]);
       const int t0 = (p.c0 + it) * C;
@@ -1071,8 +1156,8 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
       const char* vb = vh + (int64_t)row0 * svb;
       const int sl = it % R;
       if constexpr (std::is_same<TIn, bf16_t>::value) {
-        // q and k from the record's fp16 copies (rows past the end already
-        // repeat the last row)
+        // k from the record's fp16 copy (rows past the end already repeat
+        // the last row)
         const char* const kb = rech + (int64_t)it * RS + R_K16;
         const char* qb = qh + (int64_t)row0 * sqb;
 #pragma unroll
@@ -1106,25 +1191,19 @@ __global__ __launch_bounds__((64 * scan_waves<BV, SPLIT>())) void scan32_kernel(
     // Chunks 0 and 1 are published at the first barrier, and chunk it + 2
     // at iteration it's: the SCAN wave reads chunk it + 1's operands during
     // iteration it.
-    // bf16 inputs: once chunk it's copies have landed, its v tile is
-    // converted to fp16 in place (times the slice's range scale), before
-    // the barrier that publishes it (q and k arrive in fp16 from the
-    // record).
+    // bf16 inputs: once chunk it's copies have landed, its q tile is
+    // converted to fp16 in place, before the barrier that publishes it (k
+    // arrives in fp16 from the record; the SCAN waves read v's bf16 bits).
     auto convert = [&](int it) __attribute__((always_inline)) {
-      if constexpr (std::is_same<TIn, bf16_t>::value) {
+      if constexpr (BF) {
         if (it >= nloc) return;
-        constexpr int NPQ = C * K / 8 / 64, NPV = C * BV / 8 / 64;
+        constexpr int NPQ = C * K / 8 / 64;
         f16x8* const q8 = &s.rq[it % R][0][0];
-        f16x8* const v8 = &s.rv[it % R][0][0];
-        f16x8 xq[NPQ], xv[NPV];
+        f16x8 xq[NPQ];
 #pragma unroll
         for (int i = 0; i < NPQ; ++i) xq[i] = q8[64 * i + lane];
 #pragma unroll
-        for (int i = 0; i < NPV; ++i) xv[i] = v8[64 * i + lane];
-#pragma unroll
         for (int i = 0; i < NPQ; ++i) q8[64 * i + lane] = to_f16x8<TIn>(__builtin_bit_cast(uint4, xq[i]));
-#pragma unroll
-        for (int i = 0; i < NPV; ++i) v8[64 * i + lane] = to_f16x8_sc<TIn>(__builtin_bit_cast(uint4, xv[i]), rsc.v);
       }
     };
     for (int it = 0; it < D; ++it)
@@ -1180,7 +1259,6 @@ int launch_t(const SArgs& a, int K, int bv, int units, hipStream_t s) {
 }  // namespace s32
 
 bool scan32_supported(int dtype, int K, int C, int BV, int V) {
-  if (dtype == GDN_DTYPE_BF16 && V / 16 > s32::kMaxVSlices) return false;
   return (dtype == GDN_DTYPE_F16 || dtype == GDN_DTYPE_BF16) && C == s32::C && (K == 64 || K == 128) &&
          (BV == 16 || BV == 32);
 }
