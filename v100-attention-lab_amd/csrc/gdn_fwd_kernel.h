@@ -73,14 +73,10 @@ __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits) {
   return __uint_as_float(bits << 16);
 }
 
-// float -> bf16 bits, round to nearest even (NaN kept quiet).
+// float -> bf16 bits, round to nearest even (NaN stays NaN): gfx950's
+// v_cvt_pk_bf16_f32, one instruction per pair where two are packed.
 __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    return (uint16_t)((u >> 16) | 0x0040u);
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float load_scalar(const void* base, int64_t off,
