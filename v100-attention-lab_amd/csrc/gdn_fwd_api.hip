@@ -7,16 +7,14 @@
 
 namespace gdn {
 
-// BV choice.  32-row chunks, fp16: 32 columns per workgroup when that
-// still gives one workgroup per CU (256 CUs), else 16.  bf16: 32 whenever V
-// allows it: each workgroup converts its q tile to fp16, and halving the
-// workgroups halves that work, which outweighs the idle CUs (measured at
-// B2 H16 and at K = V = 64, bench.py --sweep).  Phased kernel: the largest
-// slice that still gives one workgroup per CU, else the smallest supported.
+// BV choice.  32-row chunks: 32 columns per workgroup when that still
+// gives one workgroup per CU (256 CUs), else 16 (fp16 and bf16 alike,
+// bench.py --sweep).  Phased kernel: the largest slice that still gives one
+// workgroup per CU, else the smallest supported.
 int auto_block_v(int B, int H, int K, int V, int C, int dtype) {
   const long long bh = (long long)B * H;
   if (pipe_supported(dtype, K, C, 16) && V % 16 == 0) {
-    if (V % 32 == 0 && (dtype == GDN_DTYPE_BF16 || bh * (V / 32) >= 256)) return 32;
+    if (V % 32 == 0 && bh * (V / 32) >= 256) return 32;
     return 16;
   }
   int best = -1;
