@@ -128,7 +128,7 @@ typedef struct GdnFwdParams {
 /* Enqueue one chunked GDN forward on `stream` (a hipStream_t; NULL = the
  * legacy default stream).  Returns a GdnStatus / hipError_t value.
  * Replaces gdn_chunk_fwd / _gdn_fwd_kernel (gdn_triton.py:29-140).
- *   - C = 32, fp16 or bf16 q/k/v (bf16: V <= 2496), K in {64, 128}, with a
+ *   - C = 32, fp16 or bf16 q/k/v, K in {64, 128}, with a
  *     workspace, and C = 64 with
  *     K in {32, 64, 128} (any dtype; block_v is 16 there): two launches per
  *     segment of the sequence (per-chunk records of the state-independent
